@@ -1,0 +1,258 @@
+#!/usr/bin/env python3
+"""Resident MAPF-GPT rollout throughput on one MI355X (gfx950).
+
+A step is one pass of the north-star hot path over one batch, in the order
+of the reference's resident loop (minimal_p0_mapf_gpt_resident_runner.py
+:256-281): build_tokens_from_state (goal-cache refresh + BFS of changed goals
++ 256-token contexts), append_actions, update_actions, step_sim_only
+(vertex/swap/chain resolution + standard-MAPF bookkeeping).  Actions are
+uniform random {0..4} pre-staged in HBM (C2 of BASELINE.json) instead of a
+policy forward, so the timed region is the framework's own work.
+
+Workload (BASELINE.json configs[1] + configs[2], the north-star shape):
+1024 envs x 128 agents on 64x64 maps, i.i.d. obstacles p=0.2 with the
+largest component kept; inputs resident in HBM before timing.  The first
+build (every goal fresh: 131,072 BFS fields) happens in the warmup.
+
+Prints one JSON line with the metric, a `roofline` object for the token
+kernel (algorithmic bytes / event-timed duration) and a `cpu_baseline`
+object (the Python restatement of the reference's cached CPU builder +
+step resolver on this host's cores, oracle/host_builder.py).
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import multiprocessing as mp
+import os
+import platform
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+PEAK_HBM_BPS = 8.0e12
+
+# Algorithmic bytes per agent (derivation in DESIGN.md).
+B_TOKEN_KERNEL = 8 + 10 + 242 + 1024 + 1  # pos+goal, history, 11x11 u16 window, tokens, mask
+B_STEP_NORTH_STAR = 1385  # step + token build + append + update_actions per agent-step
+
+
+def cpu_baseline(args) -> dict:
+    """Python port of the reference CPU path, one stage per worker process."""
+    from iclr_2027_jointoom_amd.synthetic import make_batch, random_actions
+    from oracle.host_builder import run_stage_worker
+
+    cores = len(os.sched_getaffinity(0))
+    workers = max(1, min(cores, 16))
+    jobs = []
+    for w in range(workers):
+        grids, starts, goals = make_batch(9000 + w, args.cpu_envs, args.map, args.map, args.agents)
+        acts = random_actions(np.random.default_rng(w), args.cpu_steps, args.cpu_envs, args.agents)
+        jobs.append((grids, starts, goals, acts, args.cpu_steps))
+    ctx = mp.get_context("fork")  # before any HIP call in this process
+    t1 = run_stage_worker(jobs[0])
+    t0 = time.perf_counter()
+    with ctx.Pool(workers) as pool:
+        results = pool.map(run_stage_worker, jobs)
+    wall = time.perf_counter() - t0
+    total = sum(n for _, n in results)
+    timed = max(t for t, _ in results)
+    cpu = platform.processor() or "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                cpu = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {
+        "value": total / timed,
+        "unit": "agent-steps/s",
+        "cores": workers,
+        "kind": "port",
+        "value_1core": t1[1] / t1[0],
+        "cpu_model": cpu,
+        "sample": (
+            f"{workers} workers x {args.cpu_envs} envs x {args.agents} agents on {args.map}x{args.map} "
+            f"p=0.2, {args.cpu_steps} steady-state steps each (goal cache warm): step resolver + "
+            f"cached deque-BFS token builder; pool wall {wall:.1f}s"
+        ),
+    }
+
+
+class HipEvents:
+    """hipEvent_t pairs from the process's HIP runtime (torch's libamdhip64)."""
+
+    def __init__(self):
+        self.rt = ctypes.CDLL("libamdhip64.so.7")
+        self.rt.hipEventCreate.argtypes = [ctypes.POINTER(ctypes.c_void_p)]
+        self.rt.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p, ctypes.c_void_p]
+        self.rt.hipEventDestroy.argtypes = [ctypes.c_void_p]
+
+    def create(self) -> int:
+        ev = ctypes.c_void_p()
+        rc = self.rt.hipEventCreate(ctypes.byref(ev))
+        if rc != 0:
+            raise RuntimeError(f"hipEventCreate failed ({rc})")
+        return ev.value
+
+    def elapsed_ms(self, a: int, b: int) -> float:
+        ms = ctypes.c_float()
+        rc = self.rt.hipEventElapsedTime(ctypes.byref(ms), ctypes.c_void_p(a), ctypes.c_void_p(b))
+        if rc != 0:
+            raise RuntimeError(f"hipEventElapsedTime failed ({rc})")
+        return float(ms.value)
+
+
+def run_gpu(args) -> dict:
+    import torch
+
+    from iclr_2027_jointoom_amd import profile
+    from iclr_2027_jointoom_amd.synthetic import make_batch
+
+    E, W, A = args.envs, args.map, args.agents
+    print(f"[bench] generating {E} maps {W}x{W}, {A} agents", file=sys.stderr, flush=True)
+    grids, starts, goals = make_batch(args.seed, E, W, W, A)
+    dev = torch.device("cuda:0")
+    ext = profile(W, W)
+    g = torch.from_numpy(grids.astype(np.int32)).to(dev)
+    horizon = 1 << 30  # no env reaches its horizon inside the run: every step does full work
+    sim = ext.GridWorldSimulator(g, A, 0, E * W * W, 20260728, "standard_mapf", horizon)
+    sim.load_state(
+        torch.from_numpy(starts).to(dev),
+        torch.from_numpy(goals).to(dev),
+        torch.zeros((E, A), dtype=torch.uint8, device=dev),
+        torch.zeros(E, dtype=torch.int32, device=dev),
+    )
+    builder = ext.MapfGPTObservationBuilder(g, A)
+    builder.reset_histories()
+    total_steps = args.warmup + args.steps
+    gen = torch.Generator(device=dev).manual_seed(args.seed)
+    actions = torch.randint(0, 5, (total_steps, E, A), dtype=torch.uint8, device=dev, generator=gen)
+    hip = HipEvents()
+
+    def one_step(s):
+        builder.build_tokens_from_state(sim.cur_x, sim.cur_y, sim.goal_x, sim.goal_y)
+        a = actions[s]
+        builder.append_actions(a)
+        sim.update_actions(a)
+        sim.step_sim_only()
+
+    print("[bench] warmup (first build refreshes every goal)", file=sys.stderr, flush=True)
+    for s in range(args.warmup):
+        one_step(s)
+    torch.cuda.synchronize()
+    diag = builder.diagnostics.cpu().tolist()
+    if any(diag):
+        raise RuntimeError(f"builder diagnostics non-zero after warmup: {diag}")
+
+    tok_events = [(hip.create(), hip.create()) for _ in range(args.steps)]
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    start.record()
+    for i in range(args.steps):
+        builder._desc.token_events[0], builder._desc.token_events[1] = tok_events[i]
+        one_step(args.warmup + i)
+    end.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    builder._desc.token_events[0] = builder._desc.token_events[1] = None
+    gpu_ms = start.elapsed_time(end)
+    tok_ms = [hip.elapsed_ms(a, b) for a, b in tok_events]
+    diag = builder.diagnostics.cpu().tolist()
+    if any(diag):
+        raise RuntimeError(f"builder diagnostics non-zero: {diag}")
+
+    N = E * A
+    ms_per_step = wall * 1000.0 / args.steps
+    value = N * args.steps / wall
+    tok_avg_s = float(np.mean(tok_ms)) / 1000.0
+    tok_bytes = B_TOKEN_KERNEL * N
+    achieved = tok_bytes / tok_avg_s
+    return {
+        "value": value,
+        "ms_per_step": ms_per_step,
+        "gpu_ms_per_step": gpu_ms / args.steps,
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "tokens_kernel<64>",
+            "achieved": achieved / 1e9,
+            "peak": PEAK_HBM_BPS / 1e9,
+            "unit": "GB/s",
+            "frac": achieved / PEAK_HBM_BPS,
+            "traffic": None,
+            "bytes_per_launch": tok_bytes,
+            "avg_launch_us": tok_avg_s * 1e6,
+        },
+        "step_effective_GBps": value * B_STEP_NORTH_STAR / 1e9,
+        "step_frac_of_peak": value * B_STEP_NORTH_STAR / PEAK_HBM_BPS,
+        "device": torch.cuda.get_device_name(0),
+    }
+
+
+def main() -> int:
+    p = argparse.ArgumentParser(description=__doc__.split("\n", 1)[0])
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=200)
+    p.add_argument("--warmup", type=int, default=10)
+    p.add_argument("--envs", type=int, default=1024)
+    p.add_argument("--agents", type=int, default=128)
+    p.add_argument("--map", type=int, default=64)
+    p.add_argument("--seed", type=int, default=20260728)
+    p.add_argument("--cpu-envs", type=int, default=2)
+    p.add_argument("--cpu-steps", type=int, default=24)
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    args = p.parse_args()
+    if args.gpus != 1:
+        print(
+            "bench.py measures one GPU: this build's hot path is per-env data parallel with no "
+            "cross-GPU exchange, and multi-GPU runs are not part of it. Use --gpus 1.",
+            file=sys.stderr,
+        )
+        return 2
+    base = None
+    if not args.no_cpu_baseline:
+        print("[bench] cpu baseline", file=sys.stderr, flush=True)
+        base = cpu_baseline(args)
+    res = run_gpu(args)
+    line = {
+        "metric": "agent-steps/sec incl. obs/token build on 1 GPU; % of HBM roofline",
+        "value": res["value"],
+        "unit": "agent-steps/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": res["ms_per_step"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int16/int32 (integer)",
+        "data": "synthetic (seeded i.i.d. maps p=0.2, largest component; distinct starts/goals; uniform random actions)",
+        "config": {
+            "workload": "resident step + MAPF-GPT token build (C2+C3 shape)",
+            "envs": args.envs,
+            "agents": args.agents,
+            "map": f"{args.map}x{args.map}",
+            "task_mode": "standard_mapf",
+        },
+        "roofline": res["roofline"],
+        "cpu_baseline": base,
+        "gpu_ms_per_step": res["gpu_ms_per_step"],
+        "step_effective_GBps": res["step_effective_GBps"],
+        "step_frac_of_peak": res["step_frac_of_peak"],
+        "device": res["device"],
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

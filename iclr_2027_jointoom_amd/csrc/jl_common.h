@@ -1,0 +1,81 @@
+// jl_common.h - shared definitions of the gfx950 kernels behind include/jointloom.h.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/jointloom.h"
+
+namespace jl {
+
+constexpr int kWave = 64;            // CDNA wavefront width
+constexpr uint16_t kUnreachable = 0xFFFFu;
+constexpr int kContext = 256;        // MAPF-GPT tokens per agent
+constexpr int kRadius = 5;
+constexpr int kDiam = 11;
+constexpr int kCostTokens = 121;
+constexpr int kVisible = 13;
+constexpr int kAgentTokens = 10;
+constexpr int kCostLimit = 20;
+constexpr int kTokUnreachable = 41;
+constexpr int kTokNegClip = 42;
+constexpr int kTokPosClip = 43;
+constexpr int kTokEmptyAction = 44;
+constexpr int kTokWait = 45;
+constexpr int kTokGreedy = 50;
+constexpr int kTokPad = 66;
+constexpr int kMaxFrontier = 4096;   // reference BFS frontier capacity (diagnostics[0])
+constexpr int kPygDiam = 13;
+constexpr int kPygArea = 169;
+constexpr int kPygFeatures = 4 * kPygArea;
+constexpr int kCommRadiusSq = 49;
+
+// Scratch layout of jl_mapfgpt_t::scratch: diagnostics accumulated by a
+// build, then published by the last workgroup of the token kernel.
+constexpr int kScratchAccum = 0;     // [0..3]
+constexpr int kScratchTicket = 4;
+
+inline bool profile_ok(int w, int h) {
+    return (h == 32 || h == 64 || h == 128 || h == 256) && w >= 1 && w <= 256;
+}
+
+inline int status(hipError_t e) { return e == hipSuccess ? JL_OK : (int)e; }
+
+inline int launch_status() { return status(hipGetLastError()); }
+
+// Map-profile dispatch on the column count H (a compile-time divisor).
+#define JL_DISPATCH_H(h, ...)                                   \
+    switch (h) {                                               \
+        case 32: { constexpr int H = 32; __VA_ARGS__; break; } \
+        case 64: { constexpr int H = 64; __VA_ARGS__; break; } \
+        case 128: { constexpr int H = 128; __VA_ARGS__; break; } \
+        case 256: { constexpr int H = 256; __VA_ARGS__; break; } \
+        default: return JL_ERR_PROFILE;                        \
+    }
+
+__device__ __forceinline__ bool bit_at(const uint32_t* bits, int cell) {
+    return (bits[cell >> 5] >> (cell & 31)) & 1u;
+}
+
+// 64-bit cross-lane read (ds_bpermute); lanes outside [0,64) wrap.
+__device__ __forceinline__ uint64_t shfl64(uint64_t v, int src_lane) {
+    const int lo = __shfl((int)(uint32_t)v, src_lane, kWave);
+    const int hi = __shfl((int)(uint32_t)(v >> 32), src_lane, kWave);
+    return ((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo;
+}
+
+__device__ __forceinline__ int coord_token(int v) {
+    v = v < -kCostLimit ? -kCostLimit : v;
+    v = v > kCostLimit ? kCostLimit : v;
+    return v + kCostLimit;
+}
+
+__device__ __forceinline__ int cost_token(uint32_t v, uint32_t center) {
+    if (v == kUnreachable) return kTokUnreachable;
+    const int d = (int)v - (int)center;
+    if (d > kCostLimit) return kTokPosClip;
+    if (d < -kCostLimit) return kTokNegClip;
+    return d + kCostLimit;
+}
+
+}  // namespace jl

@@ -1,0 +1,256 @@
+/*
+ * jointloom.h - C ABI of the MI355X (gfx950) hot path of JointLoom:
+ * batched MAPF grid step, per-goal BFS fields, MAPF-GPT token builder,
+ * MAGAT field-of-view + neighbour-graph builder.
+ *
+ * Plain C: device pointers, sizes and a HIP stream handle.  No torch types.
+ * Every entry point enqueues its work on `stream` (a hipStream_t; NULL is the
+ * legacy default stream) and returns 0 on success, a negative JL_ERR_* code
+ * for an argument error detected on the host, or a positive hipError_t.
+ * `jl_error_string` turns either into text.  No entry point synchronises the
+ * stream or allocates device memory.
+ *
+ * Data layout (same bytes as the reference, /root/reference/src/cuda_backend):
+ *   grid cell (x, y)   : flat index x*map_h + y, x = row in [0,map_w),
+ *                        y = column in [0,map_h)          (grid_world_simulator.cpp:184-187)
+ *   grid bitmap        : uint32 words, word = cell>>5, bit = cell&31,
+ *                        map_w*map_h/32 words per env       (grid_world_cuda.h:17-23)
+ *   agent state row    : 8 x uint16 {env, agent, pos_x, pos_y, target_x,
+ *                        target_y, action, reset_flag}       (grid_world_cuda.h:129-138)
+ *   MAPF-GPT raw row   : 13 x uint16 = state columns 0..7 + 5 history
+ *                        actions (5 = empty)                 (mapf_gpt_schema.py:10-13,119-126)
+ *   actions            : 0 wait, 1 (-1,0), 2 (+1,0), 3 (0,-1), 4 (0,+1)
+ *                                                            (128_agents_map_step.cu:36-37)
+ * Supported map profiles: map_h in {32, 64, 128, 256}, 1 <= map_w <= 256.
+ */
+#ifndef JOINTLOOM_H
+#define JOINTLOOM_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void* jl_stream_t; /* hipStream_t */
+
+enum {
+    JL_OK = 0,
+    JL_ERR_ARG = -1,         /* null pointer, non-positive size, size overflow */
+    JL_ERR_PROFILE = -2,     /* map_h not in {32,64,128,256} or map_w > 256 */
+    JL_ERR_CAPACITY = -3     /* an edge buffer too small for the worst case */
+};
+
+enum { JL_TASK_LIFELONG = 0, JL_TASK_STANDARD_MAPF = 1 };
+
+/* Conflict outcome per agent and step (transition_adapters.py:361-455). */
+enum {
+    JL_OUTCOME_NONE = 0,
+    JL_OUTCOME_WALL = 1,
+    JL_OUTCOME_VERTEX = 2,
+    JL_OUTCOME_SWAP = 3,
+    JL_OUTCOME_CHAIN = 4
+};
+
+/* ------------------------------------------------------------------------ */
+/* Simulator state (GridWorldContext, grid_world_cuda.h:47-97).  Every       */
+/* pointer is device memory owned by the caller; [E,A] arrays are env-major. */
+/* ------------------------------------------------------------------------ */
+typedef struct jl_sim {
+    int32_t n_envs;
+    int32_t n_agents;
+    int32_t map_w;
+    int32_t map_h;
+    int32_t task_mode;          /* JL_TASK_* */
+    int32_t max_episode_steps;  /* horizon of standard_mapf */
+    const uint32_t* grid_bits;  /* [E, W*H/32] static obstacles */
+    uint32_t* grid_ocp;         /* [E, W*H/32] agent occupancy after the step */
+    uint16_t* cur_x;            /* [E, A] */
+    uint16_t* cur_y;            /* [E, A] */
+    uint16_t* goal_x;           /* [E, A] */
+    uint16_t* goal_y;           /* [E, A] */
+    uint8_t* actions;           /* [E, A] action per agent; > 4 means wait */
+    uint8_t* arrived;           /* [E, A] standard_mapf arrival latch */
+    uint8_t* goal_changed;      /* [E, A] */
+    float* rewards;             /* [E, A] 1.0 on goal after the step */
+    uint8_t* terminated;        /* [E] */
+    uint8_t* truncated;         /* [E] */
+    int32_t* step_counts;       /* [E] */
+    uint16_t* state_packed;     /* [E*A, 8] agent state rows */
+    uint8_t* outcomes;          /* [E, A] JL_OUTCOME_* of the last step, or NULL */
+    /* lifelong goal sampling (task_mode == JL_TASK_LIFELONG) */
+    const uint32_t* free_cells; /* packed (x<<16|y), env-major, row-major per env */
+    const int32_t* env_offsets; /* [E] first free cell of each env in free_cells */
+    const int32_t* env_counts;  /* [E] number of free cells of each env */
+    uint64_t* rng_state;        /* [E*A] per-agent generator state */
+} jl_sim_t;
+
+/* Pack int32 [E, W, H] grids (nonzero = obstacle) into bitmaps.
+ * Replaces launch_encode_full_map_kernel_on_stream, grid_world_cuda.cu:112-183. */
+int jl_encode_map(const int32_t* grids, uint32_t* grid_bits, int32_t n_envs,
+                  int32_t map_w, int32_t map_h, jl_stream_t stream);
+
+/* One batched environment step with vertex / swap / chain conflict
+ * resolution and standard-MAPF bookkeeping (or lifelong goal resampling).
+ * Replaces launch_step_kernel, 128_agents_map_step.cu:25-377, called from
+ * GridWorldSimulator::step_sim_only, grid_world_simulator.cpp:694-705. */
+int jl_step(const jl_sim_t* sim, jl_stream_t stream);
+
+/* Write loaded positions/goals (int16 [E, A, 2] each), arrival latches
+ * (uint8 [E, A]) and step counts (int32 [E]) into the simulator: split
+ * state, terminated/truncated, zero rewards and actions, occupancy, packed
+ * rows (reset_flag = 1), goals marked changed.  Inputs are trusted (the
+ * caller validates them).  Replaces the device part of
+ * GridWorldSimulator::load_state, grid_world_simulator.cpp:573-589, and
+ * launch_load_state_kernel, 128_agents_map_step.cu:379-426. */
+int jl_load_state(const jl_sim_t* sim, const int16_t* positions,
+                  const int16_t* goals, const uint8_t* arrived,
+                  const int32_t* step_counts, jl_stream_t stream);
+
+/* Lifelong initialisation: free-cell lists and distinct random starts/goals.
+ * `real_extents` is int32 [E, 2]; `free_cells` must hold E*W*H entries;
+ * `env_offsets`/`env_counts` are written.  Replaces
+ * cache_map_free_cells_kernel + init_agents_kernel, grid_world_cuda.cu:225-320,
+ * 405-450, driven by run_initialization, grid_world_simulator.cpp:646-676. */
+int jl_lifelong_init(const jl_sim_t* sim, const int32_t* real_extents,
+                     uint32_t* free_cells, int32_t* env_offsets,
+                     int32_t* env_counts, jl_stream_t stream);
+
+/* Seed the per-agent generators (setup_rng_kernel, grid_world_cuda.cu:464-479). */
+int jl_seed_rng(uint64_t* rng_state, int64_t count, uint64_t seed,
+                jl_stream_t stream);
+
+/* ------------------------------------------------------------------------ */
+/* MAPF-GPT observation builder (MapfGPTCUDAContext, mapf_gpt_builder.h:8-21) */
+/* ------------------------------------------------------------------------ */
+typedef struct jl_mapfgpt {
+    int32_t n_envs;
+    int32_t n_agents;
+    int32_t map_w;
+    int32_t map_h;
+    const uint32_t* grid_bits;  /* [E, W*H/32] */
+    uint16_t* state_packed;     /* [N, 8] */
+    uint16_t* histories;        /* [N, 5] */
+    int64_t* labels;            /* [N] */
+    uint16_t* cost_to_go;       /* [E, A, W, H] exact BFS distance, 0xFFFF unreachable */
+    int32_t* agent_at_cell;     /* [E, W, H] agent id or -1 (filled on request) */
+    uint16_t* goal_cache;       /* [N, 2] goal of the last refresh (init 0xFFFF) */
+    int32_t* tokens;            /* [N, 256] */
+    uint8_t* active_mask;       /* [N] (torch.bool) */
+    int32_t* diagnostics;       /* [4] overflow, bad row/action, duplicate cell, bad goal/position */
+    int32_t* scratch;           /* [8] zero-initialised workspace owned by the builder */
+    void* token_events[2];      /* optional hipEvent_t pair recorded on the stream right
+                                   before / after the token kernel (profiling); NULL = off */
+} jl_mapfgpt_t;
+
+/* build_tokens(raw_rows int16 [N, 13]): unpack + goal-cache refresh + BFS of
+ * refreshed goals + tokens.  Replaces MapfGPTObservationBuilder::build_tokens,
+ * mapf_gpt_builder.cpp:89-114, and kernels mapf_gpt_cuda.cu:75-118, 181-325,
+ * 328-347, 350-497. */
+int jl_mapfgpt_build_rows(const jl_mapfgpt_t* b, const int16_t* raw_rows,
+                          jl_stream_t stream);
+
+/* build_tokens_from_state(cur_x, cur_y, goal_x, goal_y int16 [E, A]).
+ * Replaces MapfGPTObservationBuilder::build_tokens_from_state,
+ * mapf_gpt_builder.cpp:140-167, and mapf_gpt_state_unpack_kernel :121-152. */
+int jl_mapfgpt_build_state(const jl_mapfgpt_t* b, const int16_t* cur_x,
+                           const int16_t* cur_y, const int16_t* goal_x,
+                           const int16_t* goal_y, jl_stream_t stream);
+
+/* append_actions(uint8 [E, A]).  Replaces mapf_gpt_append_actions_kernel,
+ * mapf_gpt_cuda.cu:155-178. */
+int jl_mapfgpt_append_actions(const jl_mapfgpt_t* b, const uint8_t* actions,
+                              jl_stream_t stream);
+
+/* reset_histories(): every history slot = 5 (mapf_gpt_builder.cpp:195-197). */
+int jl_mapfgpt_reset_histories(const jl_mapfgpt_t* b, jl_stream_t stream);
+
+/* Fill agent_at_cell from state_packed (the reference rewrites it on every
+ * build, mapf_gpt_cuda.cu:328-347, 589-603; here it is filled on request). */
+int jl_mapfgpt_agent_at_cell(const jl_mapfgpt_t* b, jl_stream_t stream);
+
+/* ------------------------------------------------------------------------ */
+/* BFS distance fields                                                       */
+/* ------------------------------------------------------------------------ */
+
+/* uint8 "energy" fields for MAGAT: E = 255 - d for d <= 254, else 0, BFS
+ * from each state row's target.  Rows whose env id is out of range are
+ * skipped; with incremental_only only rows with reset_flag != 0 run.
+ * `energy` is uint8 [E, A, W, H].  Replaces launch_energy_map_kernel,
+ * energy_map.cu:80-272. */
+int jl_energy_maps(const uint32_t* grid_bits, uint8_t* energy,
+                   const uint16_t* states, int32_t length, int32_t n_envs,
+                   int32_t n_agents, int32_t map_w, int32_t map_h,
+                   int32_t incremental_only, jl_stream_t stream);
+
+/* Stateful derived state: energy fields of every agent whose goal_changed
+ * flag is set (all agents when `all_agents` != 0) from the simulator's goal
+ * arrays.  Unless `all_agents`, each changed agent's state row (reset_flag 1)
+ * is also written to changed_states[changed_prefix[g] - 1], where
+ * changed_prefix is the inclusive int64 prefix sum of the flags
+ * (pack_changed_agent_state_kernel, 128_agents_map_step.cu:469-511).
+ * Replaces GridWorldSimulator::update_derived_state,
+ * grid_world_simulator.cpp:707-753, without its host synchronisation. */
+int jl_energy_maps_flagged(const jl_sim_t* sim, uint8_t* energy,
+                           int32_t all_agents, const int64_t* changed_prefix,
+                           uint16_t* changed_states, jl_stream_t stream);
+
+/* ------------------------------------------------------------------------ */
+/* MAGAT builder (StatelessGridWorldContext, grid_world_cuda.h:99-117)        */
+/* ------------------------------------------------------------------------ */
+typedef struct jl_magat {
+    int32_t n_envs;
+    int32_t n_agents;
+    int32_t map_w;
+    int32_t map_h;
+    const uint32_t* grid_bits;  /* [E, W*H/32] static obstacles */
+    uint32_t* grid_ocp;         /* [E, W*H/32] agent occupancy */
+    const uint8_t* energy;      /* [E, A, W, H] */
+    const uint16_t* states;     /* [E*A, 8] rows the node builder reads */
+    float* pyg_x;               /* [N, 4*13*13] */
+    float* pyg_pos;             /* [N, 2] */
+    int32_t* edge_counts;       /* [N] */
+    int64_t* edge_prefix;       /* [N + 1] */
+    int64_t* num_edges;         /* [1] */
+    int64_t* edge_index;        /* [2, edge_capacity] */
+    float* edge_attr;           /* [edge_capacity, 3] */
+    int64_t edge_capacity;      /* >= E * A * (A - 1) */
+    int64_t* env_edge_base;     /* [E + 1] workspace */
+} jl_magat_t;
+
+/* Occupancy bitmap from agent state rows (rows with env id out of range are
+ * ignored).  Replaces refresh_occ_bitmap_from_packed_states_kernel,
+ * 128_agents_map_stateless_step.cu:140-173, 765-784. */
+int jl_magat_occupancy(const jl_magat_t* m, jl_stream_t stream);
+
+/* Node features pyg_x / pyg_pos and per-node edge counts.  Replaces
+ * launch_materialize_pyg_nodes_from_packed_states,
+ * 128_agents_map_stateless_step.cu:368-741. */
+int jl_magat_nodes(const jl_magat_t* m, jl_stream_t stream);
+
+/* Exclusive scan of edge counts, num_edges and COO edges ordered by source
+ * then destination id.  Replaces launch_exclusive_scan_edge_counts,
+ * grid_world_cuda.cu:17-110, and generate_pyg_edges_kernel,
+ * 128_agents_map_stateless_step.cu:854-935. */
+int jl_magat_edges(const jl_magat_t* m, jl_stream_t stream);
+
+/* ------------------------------------------------------------------------ */
+/* Misc                                                                      */
+/* ------------------------------------------------------------------------ */
+
+/* Legacy observation decode (decode_to_uint8_kernel, grid_world_cuda.cu:186-210):
+ * out[b, c, r, col] = (obs[b*2*diam + c*diam + r] >> col) & 1. */
+int jl_decode_to_uint8(const uint16_t* obs, uint8_t* out, int64_t n_batch,
+                       int32_t diameter, jl_stream_t stream);
+
+/* Text for a status code returned by any entry point. */
+const char* jl_error_string(int code);
+
+/* Library version string. */
+const char* jl_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* JOINTLOOM_H */

@@ -1,0 +1,323 @@
+"""GPU parity of the MAPF-GPT builder (jl_mapfgpt_*) against the C oracle.
+
+Ports /root/reference/tests/expert/test_mapf_gpt_cuda.py to the gfx950 path
+and adds oracle parity on maze maps (C3 shape).  Bit-exact: tokens, labels,
+active mask, cost-to-go fields, histories, diagnostics.
+"""
+import numpy as np
+import pytest
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+
+def ext128():
+    from iclr_2027_jointoom_amd import profile
+
+    return profile(128, 128)
+
+
+def _grids(ext, num_envs=2, *, device="cuda", dtype=torch.int32):
+    return torch.zeros((num_envs, ext.COMPILED_MAP_W, ext.COMPILED_MAP_H), dtype=dtype, device=device)
+
+
+def _valid_rows(num_envs=2, num_agents=4):
+    rows = torch.zeros((num_envs * num_agents, 13), dtype=torch.int16, device="cuda")
+    blocks = rows.view(num_envs, num_agents, 13)
+    blocks[:, :, 0] = torch.arange(num_envs, dtype=torch.int16, device="cuda")[:, None]
+    blocks[:, :, 1] = torch.arange(num_agents, dtype=torch.int16, device="cuda")[None, :]
+    blocks[:, :, 2] = 10
+    blocks[:, :, 3] = torch.arange(num_agents, dtype=torch.int16, device="cuda")[None, :] + 10
+    blocks[:, :, 4] = 20
+    blocks[:, :, 5] = torch.arange(num_agents, dtype=torch.int16, device="cuda")[None, :] + 10
+    blocks[:, :, 7] = 1
+    blocks[:, :, 8:13] = 5
+    return rows
+
+
+def test_api_shapes_and_no_pyg_attributes():
+    ext = ext128()
+    b = ext.MapfGPTObservationBuilder(_grids(ext), 4)
+    assert b.tokens.shape == (8, 256) and b.tokens.dtype == torch.int32
+    assert b.labels.shape == (8,) and b.labels.dtype == torch.int64
+    assert b.cost_to_go.shape == (2, 4, 128, 128) and b.cost_to_go.dtype == torch.int16
+    assert b.state_packed.shape == (8, 8) and b.state_packed.dtype == torch.int16
+    assert b.agent_at_cell.shape == (2, 128, 128) and b.agent_at_cell.dtype == torch.int32
+    assert b.pyg_ptr.tolist() == [0, 4, 8]
+    for name in ("pyg_edge_index_storage", "pyg_edge_attr_storage", "pyg_x"):
+        assert not hasattr(b, name)
+
+
+def test_memory_inventory_without_allocation():
+    ext = ext128()
+    b = ext.MapfGPTObservationBuilder(_grids(ext), 4)
+    torch.cuda.synchronize()
+    before = torch.cuda.memory_allocated()
+    inv = b.memory_tensors
+    torch.cuda.synchronize()
+    assert torch.cuda.memory_allocated() == before
+    assert inv["goal_cache"].shape == (8, 2) and inv["tokens"] is b.tokens
+
+
+def test_active_mask():
+    ext = ext128()
+    b = ext.MapfGPTObservationBuilder(_grids(ext, 1), 4)
+    rows = _valid_rows(1, 4)
+    rows[0, 4:6] = rows[0, 2:4]
+    rows[2, 4:6] = rows[2, 2:4]
+    b.build_tokens(rows)
+    assert b.active_mask.dtype == torch.bool and b.active_mask.cpu().tolist() == [False, True, False, True]
+
+
+def test_work_is_owned_by_current_stream():
+    ext = ext128()
+    A = 512
+    b = ext.MapfGPTObservationBuilder(_grids(ext, 1), A)
+    src = _valid_rows(1, A)
+    ids = torch.arange(A, dtype=torch.int16, device="cuda")
+    src[:, 2] = ids // 64 + 20
+    src[:, 3] = ids % 64 + 20
+    src[:, 4] = 100
+    src[:, 5] = src[:, 3]
+    src[:, 6] = ids % 5
+    delayed = torch.zeros_like(src)
+    stream = torch.cuda.Stream()
+    done = torch.cuda.Event()
+    default_done = torch.cuda.Event()
+    torch.cuda.synchronize()
+    with torch.cuda.stream(stream):
+        torch.cuda._sleep(50_000_000)
+        delayed.copy_(src)
+        b.build_tokens(delayed)
+        done.record()
+    default_done.record(torch.cuda.default_stream())
+    done.synchronize()
+    assert default_done.query(), "builder work escaped to the default stream"
+    assert b.labels.cpu().tolist() == (ids % 5).cpu().tolist()
+    assert b.diagnostics.cpu().tolist() == [0, 0, 0, 0]
+
+
+@pytest.mark.parametrize("grids, message", [
+    (lambda e: _grids(e, device="cpu"), "CUDA"),
+    (lambda e: _grids(e, dtype=torch.float32), "int32"),
+    (lambda e: torch.zeros((1, 8, 8), dtype=torch.int32, device="cuda"), "shape"),
+])
+def test_rejects_invalid_grids(grids, message):
+    ext = ext128()
+    with pytest.raises(RuntimeError, match=message):
+        ext.MapfGPTObservationBuilder(grids(ext), 4)
+
+
+def test_rejects_invalid_layouts():
+    ext = ext128()
+    b = ext.MapfGPTObservationBuilder(_grids(ext), 4)
+    rows = _valid_rows()
+    with pytest.raises(RuntimeError, match="int16"):
+        b.build_tokens(rows.to(torch.int32))
+    with pytest.raises(RuntimeError, match="13"):
+        b.build_tokens(rows[:, :8].contiguous())
+    with pytest.raises(RuntimeError, match="row count"):
+        b.build_tokens(rows[:-1].contiguous())
+    backing = torch.empty((8, 26), dtype=torch.int16, device="cuda")
+    nc = backing[:, ::2]
+    nc.copy_(rows)
+    with pytest.raises(RuntimeError, match="contiguous"):
+        b.build_tokens(nc)
+    b2 = ext.MapfGPTObservationBuilder(_grids(ext, 1), 2)
+    valid = torch.tensor([[10, 11]], dtype=torch.int16, device="cuda")
+    with pytest.raises(RuntimeError, match="int16"):
+        b2.build_tokens_from_state(valid.to(torch.int32), valid, valid, valid)
+    with pytest.raises(RuntimeError, match="shape"):
+        b2.build_tokens_from_state(valid[:, :1].contiguous(), valid, valid, valid)
+    with pytest.raises(RuntimeError, match="uint8"):
+        b2.append_actions(valid)
+    with pytest.raises(RuntimeError, match="shape"):
+        b2.append_actions(torch.zeros((1, 1), dtype=torch.uint8, device="cuda"))
+
+
+def test_invalid_position_is_diagnosed():
+    ext = ext128()
+    b = ext.MapfGPTObservationBuilder(_grids(ext, 1), 1)
+    rows = _valid_rows(1, 1)
+    rows[0, 2] = 128
+    b.build_tokens(rows)
+    assert b.diagnostics.cpu().tolist()[3] > 0
+    assert bool((b.tokens == 66).all())
+
+
+def _unsigned(b):
+    return b.cost_to_go.to(torch.int32).bitwise_and(0xFFFF)
+
+
+def test_cost_to_go_exact_uint16_beyond_254():
+    ext = ext128()
+    grid = torch.ones((1, 128, 128), dtype=torch.int32, device="cuda")
+    grid[0, 0, :] = 0
+    grid[0, 1, -1] = 0
+    grid[0, 2, :] = 0
+    b = ext.MapfGPTObservationBuilder(grid, 1)
+    rows = _valid_rows(1, 1)
+    rows[0, 2:6] = torch.tensor([2, 0, 0, 0], dtype=torch.int16, device="cuda")
+    rows[0, 7] = 0
+    b.build_tokens(rows)
+    cost = _unsigned(b)[0, 0]
+    assert cost[0, 0].item() == 0 and cost[0, 1].item() == 1
+    assert cost[2, 0].item() == 256 and cost[3, 0].item() == 65535
+    assert b.diagnostics[0].item() == 0
+
+
+def test_goal_change_refresh_and_replay():
+    ext = ext128()
+    b = ext.MapfGPTObservationBuilder(_grids(ext, 1), 1)
+    ra = _valid_rows(1, 1)
+    ra[0, 2:6] = torch.tensor([10, 10, 10, 20], dtype=torch.int16, device="cuda")
+    ra[0, 7] = 0
+    rb = ra.clone()
+    rb[0, 4:6] = torch.tensor([30, 30], dtype=torch.int16, device="cuda")
+    b.build_tokens(ra)
+    ca = _unsigned(b).clone()
+    b.build_tokens(rb)
+    cb = _unsigned(b).clone()
+    b.build_tokens(ra)
+    assert ca[0, 0, 10, 20].item() == 0 and cb[0, 0, 30, 30].item() == 0
+    assert not torch.equal(ca, cb) and torch.equal(ca, _unsigned(b))
+
+
+def _parity_fixture(num_agents=16):
+    grid = np.zeros((128, 128), dtype=np.int32)
+    grid[7:25, 17] = 1
+    grid[15, 17] = 0
+    positions = [(15, 15)]
+    for dx in range(-2, 3):
+        for dy in range(-2, 3):
+            if len(positions) >= num_agents:
+                break
+            pos = (15 + dx, 15 + dy)
+            if pos != positions[0] and grid[pos] == 0:
+                positions.append(pos)
+    rows = np.zeros((num_agents, 13), dtype=np.uint16)
+    rows[:, 1] = np.arange(num_agents)
+    rows[:, 2:4] = positions[:num_agents]
+    rows[:, 4] = 25
+    rows[:, 5] = np.arange(num_agents) % 10 + 20
+    rows[:, 6] = np.arange(num_agents) % 5
+    rows[:, 7] = 1
+    for a in range(num_agents):
+        rows[a, 8:13] = [5 if s < 2 else (a + s) % 5 for s in range(5)]
+    return grid[None], rows
+
+
+def test_parity_fixture_matches_oracle(oracle):
+    grids, rows = _parity_fixture()
+    ob = oracle.OracleMapfGPT(grids, 16)
+    ob.build_rows(rows)
+    ext = ext128()
+    b = ext.MapfGPTObservationBuilder(torch.from_numpy(grids).cuda(), 16)
+    b.build_tokens(torch.from_numpy(rows.astype(np.int16)).cuda())
+    assert np.array_equal(b.tokens.cpu().numpy(), ob.tokens)
+    assert np.array_equal(b.labels.cpu().numpy(), ob.labels)
+    assert np.array_equal(b.cost_to_go.cpu().numpy(), ob.cost_to_go.view(np.int16))
+    assert b.diagnostics.cpu().tolist() == [0, 0, 0, 0]
+    # agent_at_cell on request equals the oracle's scatter
+    assert np.array_equal(b.agent_at_cell.cpu().numpy(), ob.agent_at_cell)
+
+
+def test_replay_determinism_and_resident_equals_raw():
+    grids, rows_a = _parity_fixture()
+    rows_b = rows_a.copy()
+    rows_b[:, 4] = 30
+    ext = ext128()
+    g = torch.from_numpy(grids).cuda()
+    b = ext.MapfGPTObservationBuilder(g, 16)
+    ra = torch.from_numpy(rows_a.astype(np.int16)).cuda()
+    rb = torch.from_numpy(rows_b.astype(np.int16)).cuda()
+    b.build_tokens(ra)
+    ta = b.tokens.clone()
+    b.build_tokens(rb)
+    b.build_tokens(ra)
+    assert torch.equal(ta, b.tokens)
+    grids8, rows8 = _parity_fixture(8)
+    g8 = torch.from_numpy(grids8).cuda()
+    r8 = torch.from_numpy(rows8.astype(np.int16)).cuda()
+    raw = ext.MapfGPTObservationBuilder(g8, 8)
+    res = ext.MapfGPTObservationBuilder(g8, 8)
+    res.histories.copy_(r8[:, 8:13])
+    raw.build_tokens(r8)
+    blk = r8.view(1, 8, 13)
+    res.build_tokens_from_state(blk[:, :, 2].contiguous(), blk[:, :, 3].contiguous(),
+                                blk[:, :, 4].contiguous(), blk[:, :, 5].contiguous())
+    assert torch.equal(res.tokens, raw.tokens) and torch.equal(res.active_mask, raw.active_mask)
+    assert res.diagnostics.cpu().tolist() == [0, 0, 0, 0]
+
+
+def test_history_roll_kat():
+    ext = ext128()
+    b = ext.MapfGPTObservationBuilder(_grids(ext, 1), 3)
+    cx = torch.tensor([[10, 11, 12]], dtype=torch.int16, device="cuda")
+    gx = torch.tensor([[20, 11, 22]], dtype=torch.int16, device="cuda")
+    b.reset_histories()
+    b.build_tokens_from_state(cx, cx, gx, gx)
+    assert b.histories.cpu().tolist() == [[5] * 5] * 3
+    assert b.active_mask.cpu().tolist() == [True, False, True]
+    b.append_actions(torch.tensor([[1, 4, 3]], dtype=torch.uint8, device="cuda"))
+    assert b.histories.cpu().tolist() == [[5, 5, 5, 5, 1], [5, 5, 5, 5, 0], [5, 5, 5, 5, 3]]
+    b.build_tokens_from_state(cx, cx, gx, gx)
+    rows = torch.zeros((3, 13), dtype=torch.int16, device="cuda")
+    rows[:, 1] = torch.arange(3, dtype=torch.int16, device="cuda")
+    rows[:, 2] = cx[0]
+    rows[:, 3] = cx[0]
+    rows[:, 4] = gx[0]
+    rows[:, 5] = gx[0]
+    rows[:, 8:13] = b.histories
+    ref = ext.MapfGPTObservationBuilder(_grids(ext, 1), 3)
+    ref.build_tokens(rows)
+    assert torch.equal(b.tokens, ref.tokens)
+    # out-of-range action: counted in diagnostics[1], recorded as 0
+    b.append_actions(torch.tensor([[7, 0, 0]], dtype=torch.uint8, device="cuda"))
+    assert b.diagnostics.cpu().tolist()[1] == 1 and b.histories[0, 4].item() == 0
+
+
+@pytest.mark.parametrize("num_agents", [256, 512])
+def test_scales_beyond_visible_cap(num_agents):
+    ext = ext128()
+    rows = _valid_rows(1, num_agents)
+    ids = torch.arange(num_agents, dtype=torch.int16, device="cuda")
+    rows[:, 2] = ids // 64 + 20
+    rows[:, 3] = ids % 64 + 20
+    rows[:, 4] = 100
+    rows[:, 5] = ids % 64 + 20
+    b = ext.MapfGPTObservationBuilder(_grids(ext, 1), num_agents)
+    b.build_tokens(rows)
+    assert b.tokens.shape == (num_agents, 256)
+    assert bool(((b.tokens >= 0) & (b.tokens <= 66)).all()) and b.diagnostics[0].item() == 0
+
+
+@pytest.mark.parametrize("kind,E,W,A", [("maze", 64, 64, 128), ("iid", 32, 32, 64), ("iid", 4, 128, 512)])
+def test_maze_batches_match_oracle(oracle, kind, E, W, A):
+    """C3 shape on fewer envs: BFS fields + tokens of fresh goals, then a
+    steady-state rebuild with moved agents and appended histories."""
+    from iclr_2027_jointoom_amd import profile
+    from iclr_2027_jointoom_amd.synthetic import make_batch
+
+    grids, starts, goals = make_batch(7 + W, E, W, W, A, kind=kind)
+    ext = profile(W, W)
+    g = torch.from_numpy(grids.astype(np.int32)).cuda()
+    b = ext.MapfGPTObservationBuilder(g, A)
+    ob = oracle.OracleMapfGPT(grids, A)
+    cx, cy = starts[..., 0].copy(), starts[..., 1].copy()
+    gx, gy = goals[..., 0].copy(), goals[..., 1].copy()
+    rng = np.random.default_rng(0)
+    for it in range(3):
+        b.build_tokens_from_state(*(torch.from_numpy(v).cuda() for v in (cx, cy, gx, gy)))
+        ob.build_state(cx, cy, gx, gy)
+        torch.cuda.synchronize()
+        assert np.array_equal(b.cost_to_go.cpu().numpy(), ob.cost_to_go.view(np.int16)), it
+        assert np.array_equal(b.tokens.cpu().numpy(), ob.tokens), it
+        assert np.array_equal(b.state_packed.cpu().numpy(), ob.state_packed.view(np.int16)), it
+        assert b.diagnostics.cpu().tolist() == ob.diagnostics.tolist() == [0, 0, 0, 0]
+        acts = rng.integers(0, 5, size=(E, A), dtype=np.uint8)
+        b.append_actions(torch.from_numpy(acts).cuda())
+        ob.append(acts)
+        # swap a few goals between agents of env 0 to force partial refreshes
+        gx[0, :4], gy[0, :4] = gx[0, :4][::-1].copy(), gy[0, :4][::-1].copy()
+        cx, cy = np.roll(cx, 1, axis=1), np.roll(cy, 1, axis=1)
