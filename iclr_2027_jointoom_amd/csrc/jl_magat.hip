@@ -52,6 +52,8 @@ __global__ __launch_bounds__(256) void occupancy_kernel(jl_magat_t m) {
     for (int i = threadIdx.x; i < A; i += blockDim.x) {
         const uint4 r = *reinterpret_cast<const uint4*>(rows + (size_t)i * 8);
         if ((r.x & 0xFFFFu) >= (uint32_t)E) continue;
+        // positions off the map set no bit (the reference would write out of bounds)
+        if ((r.y & 0xFFFFu) >= (uint32_t)m.map_w || (r.y >> 16) >= (uint32_t)m.map_h) continue;
         const uint32_t cell = (r.y & 0xFFFFu) * (uint32_t)m.map_h + (r.y >> 16);
         atomicOr(&s_occ[cell >> 5], 1u << (cell & 31));
     }
