@@ -69,7 +69,8 @@ class MapfGPTDesc(ctypes.Structure):
         ("tokens", c_void_p),
         ("active_mask", c_void_p),
         ("diagnostics", c_void_p),
-        ("scratch", c_void_p),
+        ("agent_info", c_void_p),
+        ("cost_tiles", c_void_p),
         ("token_events", c_void_p * 2),
     ]
 

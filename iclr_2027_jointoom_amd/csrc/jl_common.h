@@ -57,6 +57,16 @@ __device__ __forceinline__ bool bit_at(const uint32_t* bits, int cell) {
     return (bits[cell >> 5] >> (cell & 31)) & 1u;
 }
 
+// Orders one wavefront's LDS accesses around this point: the compiler keeps
+// LDS reads and writes on their side of it, and since a wavefront's LDS
+// operations execute in issue order, writes made before it by any lane of
+// the wavefront are seen by reads after it.
+__device__ __forceinline__ void wave_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 // 64-bit cross-lane read (ds_bpermute); lanes outside [0,64) wrap.
 __device__ __forceinline__ uint64_t shfl64(uint64_t v, int src_lane) {
     const int lo = __shfl((int)(uint32_t)v, src_lane, kWave);

@@ -1,28 +1,39 @@
 // jl_mapfgpt.hip - MAPF-GPT observation builder for gfx950.
 //
 // A build is two launches:
-//   1. unpack_bfs: one wavefront per 64 agents unpacks the state (raw rows or
-//      resident split arrays), refreshes the goal cache, and runs the
-//      bit-parallel BFS (jl_bfs.h) for each agent whose reset flag is set,
-//      staging the field in LDS and storing it with coalesced 16-byte writes.
-//   2. tokens: one workgroup per env.  Agent positions, goals, histories and
-//      greedy masks of the env live in LDS together with an occupancy bitmap
-//      and a cell->agent hash, so the visible-agent search never touches HBM;
-//      the 11x11 cost windows of a chunk of egos are gathered into LDS with
-//      many independent loads in flight; each ego's 1 KB token row is then
-//      written by one wavefront as 64 x 16-byte stores.
+//   1. unpack_bfs: one lane per agent, 1-4 wavefronts per workgroup.  Unpacks
+//      the state (raw rows or resident split arrays), refreshes the goal
+//      cache, runs the bit-parallel BFS (jl_bfs.h) for each agent whose reset
+//      flag is set in the wavefront's own LDS region, stores the field both
+//      row-major (cost_to_go, the API tensor) and in 8x8 tiles (cost_tiles),
+//      and writes every agent's info word: greedy-move mask + diagnostic
+//      flags.  It also clears `diagnostics` for the build.
+//   2. tokens: one 512-thread workgroup per env.  Phase 1 stages the env's
+//      agents (position, goal, history, greedy mask) and a cell -> agent map
+//      in LDS and sums the env's diagnostics.  Phase 2 takes the egos in
+//      chunks: all threads gather the chunk's 11x11 windows from the tiled
+//      fields into LDS (the next chunk's loads are in flight while the
+//      current chunk is turned into tokens), then one wavefront per ego ranks
+//      the visible agents with ballots and writes the 1 KB token row as
+//      64 x 16-byte stores.
 // The reference runs four kernels plus a 16 KB/env memset per build
 // (mapf_gpt_builder.cpp:108-110, mapf_gpt_cuda.cu:544-610) with the
-// top-13 search done serially by one lane per ego (:395-496).
+// top-13 search done serially by one lane per ego (:395-496) and every
+// window row read from the row-major field (one 128-byte line per row).
 #include "jl_bfs.h"
 #include "jl_common.h"
 
 namespace jl {
 namespace {
 
-constexpr int kTokThreads = 256;
 constexpr uint32_t kEmptyKey = 0xFFFFFFFFu;
 constexpr uint32_t kNoAgent = 0xFFFFFFFFu;
+
+// agent_info word, written for every agent by pass 1, read by pass 2.
+constexpr uint32_t kInfoGreedy = 0xFu;        // greedy-move mask
+constexpr uint32_t kInfoBadRow = 1u << 4;     // raw row rejected (diagnostics[1])
+constexpr uint32_t kInfoBadGoal = 1u << 5;    // refresh with goal off map / on obstacle ([3])
+constexpr int kInfoOverflowShift = 8;         // BFS frontier overflow count ([0]), 24 bits
 
 __device__ __forceinline__ uint32_t hash_cell(uint32_t cell, uint32_t mask) {
     return (cell * 2654435761u >> 7) & mask;
@@ -59,28 +70,59 @@ __device__ __forceinline__ void store_state_row(uint16_t* dst, uint32_t env, uin
     *reinterpret_cast<uint4*>(dst) = v;
 }
 
+// Greedy-move mask of one agent (mapf_gpt_cuda.cu:459-480): bit (3 - dir)
+// is set when the neighbour in direction dir, order (-1,0), (+1,0), (0,-1),
+// (0,+1), is reachable and strictly closer to the goal than the agent's cell.
+template <int H, typename Field>
+__device__ __forceinline__ uint32_t greedy_mask(Field f, int x, int y, int W) {
+    const uint32_t c0 = f(x * H + y);
+    const uint32_t n0 = x > 0 ? f((x - 1) * H + y) : kUnreachable;
+    const uint32_t n1 = x + 1 < W ? f((x + 1) * H + y) : kUnreachable;
+    const uint32_t n2 = y > 0 ? f(x * H + y - 1) : kUnreachable;
+    const uint32_t n3 = y + 1 < H ? f(x * H + y + 1) : kUnreachable;
+    uint32_t m = 0;
+    if (n0 != kUnreachable && c0 > n0) m |= 8u;
+    if (n1 != kUnreachable && c0 > n1) m |= 4u;
+    if (n2 != kUnreachable && c0 > n2) m |= 2u;
+    if (n3 != kUnreachable && c0 > n3) m |= 1u;
+    return m;
+}
+
+// Tiled field: 8x8 tiles of uint16 (128 bytes, one cache line each), tiles
+// row-major with H/8 tiles per row, ceil(W/8) tile rows.
+__host__ __device__ inline size_t tiled_cells(int W, int H) { return (size_t)((W + 7) / 8) * 8 * H; }
+
+template <int H>
+__device__ __forceinline__ uint32_t tile_offset(int x, int y) {
+    return ((uint32_t)(x >> 3) * (uint32_t)(H / 8) + (uint32_t)(y >> 3)) * 64u +
+           (uint32_t)((x & 7) * 8 + (y & 7));
+}
+
 // ---------------------------------------------------------------------------
-// Launch 1: unpack + goal-cache refresh + BFS of refreshed goals.
+// Pass 1: unpack + goal-cache refresh + BFS of refreshed goals + agent info.
 // kRows: raw 13-column rows (mapf_gpt_unpack_kernel, mapf_gpt_cuda.cu:75-118);
 // otherwise resident split arrays (mapf_gpt_state_unpack_kernel, :121-152).
 // ---------------------------------------------------------------------------
-template <int H, int R, bool kRows>
-__global__ __launch_bounds__(kWave) void unpack_bfs_kernel(jl_mapfgpt_t b,
-                                                            const int16_t* __restrict__ raw_rows,
-                                                            const int16_t* __restrict__ cur_x,
-                                                            const int16_t* __restrict__ cur_y,
-                                                            const int16_t* __restrict__ goal_x,
-                                                            const int16_t* __restrict__ goal_y) {
-    extern __shared__ uint16_t s_dist[];
+template <int H, int R, bool kRows, int kWaves>
+__global__ __launch_bounds__(kWave* kWaves) void unpack_bfs_kernel(
+    jl_mapfgpt_t b, const int16_t* __restrict__ raw_rows, const int16_t* __restrict__ cur_x,
+    const int16_t* __restrict__ cur_y, const int16_t* __restrict__ goal_x,
+    const int16_t* __restrict__ goal_y) {
+    extern __shared__ __align__(16) uint16_t s_dist_all[];
     const int A = b.n_agents, W = b.map_w;
     const int N = b.n_envs * A;
-    const int lane = threadIdx.x;
-    const int i = blockIdx.x * kWave + lane;
-    int32_t* accum = b.scratch + kScratchAccum;
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = threadIdx.x / kWave;
+    const int i = blockIdx.x * (kWave * kWaves) + threadIdx.x;
+    const int cells = W * H;
+    uint16_t* s_dist = s_dist_all + (size_t)wave * cells;  // this wavefront's field
+    // the build's diagnostics start from zero; pass 2 and append_actions add
+    if (blockIdx.x == 0 && threadIdx.x < 4) b.diagnostics[threadIdx.x] = 0;
 
     bool reset = false;
     uint32_t env = 0, tx = 0, ty = 0;
-    bool bad_row = false;
+    uint32_t px = kUnreachable, py = kUnreachable;  // position of the row this lane now holds
+    uint32_t info = 0;
     if (i < N) {
         uint16_t* st = b.state_packed + (size_t)i * 8;
         if (kRows) {
@@ -91,9 +133,11 @@ __global__ __launch_bounds__(kWave) void unpack_bfs_kernel(jl_mapfgpt_t b,
             if (c[0] >= b.n_envs || c[1] >= A || i != (int)c[0] * A + c[1]) {
                 // rejected row: every output of this agent keeps its old value,
                 // including the reset flag the BFS pass reads (:90-92, :186-189)
-                bad_row = true;
+                info = kInfoBadRow;
                 const uint4 old = *reinterpret_cast<const uint4*>(st);
                 env = old.x & 0xFFFFu;
+                px = old.y & 0xFFFFu;
+                py = old.y >> 16;
                 tx = old.z & 0xFFFFu;
                 ty = old.z >> 16;
                 reset = (old.w >> 16) != 0;
@@ -105,6 +149,8 @@ __global__ __launch_bounds__(kWave) void unpack_bfs_kernel(jl_mapfgpt_t b,
                 if (changed) *reinterpret_cast<uint32_t*>(gc) = goal;
                 reset = c[7] != 0 || changed;
                 env = c[0];
+                px = c[2];
+                py = c[3];
                 tx = c[4];
                 ty = c[5];
                 store_state_row(st, c[0], c[1], c[2], c[3], c[4], c[5], c[6], reset ? 1u : 0u);
@@ -116,6 +162,8 @@ __global__ __launch_bounds__(kWave) void unpack_bfs_kernel(jl_mapfgpt_t b,
         } else {
             env = (uint32_t)(i / A);
             const uint32_t agent = (uint32_t)(i - (int)env * A);
+            px = (uint16_t)cur_x[i];
+            py = (uint16_t)cur_y[i];
             tx = (uint16_t)goal_x[i];
             ty = (uint16_t)goal_y[i];
             uint16_t* gc = b.goal_cache + (size_t)i * 2;
@@ -123,112 +171,142 @@ __global__ __launch_bounds__(kWave) void unpack_bfs_kernel(jl_mapfgpt_t b,
             const uint32_t goal = tx | (ty << 16);
             reset = cache != goal;
             if (reset) *reinterpret_cast<uint32_t*>(gc) = goal;
-            store_state_row(st, env, agent, (uint16_t)cur_x[i], (uint16_t)cur_y[i], tx, ty, 0u,
-                            reset ? 1u : 0u);
+            store_state_row(st, env, agent, px, py, tx, ty, 0u, reset ? 1u : 0u);
             b.labels[i] = 0;
         }
     }
-    const uint64_t bad_mask = __ballot(bad_row);
-    if (lane == 0 && bad_mask) atomicAdd(accum + 1, (int)__popcll(bad_mask));
 
-    uint64_t todo = __ballot(reset);
-    if (!todo) return;
+    // Fields this launch does not rewrite are read from HBM (written by an
+    // earlier launch); refreshed ones are read from LDS below.
+    const bool on_map = i < N && px < (uint32_t)W && py < (uint32_t)H;
+    if (on_map && !reset) {
+        const uint16_t* f = b.cost_to_go + (size_t)i * cells;
+        info |= greedy_mask<H>([f](int c) { return (uint32_t)f[c]; }, (int)px, (int)py, W);
+    }
 
     constexpr int HW = RowWords<H>::HW;
-    const int cells = W * H;
     const int words = cells / 32;
+    const size_t tcells = tiled_cells(W, H);
+    uint64_t todo = __ballot(reset);
     while (todo) {
         const int src = __ffsll((unsigned long long)todo) - 1;
         todo &= todo - 1;
         const uint32_t e = (uint32_t)__shfl((int)env, src, kWave);
         const int gx = __shfl((int)tx, src, kWave);
         const int gy = __shfl((int)ty, src, kWave);
-        const size_t agent_index = (size_t)blockIdx.x * kWave + src;
+        const int spx = __shfl((int)px, src, kWave);
+        const int spy = __shfl((int)py, src, kWave);
+        const size_t agent_index = (size_t)(i - lane) + src;
         for (int c = lane; c < cells; c += kWave) s_dist[c] = kUnreachable;
-        __syncthreads();
+        wave_sync();
         bool ok = e < (uint32_t)b.n_envs && gx < W && gy < H;
         const uint32_t* env_bits = b.grid_bits + (size_t)(ok ? e : 0) * words;
         if (ok && bit_at(env_bits, gx * H + gy)) ok = false;
+        int overflow = 0;
         if (ok) {
             uint64_t fr[R][HW];
             load_free_rows<H, R>(env_bits, W, fr);
             if (lane == 0) s_dist[gx * H + gy] = 0;
-            __syncthreads();
-            int overflow;
+            wave_sync();
             if (W * H > kMaxFrontier + 1) {
                 overflow = wave_bfs<H, R, uint16_t, true>(fr, gx, gy, 0x7FFFFFFF, s_dist);
             } else {
                 overflow = wave_bfs<H, R, uint16_t, false>(fr, gx, gy, 0x7FFFFFFF, s_dist);
             }
-            if (lane == 0 && overflow) atomicAdd(accum + 0, overflow);
-        } else if (lane == 0) {
-            atomicAdd(accum + 3, 1);  // goal off the map or on an obstacle (:224-236)
         }
-        __syncthreads();
+        wave_sync();
+        if (lane == src) {
+            // goal off the map or on an obstacle: all-unreachable field (:224-236)
+            info |= ok ? (uint32_t)(overflow < 0xFFFFFF ? overflow : 0xFFFFFF) << kInfoOverflowShift
+                       : kInfoBadGoal;
+            if (spx < W && spy < H)
+                info |= greedy_mask<H>([s_dist](int c) { return (uint32_t)s_dist[c]; }, spx, spy, W);
+        }
+        // row-major field (the API tensor) and the tiled copy, 16-byte stores
+        const uint4* lds4 = reinterpret_cast<const uint4*>(s_dist);
         uint4* out = reinterpret_cast<uint4*>(b.cost_to_go + agent_index * (size_t)cells);
-        const uint4* src_lds = reinterpret_cast<const uint4*>(s_dist);
-        for (int c = lane; c < cells / 8; c += kWave) out[c] = src_lds[c];
-        __syncthreads();
+        for (int c = lane; c < cells / 8; c += kWave) out[c] = lds4[c];
+        uint4* tout = reinterpret_cast<uint4*>(b.cost_tiles + agent_index * tcells);
+        for (int c = lane; c < (int)(tcells / 8); c += kWave) {
+            const int t = c >> 3, r = c & 7;  // tile, row inside the tile
+            const int x = (t / (H / 8)) * 8 + r, y0 = (t % (H / 8)) * 8;
+            const bool in = x < W;  // rows past the map in the last tile row: unreachable
+            uint4 v = lds4[((in ? x : 0) * H + y0) >> 3];
+            v.x = in ? v.x : 0xFFFFFFFFu;
+            v.y = in ? v.y : 0xFFFFFFFFu;
+            v.z = in ? v.z : 0xFFFFFFFFu;
+            v.w = in ? v.w : 0xFFFFFFFFu;
+            tout[c] = v;
+        }
+        wave_sync();  // the LDS field is rewritten by the next refresh
     }
+    if (i < N) b.agent_info[i] = info;
 }
 
 // ---------------------------------------------------------------------------
-// Launch 2: tokens (mapf_gpt_materialize_tokens_kernel, :350-497) plus the
+// Pass 2: tokens (mapf_gpt_materialize_tokens_kernel, :350-497) plus the
 // agent scatter and its diagnostics (:328-347).
+//
+// Phase 1 (whole workgroup, one env): positions and each agent's record
+// (position, goal, raw history values and greedy mask: the ego-independent
+// part of its 10 tokens) and a cell -> agent map live in LDS; the map is
+// dense (one int32 per cell) up to 16384 cells, an occupancy bitmap + hash
+// beyond.  Phase 2 (chunks of kChunk egos): the chunk's windows are gathered
+// into LDS by every thread; then each ego is one wavefront: lane l produces
+// tokens 4l..4l+3.  Visible agents: lanes test window cells l and l+64 in the
+// map; a candidate's rank under the key (Manhattan distance, id) is the
+// number of smaller keys, counted by walking the ballot of candidates with
+// uniform readlanes; ranks 0..12 are the reference's sorted top 13 because
+// keys are unique.  The row is stored as 64 x 16-byte writes.
 // ---------------------------------------------------------------------------
+constexpr int kTokThreads = 512;
+constexpr int kDenseCellLimit = 16384;
+constexpr int kChunk = 16;                 // egos whose windows share LDS at a time
+constexpr int kGatherPerThread = (kChunk * kCostTokens + kTokThreads - 1) / kTokThreads;
+constexpr int kSlotStride = 16;            // per-wave top-13 slot array (words)
+constexpr int kRecWords = 5;               // per-agent record: pos, goal, 3 words history+greedy
+typedef int v4i __attribute__((ext_vector_type(4)));
+
 struct TokLayout {
-    int hash_slots;  // power of two >= 2A
-    int chunk;       // egos per window pass
-    size_t occ_off, keys_off, vals_off, pos_off, goal_off, hist_off, greedy_off, win_off, sel_off,
-        nsel_off, total;
+    bool dense;
+    int hash_slots;
+    size_t map_off, occ_off, keys_off, vals_off, pos_off, rec_off, win_off, slot_off, diag_off,
+        total;
 };
 
 __host__ __device__ inline size_t align16(size_t v) { return (v + 15) & ~(size_t)15; }
 
 __host__ __device__ inline TokLayout tok_layout(int A, int W, int H) {
     TokLayout L;
+    const size_t cells = (size_t)W * H;
+    L.dense = cells <= (size_t)kDenseCellLimit;
     int s = 64;
     while (s < 2 * A) s <<= 1;
-    L.hash_slots = s;
-    L.chunk = A < 128 ? A : 128;
+    L.hash_slots = L.dense ? 0 : s;
     size_t off = 0;
+    L.map_off = off;
+    if (L.dense) off = align16(off + cells * 4);
     L.occ_off = off;
-    off = align16(off + (size_t)W * H / 8);
+    if (!L.dense) off = align16(off + cells / 8);
     L.keys_off = off;
-    off = align16(off + (size_t)s * 4);
+    off = align16(off + (size_t)L.hash_slots * 4);
     L.vals_off = off;
-    off = align16(off + (size_t)s * 4);
+    off = align16(off + (size_t)L.hash_slots * 4);
     L.pos_off = off;
     off = align16(off + (size_t)A * 4);
-    L.goal_off = off;
-    off = align16(off + (size_t)A * 4);
-    L.hist_off = off;
-    off = align16(off + (size_t)A * 10);
-    L.greedy_off = off;
-    off = align16(off + (size_t)A);
+    L.rec_off = off;
+    off = align16(off + (size_t)A * kRecWords * 4);
     L.win_off = off;
-    off = align16(off + (size_t)L.chunk * kCostTokens * 2);
-    L.sel_off = off;
-    off = align16(off + (size_t)L.chunk * kVisible * 2);
-    L.nsel_off = off;
-    off = align16(off + (size_t)L.chunk);
+    off = align16(off + (size_t)kChunk * kCostTokens * 2);
+    L.slot_off = off;
+    off = align16(off + (size_t)(kTokThreads / kWave) * kSlotStride * 4);
+    L.diag_off = off;
+    off = align16(off + 4 * 4);
     L.total = off;
     return L;
 }
 
-// 11-bit occupancy of columns y0..y0+10 of row x (bits outside the map are 0).
-template <int H>
-__device__ __forceinline__ uint32_t occ_window_row(const uint32_t* occ, int x, int y0) {
-    uint32_t bits = 0;
-#pragma unroll
-    for (int c = 0; c < kDiam; ++c) {
-        const int y = y0 + c;
-        if (y >= 0 && y < H) bits |= ((occ[(x * H + y) >> 5] >> ((x * H + y) & 31)) & 1u) << c;
-    }
-    return bits;
-}
-
-template <int H>
+template <int H, bool kDense>
 __global__ __launch_bounds__(kTokThreads) void tokens_kernel(jl_mapfgpt_t b) {
     extern __shared__ __align__(16) uint8_t smem[];
     const int A = b.n_agents, W = b.map_w;
@@ -236,207 +314,259 @@ __global__ __launch_bounds__(kTokThreads) void tokens_kernel(jl_mapfgpt_t b) {
     const int tid = threadIdx.x;
     const int lane = tid & (kWave - 1);
     const int wave = tid / kWave;
-    const int nwaves = kTokThreads / kWave;
+    constexpr int nwaves = kTokThreads / kWave;
     const TokLayout L = tok_layout(A, W, H);
+    uint32_t* s_map = reinterpret_cast<uint32_t*>(smem + L.map_off);
     uint32_t* s_occ = reinterpret_cast<uint32_t*>(smem + L.occ_off);
     uint32_t* s_keys = reinterpret_cast<uint32_t*>(smem + L.keys_off);
     uint32_t* s_vals = reinterpret_cast<uint32_t*>(smem + L.vals_off);
     uint32_t* s_pos = reinterpret_cast<uint32_t*>(smem + L.pos_off);
-    uint32_t* s_goal = reinterpret_cast<uint32_t*>(smem + L.goal_off);
-    uint16_t* s_hist = reinterpret_cast<uint16_t*>(smem + L.hist_off);
-    uint8_t* s_greedy = smem + L.greedy_off;
-    uint16_t* s_win = reinterpret_cast<uint16_t*>(smem + L.win_off);
-    uint16_t* s_sel = reinterpret_cast<uint16_t*>(smem + L.sel_off);
-    uint8_t* s_nsel = smem + L.nsel_off;
+    uint32_t* s_rec = reinterpret_cast<uint32_t*>(smem + L.rec_off);    // kRecWords per agent
+    uint16_t* s_win = reinterpret_cast<uint16_t*>(smem + L.win_off);    // [kChunk][121]
+    uint32_t* s_slot = reinterpret_cast<uint32_t*>(smem + L.slot_off);
+    int* s_diag = reinterpret_cast<int*>(smem + L.diag_off);
     const uint32_t hmask = (uint32_t)L.hash_slots - 1;
-    const int occ_words = W * H / 32;
     const size_t cells = (size_t)W * H;
 
-    for (int k = tid; k < occ_words; k += kTokThreads) s_occ[k] = 0;
-    for (int k = tid; k < L.hash_slots; k += kTokThreads) {
-        s_keys[k] = kEmptyKey;
-        s_vals[k] = kNoAgent;
+    // ---- phase 1 -----------------------------------------------------------
+    if (kDense) {
+        uint4* m4 = reinterpret_cast<uint4*>(s_map);
+        const uint4 none = make_uint4(kNoAgent, kNoAgent, kNoAgent, kNoAgent);
+        for (int k = tid; k < (int)(cells / 4); k += kTokThreads) m4[k] = none;
+    } else {
+        for (int k = tid; k < (int)(cells / 32); k += kTokThreads) s_occ[k] = 0;
+        for (int k = tid; k < L.hash_slots; k += kTokThreads) {
+            s_keys[k] = kEmptyKey;
+            s_vals[k] = kNoAgent;
+        }
     }
+    if (tid < 4) s_diag[tid] = 0;
     __syncthreads();
-
-    // Agents of this env: LDS state, greedy masks, active mask, scatter.
-    int dup = 0, oob = 0;
+    int d_over = 0, d_row = 0, d_dup = 0, d_bad = 0;
     for (int a = tid; a < A; a += kTokThreads) {
         const size_t g = (size_t)env * A + a;
         const uint4 st = *reinterpret_cast<const uint4*>(b.state_packed + g * 8);
+        const uint32_t info = b.agent_info[g];
         const uint32_t px = st.y & 0xFFFFu, py = st.y >> 16;
         const uint32_t gx = st.z & 0xFFFFu, gy = st.z >> 16;
         b.active_mask[g] = (px != gx || py != gy) ? 1 : 0;
         const bool valid = px < (uint32_t)W && py < (uint32_t)H;
         s_pos[a] = valid ? (px | (py << 16)) : kNoAgent;
-        s_goal[a] = st.z;
+        // record: position, goal, raw history values (the token is computed
+        // at use: any uint16 is legal in a raw row) and the greedy mask
         const uint16_t* h = b.histories + g * 5;
-#pragma unroll
-        for (int k = 0; k < 5; ++k) s_hist[a * 5 + k] = h[k];
-        uint32_t greedy = 0;
+        uint32_t* rec = s_rec + a * kRecWords;
+        rec[0] = st.y;
+        rec[1] = st.z;
+        rec[2] = (uint32_t)h[0] | ((uint32_t)h[1] << 16);
+        rec[3] = (uint32_t)h[2] | ((uint32_t)h[3] << 16);
+        rec[4] = (uint32_t)h[4] | ((info & kInfoGreedy) << 16);
+        d_over += (int)(info >> kInfoOverflowShift);
+        d_row += (info & kInfoBadRow) ? 1 : 0;
+        d_bad += (info & kInfoBadGoal) ? 1 : 0;
         if (valid) {
-            const uint16_t* f = b.cost_to_go + g * cells;
-            const int x = (int)px, y = (int)py;
-            const uint32_t c0 = f[x * H + y];
-            const uint32_t n0 = x > 0 ? f[(x - 1) * H + y] : kUnreachable;
-            const uint32_t n1 = x + 1 < W ? f[(x + 1) * H + y] : kUnreachable;
-            const uint32_t n2 = y > 0 ? f[x * H + y - 1] : kUnreachable;
-            const uint32_t n3 = y + 1 < H ? f[x * H + y + 1] : kUnreachable;
-            // bit (3 - dir), dir order (-1,0), (+1,0), (0,-1), (0,+1) (:465-479)
-            if (n0 != kUnreachable && c0 > n0) greedy |= 8u;
-            if (n1 != kUnreachable && c0 > n1) greedy |= 4u;
-            if (n2 != kUnreachable && c0 > n2) greedy |= 2u;
-            if (n3 != kUnreachable && c0 > n3) greedy |= 1u;
             const uint32_t cell = px * H + py;
-            atomicOr(&s_occ[cell >> 5], 1u << (cell & 31));
-            const uint32_t slot = hash_insert(s_keys, hmask, cell);
-            // lowest id keeps a shared cell; each extra agent counts once
-            const uint32_t prev = atomicMin(&s_vals[slot], (uint32_t)a);
-            if (prev != kNoAgent) ++dup;
-        } else {
-            ++oob;
-        }
-        s_greedy[a] = (uint8_t)greedy;
-    }
-    {
-        const int d = __syncthreads_count(dup);
-        const int o = __syncthreads_count(oob);
-        if (tid == 0) {
-            if (d) atomicAdd(b.scratch + kScratchAccum + 2, d);
-            if (o) atomicAdd(b.scratch + kScratchAccum + 3, o);
-        }
-    }
-    // __syncthreads_count are barriers: LDS tables are complete here.
-
-    for (int c0 = 0; c0 < A; c0 += L.chunk) {
-        const int nch = (A - c0) < L.chunk ? (A - c0) : L.chunk;
-        // Gather the cost windows of the chunk: (ego, cell) pairs spread over
-        // the workgroup so every thread keeps many independent loads in flight.
-        const int pairs = nch * kCostTokens;
-#pragma unroll 4
-        for (int p = tid; p < pairs; p += kTokThreads) {
-            const int el = p / kCostTokens;
-            const int c = p - el * kCostTokens;
-            const int e = c0 + el;
-            const uint32_t pos = s_pos[e];
-            uint16_t v = kUnreachable;
-            if (pos != kNoAgent) {
-                const int x = (int)(pos & 0xFFFFu) + c / kDiam - kRadius;
-                const int y = (int)(pos >> 16) + c % kDiam - kRadius;
-                if (x >= 0 && x < W && y >= 0 && y < H) {
-                    v = b.cost_to_go[((size_t)env * A + e) * cells + (size_t)(x * H + y)];
-                }
-            }
-            s_win[el * kCostTokens + c] = v;
-        }
-        // Visible agents of each ego: top 13 by (Manhattan distance, id),
-        // ego included (:383-431), from the LDS occupancy bitmap + hash.
-        for (int el = tid; el < nch; el += kTokThreads) {
-            const int e = c0 + el;
-            const uint32_t pos = s_pos[e];
-            int n = 0;
-            int sd[kVisible];
-            int sid[kVisible];
-            if (pos != kNoAgent) {
-                const int ex = (int)(pos & 0xFFFFu), ey = (int)(pos >> 16);
-                for (int dx = -kRadius; dx <= kRadius; ++dx) {
-                    const int x = ex + dx;
-                    if (x < 0 || x >= W) continue;
-                    uint32_t bits = occ_window_row<H>(s_occ, x, ey - kRadius);
-                    while (bits) {
-                        const int c = __ffs(bits) - 1;
-                        bits &= bits - 1;
-                        const int dy = c - kRadius;
-                        const uint32_t cell = (uint32_t)(x * H + ey + dy);
-                        const uint32_t slot = hash_find(s_keys, hmask, cell);
-                        const int id = (int)s_vals[slot];
-                        const int d = (dx < 0 ? -dx : dx) + (dy < 0 ? -dy : dy);
-                        int at = n;
-                        if (n == kVisible) {
-                            const int ld = sd[kVisible - 1], li = sid[kVisible - 1];
-                            if (!(d < ld || (d == ld && id < li))) continue;
-                            at = kVisible - 1;
-                        } else {
-                            ++n;
-                        }
-                        while (at > 0 && (d < sd[at - 1] || (d == sd[at - 1] && id < sid[at - 1]))) {
-                            sd[at] = sd[at - 1];
-                            sid[at] = sid[at - 1];
-                            --at;
-                        }
-                        sd[at] = d;
-                        sid[at] = id;
-                    }
-                }
-            }
-            for (int s = 0; s < n; ++s) s_sel[el * kVisible + s] = (uint16_t)sid[s];
-            s_nsel[el] = (uint8_t)n;
-        }
-        __syncthreads();
-
-        // One wavefront per ego row: lane l builds tokens 4l..4l+3.
-        for (int el = wave; el < nch; el += nwaves) {
-            const int e = c0 + el;
-            const uint32_t pos = s_pos[e];
-            int tok[4];
-            if (pos == kNoAgent) {
-                tok[0] = tok[1] = tok[2] = tok[3] = kTokPad;
+            uint32_t prev;
+            if (kDense) {
+                prev = atomicMin(&s_map[cell], (uint32_t)a);
             } else {
+                atomicOr(&s_occ[cell >> 5], 1u << (cell & 31));
+                const uint32_t slot = hash_insert(s_keys, hmask, cell);
+                prev = atomicMin(&s_vals[slot], (uint32_t)a);
+            }
+            // lowest id keeps a shared cell; each extra agent counts once
+            if (prev != kNoAgent) ++d_dup;
+        } else {
+            ++d_bad;  // position off the map (scatter, :336-339)
+        }
+    }
+    if (d_over) atomicAdd(&s_diag[0], d_over);
+    if (d_row) atomicAdd(&s_diag[1], d_row);
+    if (d_dup) atomicAdd(&s_diag[2], d_dup);
+    if (d_bad) atomicAdd(&s_diag[3], d_bad);
+    __syncthreads();
+    // relaxed device-scope adds: the build's totals are complete when the
+    // kernel is, and pass 1 of the build cleared them
+    if (tid < 4 && s_diag[tid]) atomicAdd(b.diagnostics + tid, s_diag[tid]);
+
+    // ---- phase 2: lane constants ---------------------------------------------
+    // Lane l produces tokens 4l..4l+3: byte j of slot_pack / field_pack is
+    // the visible-agent slot / record field of token 4l+j (slot kVisible:
+    // not an agent token).
+    uint32_t cost_mask = 0, agent_mask = 0, slot_pack = 0, field_pack = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int t = 4 * lane + j;
+        cost_mask |= t < kCostTokens ? (1u << j) : 0u;
+        const int u = t - kCostTokens;
+        const bool agent_tok = u >= 0 && u < kVisible * kAgentTokens;
+        agent_mask |= agent_tok ? (1u << j) : 0u;
+        slot_pack |= (uint32_t)(agent_tok ? u / kAgentTokens : kVisible) << (8 * j);
+        field_pack |= (uint32_t)(agent_tok ? u % kAgentTokens : 0) << (8 * j);
+    }
+    auto slot_of = [&](int j) { return (int)((slot_pack >> (8 * j)) & 0xFFu); };
+    const int slot_a = slot_of(0) < kVisible ? slot_of(0) : slot_of(3);
+    const int slot_b = slot_of(3) < kVisible ? slot_of(3) : slot_of(0);
+    const int q0 = lane, q1 = lane + kWave;
+    const int qdx0 = q0 / kDiam - kRadius, qdy0 = q0 % kDiam - kRadius;
+    const int qdx1 = q1 / kDiam - kRadius, qdy1 = q1 % kDiam - kRadius;
+    const bool qval1 = q1 < kCostTokens;
+    const uint32_t qd0 = (uint32_t)(abs(qdx0) + abs(qdy0)) << 16;
+    const uint32_t qd1 = (uint32_t)(abs(qdx1) + abs(qdy1)) << 16;
+    uint32_t* my_slots = s_slot + wave * kSlotStride;
+
+    // Agent at (x, y) of this env or kNoAgent.  The dense map is read at a
+    // clamped cell so the read needs no branch.
+    auto agent_at = [&](int x, int y) -> uint32_t {
+        const bool in = x >= 0 && x < W && y >= 0 && y < H;
+        if (kDense) {
+            const int xc = x < 0 ? 0 : (x >= W ? W - 1 : x);
+            const int yc = y < 0 ? 0 : (y >= H ? H - 1 : y);
+            const uint32_t v = s_map[xc * H + yc];
+            return in ? v : kNoAgent;
+        }
+        if (!in) return kNoAgent;
+        const uint32_t cell = (uint32_t)(x * H + y);
+        if (!((s_occ[cell >> 5] >> (cell & 31)) & 1u)) return kNoAgent;
+        return s_vals[hash_find(s_keys, hmask, cell)];
+    };
+
+    // Window gather of a chunk: item p = tid + k * kTokThreads of the chunk is
+    // window cell p % 121 of the chunk's ego p / 121, so consecutive threads
+    // read consecutive columns of a window row.  Every thread issues its loads without branches (addresses clamped into
+    // the field) and keeps the values in registers; `commit` writes them to
+    // LDS, unreachable for cells off the map, after the previous chunk's
+    // tokens have been produced.  Offsets are 32-bit bytes from the env's
+    // first tiled field (the host checks that an env's fields fit).
+    const size_t tcells = tiled_cells(W, H);
+    const uint8_t* env_tiles =
+        reinterpret_cast<const uint8_t*>(b.cost_tiles + (size_t)env * A * tcells);
+    uint16_t graw[kGatherPerThread];
+    uint32_t gok = 0;
+    auto stage = [&](int c0, int nch) {
+        gok = 0;
+#pragma unroll
+        for (int k = 0; k < kGatherPerThread; ++k) {
+            const int p = tid + k * kTokThreads;
+            const int el = p / kCostTokens, c = p - el * kCostTokens;
+            const bool live = el < nch;
+            const uint32_t pos = s_pos[c0 + (live ? el : 0)];
+            const bool ok = live && pos != kNoAgent;
+            const int x = (int)(pos & 0xFFFFu) + c / kDiam - kRadius;
+            const int y = (int)(pos >> 16) + c % kDiam - kRadius;
+            const bool in = ok && x >= 0 && x < W && y >= 0 && y < H;
+            const int xc = ok ? (x < 0 ? 0 : (x >= W ? W - 1 : x)) : 0;
+            const int yc = ok ? (y < 0 ? 0 : (y >= H ? H - 1 : y)) : 0;
+            const uint32_t off =
+                ((uint32_t)(c0 + (live ? el : 0)) * (uint32_t)tcells + tile_offset<H>(xc, yc)) * 2u;
+            graw[k] = *reinterpret_cast<const uint16_t*>(env_tiles + off);
+            gok |= in ? (1u << k) : 0u;
+        }
+    };
+    auto commit = [&](int nch) {
+        // keep every use of the gathered values here, so that the loads stay
+        // in flight across the previous chunk's token work
+#pragma unroll
+        for (int k = 0; k < kGatherPerThread; ++k) asm volatile("" : "+v"(graw[k]));
+#pragma unroll
+        for (int k = 0; k < kGatherPerThread; ++k) {
+            const int p = tid + k * kTokThreads;
+            if (p < nch * kCostTokens) s_win[p] = (gok >> k) & 1u ? graw[k] : kUnreachable;
+        }
+    };
+
+    // ---- phase 2: chunks of kChunk egos, one wavefront per ego ---------------
+    const int nchunks = (A + kChunk - 1) / kChunk;
+    stage(0, A < kChunk ? A : kChunk);
+    for (int q = 0; q < nchunks; ++q) {
+        const int c0 = q * kChunk;
+        const int nch = (A - c0) < kChunk ? (A - c0) : kChunk;
+        commit(nch);
+        __syncthreads();
+        if (q + 1 < nchunks) {
+            const int c1 = c0 + kChunk;
+            stage(c1, (A - c1) < kChunk ? (A - c1) : kChunk);
+        }
+        // lane i holds the position of this wave's i-th ego of the chunk
+        const int mine = wave < nch ? (nch - wave + nwaves - 1) / nwaves : 0;
+        const uint32_t pos_mine = lane < mine ? s_pos[c0 + wave + lane * nwaves] : kNoAgent;
+        for (int i = 0; i < mine; ++i) {
+            const int el = wave + i * nwaves;
+            const int e = c0 + el;
+            const uint32_t pos = (uint32_t)__builtin_amdgcn_readlane((int)pos_mine, i);
+            int tok[4] = {kTokPad, kTokPad, kTokPad, kTokPad};
+            if (pos != kNoAgent) {
                 const int ex = (int)(pos & 0xFFFFu), ey = (int)(pos >> 16);
                 const uint16_t* win = s_win + el * kCostTokens;
-                const uint32_t center = win[kRadius * kDiam + kRadius];
-                const int nsel = s_nsel[el];
+                // all independent LDS reads of the ego first, then one wait
+                const uint32_t center = win[kCostTokens / 2];
+                uint32_t wv[4];
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const int t = 4 * lane + j;
-                    int v = kTokPad;
-                    if (t < kCostTokens) {
-                        v = cost_token(win[t], center);
-                    } else if (t < kCostTokens + kVisible * kAgentTokens) {
-                        const int s = (t - kCostTokens) / kAgentTokens;
-                        const int f = (t - kCostTokens) - s * kAgentTokens;
-                        if (s < nsel) {
-                            const int o = s_sel[el * kVisible + s];
-                            const uint32_t op = s_pos[o];
-                            const uint32_t og = s_goal[o];
-                            switch (f) {
-                                case 0: v = coord_token((int)(op & 0xFFFFu) - ex); break;
-                                case 1: v = coord_token((int)(op >> 16) - ey); break;
-                                case 2: v = coord_token((int)(og & 0xFFFFu) - ex); break;
-                                case 3: v = coord_token((int)(og >> 16) - ey); break;
-                                case 9: v = kTokGreedy + s_greedy[o]; break;
-                                default: {
-                                    const int act = s_hist[o * 5 + (f - 4)];
-                                    v = act == 5 ? kTokEmptyAction : kTokWait + act;
-                                }
-                            }
-                        }
+                for (int j = 0; j < 4; ++j)
+                    wv[j] = win[(cost_mask >> j) & 1u ? 4 * lane + j : kCostTokens / 2];
+                const uint32_t id0 = agent_at(ex + qdx0, ey + qdy0);
+                const uint32_t id1r = agent_at(ex + qdx1, ey + qdy1);
+                const uint32_t id1 = qval1 ? id1r : kNoAgent;
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    tok[j] = (cost_mask >> j) & 1u ? cost_token(wv[j], center) : kTokPad;
+                // candidates: (distance << 16 | id), all-ones when the cell is empty
+                const uint32_t key0 = id0 == kNoAgent ? 0xFFFFFFFFu : (qd0 | id0);
+                const uint32_t key1 = id1 == kNoAgent ? 0xFFFFFFFFu : (qd1 | id1);
+                const uint64_t m0 = __ballot(id0 != kNoAgent);
+                const uint64_t m1 = __ballot(id1 != kNoAgent);
+                int r0 = 0, r1 = 0;
+                for (uint64_t m = m0; m; m &= m - 1) {
+                    const uint32_t k =
+                        (uint32_t)__builtin_amdgcn_readlane((int)key0, __ffsll((unsigned long long)m) - 1);
+                    r0 += k < key0;
+                    r1 += k < key1;
+                }
+                for (uint64_t m = m1; m; m &= m - 1) {
+                    const uint32_t k =
+                        (uint32_t)__builtin_amdgcn_readlane((int)key1, __ffsll((unsigned long long)m) - 1);
+                    r0 += k < key0;
+                    r1 += k < key1;
+                }
+                const int count = __popcll(m0) + __popcll(m1);
+                const int nsel = count < kVisible ? count : kVisible;
+                if (nsel > 0) {
+                    // the selected ids move through the wave's slot array in LDS
+                    if (id0 != kNoAgent && r0 < kVisible) my_slots[r0] = id0;
+                    if (id1 != kNoAgent && r1 < kVisible) my_slots[r1] = id1;
+                    wave_sync();
+                    uint32_t ida = my_slots[slot_a < kVisible ? slot_a : 0];
+                    uint32_t idb = my_slots[slot_b < kVisible ? slot_b : 0];
+                    // slots at or past nsel hold stale ids: keep the reads in bounds
+                    ida = ida < (uint32_t)A ? ida : 0u;
+                    idb = idb < (uint32_t)A ? idb : 0u;
+                    uint32_t rw[4];
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        // record word of field f: 0 pos, 1 goal, 2.. history pairs, greedy
+                        const int f = (int)((field_pack >> (8 * j)) & 0xFFu);
+                        const uint32_t o = slot_of(j) == slot_a ? ida : idb;
+                        rw[j] = s_rec[o * kRecWords + (f < 2 ? 0 : (f < 4 ? 1 : 2 + ((f - 4) >> 1)))];
                     }
-                    tok[j] = v;
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        const int f = (int)((field_pack >> (8 * j)) & 0xFFu);
+                        const int shift = f < 4 ? 16 * (f & 1) : 16 * ((f - 4) & 1);
+                        const int v16 = (int)((rw[j] >> shift) & 0xFFFFu);
+                        const int coord = coord_token(v16 - ((f & 1) ? ey : ex));
+                        const int hist = v16 == 5 ? kTokEmptyAction : kTokWait + v16;
+                        const int val = f < 4 ? coord : (f < 9 ? hist : kTokGreedy + v16);
+                        tok[j] = ((agent_mask >> j) & 1u) && slot_of(j) < nsel ? val : tok[j];
+                    }
+                    wave_sync();  // slot reads done before the next ego's writes
                 }
             }
-            int4 out;
-            out.x = tok[0];
-            out.y = tok[1];
-            out.z = tok[2];
-            out.w = tok[3];
-            reinterpret_cast<int4*>(b.tokens + ((size_t)env * A + e) * kContext)[lane] = out;
+            // streaming store: the row is not read again by this build
+            const v4i out = {tok[0], tok[1], tok[2], tok[3]};
+            __builtin_nontemporal_store(
+                out, reinterpret_cast<v4i*>(b.tokens + ((size_t)env * A + e) * kContext) + lane);
         }
-        __syncthreads();
-    }
-
-    // Publish the build's diagnostics once every workgroup is done.
-    if (tid == 0) {
-        __threadfence();
-        const int ticket = atomicAdd(b.scratch + kScratchTicket, 1);
-        if (ticket == (int)gridDim.x - 1) {
-            __threadfence();
-#pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                b.diagnostics[k] = atomicExch(b.scratch + kScratchAccum + k, 0);
-            }
-            atomicExch(b.scratch + kScratchTicket, 0);
-        }
+        __syncthreads();  // the chunk's windows are consumed
     }
 }
 
@@ -490,10 +620,42 @@ int check_builder(const jl_mapfgpt_t* b) {
     if (!profile_ok(b->map_w, b->map_h)) return JL_ERR_PROFILE;
     if ((int64_t)b->n_envs * b->n_agents > 0x7FFFFFFF) return JL_ERR_ARG;
     if (b->n_agents > 65535 || b->n_envs > 65535) return JL_ERR_ARG;
+    // the token pass addresses an env's tiled fields with 32-bit byte offsets
+    if ((uint64_t)b->n_agents * tiled_cells(b->map_w, b->map_h) * 2u > 0xFFFFFFFFull)
+        return JL_ERR_ARG;
     if (!b->grid_bits || !b->state_packed || !b->histories || !b->labels || !b->cost_to_go ||
-        !b->goal_cache || !b->tokens || !b->active_mask || !b->diagnostics || !b->scratch)
+        !b->goal_cache || !b->tokens || !b->active_mask || !b->diagnostics || !b->agent_info ||
+        !b->cost_tiles)
         return JL_ERR_ARG;
     return JL_OK;
+}
+
+// Pass 1 wavefronts per workgroup: each owns a W*H uint16 LDS field; up to
+// 64 KB of them per workgroup, at most 4.
+inline int pass1_waves(int W, int H) {
+    const size_t field = (size_t)W * H * 2;
+    return field <= 16384 ? 4 : (field <= 32768 ? 2 : 1);
+}
+
+template <int H, int R, bool kRows>
+int launch_pass1(const jl_mapfgpt_t* b, const int16_t* rows, const int16_t* cx, const int16_t* cy,
+                 const int16_t* gx, const int16_t* gy, hipStream_t stream) {
+    const int N = b->n_envs * b->n_agents;
+    const int waves = pass1_waves(b->map_w, H);
+    const size_t lds = (size_t)waves * b->map_w * H * sizeof(uint16_t);
+    const int per_block = kWave * waves;
+    const dim3 grid((N + per_block - 1) / per_block);
+    if (waves == 4) {
+        hipLaunchKernelGGL((unpack_bfs_kernel<H, R, kRows, 4>), grid, dim3(per_block), lds, stream,
+                           *b, rows, cx, cy, gx, gy);
+    } else if (waves == 2) {
+        hipLaunchKernelGGL((unpack_bfs_kernel<H, R, kRows, 2>), grid, dim3(per_block), lds, stream,
+                           *b, rows, cx, cy, gx, gy);
+    } else {
+        hipLaunchKernelGGL((unpack_bfs_kernel<H, R, kRows, 1>), grid, dim3(per_block), lds, stream,
+                           *b, rows, cx, cy, gx, gy);
+    }
+    return launch_status();
 }
 
 template <bool kRows>
@@ -501,31 +663,29 @@ int build(const jl_mapfgpt_t* b, const int16_t* rows, const int16_t* cx, const i
           const int16_t* gx, const int16_t* gy, hipStream_t stream) {
     int rc = check_builder(b);
     if (rc) return rc;
-    const int N = b->n_envs * b->n_agents;
     const int W = b->map_w;
-    const int grid1 = (N + kWave - 1) / kWave;
-    const size_t bfs_lds = (size_t)W * b->map_h * sizeof(uint16_t);
     const TokLayout L = tok_layout(b->n_agents, W, b->map_h);
-    if (L.total > 160 * 1024 || bfs_lds > 160 * 1024) return JL_ERR_PROFILE;
+    if (L.total > 160 * 1024) return JL_ERR_PROFILE;
     JL_DISPATCH_H(b->map_h, {
         if (W <= 64) {
-            hipLaunchKernelGGL((unpack_bfs_kernel<H, 1, kRows>), dim3(grid1), dim3(kWave), bfs_lds,
-                               stream, *b, rows, cx, cy, gx, gy);
+            rc = launch_pass1<H, 1, kRows>(b, rows, cx, cy, gx, gy, stream);
         } else if (W <= 128) {
-            hipLaunchKernelGGL((unpack_bfs_kernel<H, 2, kRows>), dim3(grid1), dim3(kWave), bfs_lds,
-                               stream, *b, rows, cx, cy, gx, gy);
+            rc = launch_pass1<H, 2, kRows>(b, rows, cx, cy, gx, gy, stream);
         } else {
-            hipLaunchKernelGGL((unpack_bfs_kernel<H, 4, kRows>), dim3(grid1), dim3(kWave), bfs_lds,
-                               stream, *b, rows, cx, cy, gx, gy);
+            rc = launch_pass1<H, 4, kRows>(b, rows, cx, cy, gx, gy, stream);
         }
-        rc = launch_status();
         if (rc) return rc;
         if (b->token_events[0]) {
             rc = status(hipEventRecord((hipEvent_t)b->token_events[0], stream));
             if (rc) return rc;
         }
-        hipLaunchKernelGGL((tokens_kernel<H>), dim3(b->n_envs), dim3(kTokThreads), L.total, stream,
-                           *b);
+        if (L.dense) {
+            hipLaunchKernelGGL((tokens_kernel<H, true>), dim3(b->n_envs), dim3(kTokThreads), L.total,
+                               stream, *b);
+        } else {
+            hipLaunchKernelGGL((tokens_kernel<H, false>), dim3(b->n_envs), dim3(kTokThreads),
+                               L.total, stream, *b);
+        }
         rc = launch_status();
         if (rc) return rc;
         if (b->token_events[1]) {

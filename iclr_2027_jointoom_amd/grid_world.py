@@ -261,8 +261,12 @@ class MapfGPTObservationBuilder(_Base):
             self.t_goal_cache = torch.full((N, 2), -1, dtype=torch.int16, device=device)
             self.t_diagnostics = torch.zeros((4,), dtype=torch.int32, device=device)
             self.t_pyg_ptr = torch.arange(E + 1, dtype=torch.int64, device=device) * n_agents
-            # build-private workspace: diagnostics accumulator + ticket
-            self._scratch = torch.zeros((8,), dtype=torch.int32, device=device)
+            # build-private workspaces: per-agent greedy mask + diagnostic flags, and
+            # the distance fields in 8x8 tiles (the token pass reads its windows there)
+            self._agent_info = torch.zeros((N,), dtype=torch.int32, device=device)
+            self._cost_tiles = torch.full(
+                (E, n_agents, (W + 7) // 8 * 8 * H), -1, dtype=torch.int16, device=device
+            )
         self._desc = MapfGPTDesc(
             n_envs=E,
             n_agents=n_agents,
@@ -278,7 +282,8 @@ class MapfGPTObservationBuilder(_Base):
             tokens=_ptr(self.t_tokens),
             active_mask=_ptr(self.t_active_mask),
             diagnostics=_ptr(self.t_diagnostics),
-            scratch=_ptr(self._scratch),
+            agent_info=_ptr(self._agent_info),
+            cost_tiles=_ptr(self._cost_tiles),
         )
         self._desc_ref = ctypes.byref(self._desc)
 

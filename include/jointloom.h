@@ -138,12 +138,19 @@ typedef struct jl_mapfgpt {
     int32_t* tokens;            /* [N, 256] */
     uint8_t* active_mask;       /* [N] (torch.bool) */
     int32_t* diagnostics;       /* [4] overflow, bad row/action, duplicate cell, bad goal/position */
-    int32_t* scratch;           /* [8] zero-initialised workspace owned by the builder */
+    uint32_t* agent_info;       /* [N] workspace: greedy-move mask and diagnostic flags of
+                                   each agent, written by the first pass of a build */
+    uint16_t* cost_tiles;       /* [E, A, ceil(W/8), H/8, 8, 8] workspace: the same fields as
+                                   cost_to_go in 8x8 tiles (one 128-byte line per tile) */
     void* token_events[2];      /* optional hipEvent_t pair recorded on the stream right
                                    before / after the token kernel (profiling); NULL = off */
 } jl_mapfgpt_t;
 
-/* build_tokens(raw_rows int16 [N, 13]): unpack + goal-cache refresh + BFS of
+/* cost_tiles holds what the builder last wrote into cost_to_go; the token
+ * pass reads the windows from it, so values written into cost_to_go by the
+ * caller are not seen by later builds (cost_to_go is an output).
+ *
+ * build_tokens(raw_rows int16 [N, 13]): unpack + goal-cache refresh + BFS of
  * refreshed goals + tokens.  Replaces MapfGPTObservationBuilder::build_tokens,
  * mapf_gpt_builder.cpp:89-114, and kernels mapf_gpt_cuda.cu:75-118, 181-325,
  * 328-347, 350-497. */

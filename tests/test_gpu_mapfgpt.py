@@ -321,3 +321,61 @@ def test_maze_batches_match_oracle(oracle, kind, E, W, A):
         # swap a few goals between agents of env 0 to force partial refreshes
         gx[0, :4], gy[0, :4] = gx[0, :4][::-1].copy(), gy[0, :4][::-1].copy()
         cx, cy = np.roll(cx, 1, axis=1), np.roll(cy, 1, axis=1)
+
+
+def _state_parity(oracle, grids, starts, goals, A, builds=2, seed=0):
+    from iclr_2027_jointoom_amd import profile
+
+    E, W, H = grids.shape
+    ext = profile(W, H)
+    b = ext.MapfGPTObservationBuilder(torch.from_numpy(grids.astype(np.int32)).cuda(), A)
+    ob = oracle.OracleMapfGPT(grids, A)
+    cx, cy = starts[..., 0].copy(), starts[..., 1].copy()
+    gx, gy = goals[..., 0].copy(), goals[..., 1].copy()
+    rng = np.random.default_rng(seed)
+    for it in range(builds):
+        b.build_tokens_from_state(*(torch.from_numpy(v).cuda() for v in (cx, cy, gx, gy)))
+        ob.build_state(cx, cy, gx, gy)
+        torch.cuda.synchronize()
+        assert np.array_equal(b.tokens.cpu().numpy(), ob.tokens), it
+        assert np.array_equal(b.active_mask.cpu().numpy().astype(np.uint8), ob.active_mask), it
+        assert b.diagnostics.cpu().tolist() == ob.diagnostics.tolist(), it
+        acts = rng.integers(0, 5, size=(E, A), dtype=np.uint8)
+        b.append_actions(torch.from_numpy(acts).cuda())
+        ob.append(acts)
+        cx, cy = np.roll(cx, 1, axis=1), np.roll(cy, 1, axis=1)
+    return b, ob
+
+
+def test_more_than_13_visible_agents_match_oracle(oracle):
+    """Half of a 32x32 map occupied: windows hold up to ~60 agents, so the
+    top-13 selection by (Manhattan, id) is exercised well past the cap."""
+    from iclr_2027_jointoom_amd.synthetic import make_batch
+
+    grids, starts, goals = make_batch(3, 2, 32, 32, 400, density=0.1)
+    b, _ = _state_parity(oracle, grids, starts, goals, 400)
+    # the visible-agent block is full for most egos
+    full = (b.tokens[:, 121 + 12 * 10].cpu().numpy() != 66).mean()
+    assert full > 0.5
+
+
+def test_hash_cell_map_on_256_maps_matches_oracle(oracle):
+    """256x256 maps use the LDS occupancy bitmap + hash instead of the dense map."""
+    from iclr_2027_jointoom_amd.synthetic import make_batch
+
+    grids, starts, goals = make_batch(11, 2, 256, 256, 192)
+    _state_parity(oracle, grids, starts, goals, 192)
+
+
+def test_raw_row_history_values_outside_action_range(oracle):
+    """The reference emits 45 + value for any uint16 history value of a raw row."""
+    grids, rows = _parity_fixture()
+    rows[:, 8] = [0, 1, 2, 3, 4, 5, 6, 100, 210, 211, 255, 256, 4095, 40000, 65534, 65535][: len(rows)]
+    ob = oracle.OracleMapfGPT(grids, 16)
+    ob.build_rows(rows)
+    ext = ext128()
+    b = ext.MapfGPTObservationBuilder(torch.from_numpy(grids).cuda(), 16)
+    b.build_tokens(torch.from_numpy(rows.astype(np.int16)).cuda())
+    torch.cuda.synchronize()
+    assert np.array_equal(b.tokens.cpu().numpy(), ob.tokens)
+    assert ob.tokens.max() > 66  # the unbounded history tokens are really present
