@@ -37,6 +37,9 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 PEAK_HBM_BPS = 8.0e12
+# HBM bytes per token-kernel launch measured with rocprofv3 --pmc FETCH_SIZE /
+# WRITE_SIZE on this workload, scaled by the copy calibration (file header).
+TRAFFIC_FILE = ROOT / "profiles" / "tokens_kernel_pmc_1024x128_64.txt"
 
 # Algorithmic bytes per agent (derivation in DESIGN.md).
 B_TOKEN_KERNEL = 8 + 10 + 242 + 1024 + 1  # pos+goal, history, 11x11 u16 window, tokens, mask
@@ -108,6 +111,32 @@ class HipEvents:
         if rc != 0:
             raise RuntimeError(f"hipEventElapsedTime failed ({rc})")
         return float(ms.value)
+
+
+def measured_traffic() -> int | None:
+    """traffic_bytes from the committed PMC summary, or None."""
+    try:
+        for line in TRAFFIC_FILE.read_text().splitlines():
+            if line.startswith("traffic_bytes="):
+                return int(float(line.split("=", 1)[1]))
+    except OSError:
+        return None
+    return None
+
+
+def copy_calibration() -> None:
+    """Three device copies of 256 MiB: the reference reading for the PMC
+    byte counters (FETCH_SIZE / WRITE_SIZE per dispatch of a known size)."""
+    import torch
+
+    n = 256 << 20
+    a = torch.empty(n, dtype=torch.uint8, device="cuda")
+    b = torch.empty_like(a)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    print(f"copied 3 x {n} bytes", flush=True)
 
 
 def run_gpu(args) -> dict:
@@ -188,7 +217,7 @@ def run_gpu(args) -> dict:
             "peak": PEAK_HBM_BPS / 1e9,
             "unit": "GB/s",
             "frac": achieved / PEAK_HBM_BPS,
-            "traffic": None,
+            "traffic": measured_traffic(),
             "bytes_per_launch": tok_bytes,
             "avg_launch_us": tok_avg_s * 1e6,
         },
@@ -210,7 +239,12 @@ def main() -> int:
     p.add_argument("--cpu-envs", type=int, default=2)
     p.add_argument("--cpu-steps", type=int, default=24)
     p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--copy-calibration", action="store_true",
+                   help="only run 3 device copies of 256 MiB (PMC byte-counter calibration)")
     args = p.parse_args()
+    if args.copy_calibration:
+        copy_calibration()
+        return 0
     if args.gpus != 1:
         print(
             "bench.py measures one GPU: this build's hot path is per-env data parallel with no "
