@@ -1,0 +1,87 @@
+"""The C-ABI boundary (include/jointloom.h, libjointloom.so) without a GPU:
+every declared entry point is exported, the ctypes mirror has the header's
+struct layout (checked against gcc on the header itself), and the host-side
+argument checks return the documented status codes before any device work.
+"""
+import ctypes
+import re
+import subprocess
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "jointloom.h"
+
+
+def declared_functions():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"\b(jl_[a-z0-9_]+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from iclr_2027_jointoom_amd._abi import load_library
+
+    return load_library()
+
+
+def test_every_declared_entry_point_is_exported(lib):
+    from iclr_2027_jointoom_amd._abi import SIGNATURES
+
+    names = declared_functions()
+    assert len(names) >= 18
+    assert sorted(SIGNATURES) == names
+    for name in names:
+        assert getattr(lib, name) is not None
+
+
+def test_version_and_error_strings(lib):
+    assert lib.jl_version().decode().startswith("jointloom-gfx950")
+    assert b"invalid argument" in lib.jl_error_string(-1)
+    assert b"map profile" in lib.jl_error_string(-2)
+    assert b"edge buffer" in lib.jl_error_string(-3)
+    assert lib.jl_error_string(0) == b"success"
+
+
+def test_host_side_argument_checks_return_before_device_work(lib):
+    from iclr_2027_jointoom_amd._abi import MagatDesc, MapfGPTDesc, SimDesc
+
+    assert lib.jl_step(None, None) == -1
+    assert lib.jl_encode_map(None, None, 1, 64, 64, None) == -1
+    assert lib.jl_encode_map(1, 1, 1, 64, 48, None) == -2  # H must be 32/64/128/256
+    sim = SimDesc(n_envs=1, n_agents=4, map_w=64, map_h=64, task_mode=1)
+    assert lib.jl_step(ctypes.byref(sim), None) == -1  # null buffers
+    sim.map_h = 96
+    assert lib.jl_step(ctypes.byref(sim), None) == -2
+    b = MapfGPTDesc(n_envs=1, n_agents=4, map_w=300, map_h=64)
+    assert lib.jl_mapfgpt_build_state(ctypes.byref(b), 1, 1, 1, 1, None) == -2
+    assert lib.jl_mapfgpt_build_rows(ctypes.byref(b), None, None) == -1
+    m = MagatDesc(n_envs=1, n_agents=4, map_w=64, map_h=64)
+    assert lib.jl_magat_nodes(ctypes.byref(m), None) == -1
+    assert lib.jl_energy_maps(None, None, None, 1, 1, 1, 64, 64, 0, None) == -1
+    assert lib.jl_energy_maps(1, 1, None, 0, 1, 1, 64, 64, 0, None) == 0  # empty batch: nothing to do
+    assert lib.jl_seed_rng(None, 4, 1, None) == -1
+    assert lib.jl_decode_to_uint8(1, 1, 1, 17, None) == -1
+
+
+def test_ctypes_structs_match_the_c_layout(tmp_path):
+    from iclr_2027_jointoom_amd._abi import MagatDesc, MapfGPTDesc, SimDesc
+
+    structs = {"jl_sim_t": SimDesc, "jl_mapfgpt_t": MapfGPTDesc, "jl_magat_t": MagatDesc}
+    lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{HEADER}"', "int main(void) {"]
+    for cname, py in structs.items():
+        lines.append(f'printf("{cname} size %zu\\n", sizeof({cname}));')
+        for field, _ in py._fields_:
+            lines.append(f'printf("{cname} {field} %zu\\n", offsetof({cname}, {field}));')
+    lines += ["return 0; }"]
+    src = tmp_path / "layout.c"
+    src.write_text("\n".join(lines))
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-std=c11", "-o", str(exe), str(src)], check=True)
+    out = subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.split("\n")
+    c = {(ln.split()[0], ln.split()[1]): int(ln.split()[2]) for ln in out if ln}
+    for cname, py in structs.items():
+        assert c[(cname, "size")] == ctypes.sizeof(py), cname
+        for field, _ in py._fields_:
+            assert c[(cname, field)] == getattr(py, field).offset, (cname, field)

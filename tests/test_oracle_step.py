@@ -205,3 +205,15 @@ def test_standard_mode_kats(oracle):
     sim.step([[2]])
     after = (sim.cur_x, sim.step_counts, sim.state_packed, sim.grid_ocp)
     assert all(np.array_equal(a, b) for a, b in zip(before, after))
+
+
+@pytest.mark.parametrize("W,H", [(32, 32), (64, 64), (7, 128), (256, 256)])
+def test_encode_map_closed_form(oracle, W, H):
+    """grid_world_cuda.h:17-23: word = cell >> 5, bit = cell & 31, cell = x*H + y."""
+    rng = np.random.default_rng(W * 1000 + H)
+    grids = (rng.random((2, W, H)) < 0.3).astype(np.int32) * rng.integers(1, 7, size=(2, W, H))
+    bits = oracle.encode(grids)
+    assert bits.shape == (2, W * H // 32)
+    cells = np.arange(W * H)
+    got = (bits[:, cells >> 5] >> (cells & 31).astype(np.uint32)) & 1
+    assert np.array_equal(got.reshape(2, W, H), (grids != 0).astype(np.uint32))
