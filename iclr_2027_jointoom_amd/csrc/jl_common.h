@@ -67,6 +67,16 @@ __device__ __forceinline__ void wave_sync() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
+// Workgroup barrier that orders LDS only: LDS writes before it are seen by
+// LDS reads after it in every wavefront of the workgroup, while outstanding
+// global loads and stores stay in flight (__syncthreads() also waits for
+// those, which would drain a prefetch issued before the barrier).
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // 64-bit cross-lane read (ds_bpermute); lanes outside [0,64) wrap.
 __device__ __forceinline__ uint64_t shfl64(uint64_t v, int src_lane) {
     const int lo = __shfl((int)(uint32_t)v, src_lane, kWave);

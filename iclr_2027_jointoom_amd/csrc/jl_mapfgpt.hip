@@ -75,11 +75,11 @@ __device__ __forceinline__ void store_state_row(uint16_t* dst, uint32_t env, uin
 // (0,+1), is reachable and strictly closer to the goal than the agent's cell.
 template <int H, typename Field>
 __device__ __forceinline__ uint32_t greedy_mask(Field f, int x, int y, int W) {
-    const uint32_t c0 = f(x * H + y);
-    const uint32_t n0 = x > 0 ? f((x - 1) * H + y) : kUnreachable;
-    const uint32_t n1 = x + 1 < W ? f((x + 1) * H + y) : kUnreachable;
-    const uint32_t n2 = y > 0 ? f(x * H + y - 1) : kUnreachable;
-    const uint32_t n3 = y + 1 < H ? f(x * H + y + 1) : kUnreachable;
+    const uint32_t c0 = f(x, y);
+    const uint32_t n0 = x > 0 ? f(x - 1, y) : kUnreachable;
+    const uint32_t n1 = x + 1 < W ? f(x + 1, y) : kUnreachable;
+    const uint32_t n2 = y > 0 ? f(x, y - 1) : kUnreachable;
+    const uint32_t n3 = y + 1 < H ? f(x, y + 1) : kUnreachable;
     uint32_t m = 0;
     if (n0 != kUnreachable && c0 > n0) m |= 8u;
     if (n1 != kUnreachable && c0 > n1) m |= 4u;
@@ -177,16 +177,18 @@ __global__ __launch_bounds__(kWave* kWaves) void unpack_bfs_kernel(
     }
 
     // Fields this launch does not rewrite are read from HBM (written by an
-    // earlier launch); refreshed ones are read from LDS below.
+    // earlier launch), from the tiled copy where the cross of five cells
+    // spans 1-3 lines; refreshed ones are read from LDS below.
     const bool on_map = i < N && px < (uint32_t)W && py < (uint32_t)H;
+    const size_t tcells = tiled_cells(W, H);
     if (on_map && !reset) {
-        const uint16_t* f = b.cost_to_go + (size_t)i * cells;
-        info |= greedy_mask<H>([f](int c) { return (uint32_t)f[c]; }, (int)px, (int)py, W);
+        const uint16_t* f = b.cost_tiles + (size_t)i * tcells;
+        info |= greedy_mask<H>([f](int x, int y) { return (uint32_t)f[tile_offset<H>(x, y)]; },
+                               (int)px, (int)py, W);
     }
 
     constexpr int HW = RowWords<H>::HW;
     const int words = cells / 32;
-    const size_t tcells = tiled_cells(W, H);
     uint64_t todo = __ballot(reset);
     while (todo) {
         const int src = __ffsll((unsigned long long)todo) - 1;
@@ -220,7 +222,8 @@ __global__ __launch_bounds__(kWave* kWaves) void unpack_bfs_kernel(
             info |= ok ? (uint32_t)(overflow < 0xFFFFFF ? overflow : 0xFFFFFF) << kInfoOverflowShift
                        : kInfoBadGoal;
             if (spx < W && spy < H)
-                info |= greedy_mask<H>([s_dist](int c) { return (uint32_t)s_dist[c]; }, spx, spy, W);
+                info |= greedy_mask<H>([s_dist](int x, int y) { return (uint32_t)s_dist[x * H + y]; },
+                                       spx, spy, W);
         }
         // row-major field (the API tensor) and the tiled copy, 16-byte stores
         const uint4* lds4 = reinterpret_cast<const uint4*>(s_dist);
@@ -262,9 +265,14 @@ __global__ __launch_bounds__(kWave* kWaves) void unpack_bfs_kernel(
 constexpr int kTokThreads = 512;
 constexpr int kDenseCellLimit = 16384;
 constexpr int kChunk = 16;                 // egos whose windows share LDS at a time
-constexpr int kGatherPerThread = (kChunk * kCostTokens + kTokThreads - 1) / kTokThreads;
+// A window is read as 11 rows x 3 tile columns of 16-byte tile-row segments
+// (8 cells each): the 11 columns of a row span 2 or 3 tile columns.
+constexpr int kSegPerEgo = kDiam * 3;
+constexpr int kRegionCols = 24;            // cells per region row (3 tile columns)
+constexpr int kGatherPerThread = (kChunk * kSegPerEgo + kTokThreads - 1) / kTokThreads;
 constexpr int kSlotStride = 16;            // per-wave top-13 slot array (words)
 constexpr int kRecWords = 5;               // per-agent record: pos, goal, 3 words history+greedy
+constexpr int kEgosPerBlock = 64;          // egos per workgroup: an env spans ceil(A / 64) workgroups
 typedef int v4i __attribute__((ext_vector_type(4)));
 
 struct TokLayout {
@@ -297,7 +305,7 @@ __host__ __device__ inline TokLayout tok_layout(int A, int W, int H) {
     L.rec_off = off;
     off = align16(off + (size_t)A * kRecWords * 4);
     L.win_off = off;
-    off = align16(off + (size_t)kChunk * kCostTokens * 2);
+    off = align16(off + (size_t)kChunk * kSegPerEgo * 16);
     L.slot_off = off;
     off = align16(off + (size_t)(kTokThreads / kWave) * kSlotStride * 4);
     L.diag_off = off;
@@ -310,7 +318,12 @@ template <int H, bool kDense>
 __global__ __launch_bounds__(kTokThreads) void tokens_kernel(jl_mapfgpt_t b) {
     extern __shared__ __align__(16) uint8_t smem[];
     const int A = b.n_agents, W = b.map_w;
-    const int env = blockIdx.x;
+    // workgroup = (env, slice of kEgosPerBlock egos); every slice stages the whole env
+    const int parts = (A + kEgosPerBlock - 1) / kEgosPerBlock;
+    const int env = blockIdx.x / parts;
+    const int part = blockIdx.x - env * parts;
+    const int e_begin = part * kEgosPerBlock;
+    const int e_end = (e_begin + kEgosPerBlock) < A ? (e_begin + kEgosPerBlock) : A;
     const int tid = threadIdx.x;
     const int lane = tid & (kWave - 1);
     const int wave = tid / kWave;
@@ -322,7 +335,7 @@ __global__ __launch_bounds__(kTokThreads) void tokens_kernel(jl_mapfgpt_t b) {
     uint32_t* s_vals = reinterpret_cast<uint32_t*>(smem + L.vals_off);
     uint32_t* s_pos = reinterpret_cast<uint32_t*>(smem + L.pos_off);
     uint32_t* s_rec = reinterpret_cast<uint32_t*>(smem + L.rec_off);    // kRecWords per agent
-    uint16_t* s_win = reinterpret_cast<uint16_t*>(smem + L.win_off);    // [kChunk][121]
+    uint4* s_win = reinterpret_cast<uint4*>(smem + L.win_off);  // [kChunk][11 rows][3 segments]
     uint32_t* s_slot = reinterpret_cast<uint32_t*>(smem + L.slot_off);
     int* s_diag = reinterpret_cast<int*>(smem + L.diag_off);
     const uint32_t hmask = (uint32_t)L.hash_slots - 1;
@@ -341,7 +354,7 @@ __global__ __launch_bounds__(kTokThreads) void tokens_kernel(jl_mapfgpt_t b) {
         }
     }
     if (tid < 4) s_diag[tid] = 0;
-    __syncthreads();
+    lds_barrier();
     int d_over = 0, d_row = 0, d_dup = 0, d_bad = 0;
     for (int a = tid; a < A; a += kTokThreads) {
         const size_t g = (size_t)env * A + a;
@@ -349,7 +362,7 @@ __global__ __launch_bounds__(kTokThreads) void tokens_kernel(jl_mapfgpt_t b) {
         const uint32_t info = b.agent_info[g];
         const uint32_t px = st.y & 0xFFFFu, py = st.y >> 16;
         const uint32_t gx = st.z & 0xFFFFu, gy = st.z >> 16;
-        b.active_mask[g] = (px != gx || py != gy) ? 1 : 0;
+        if (a >= e_begin && a < e_end) b.active_mask[g] = (px != gx || py != gy) ? 1 : 0;
         const bool valid = px < (uint32_t)W && py < (uint32_t)H;
         s_pos[a] = valid ? (px | (py << 16)) : kNoAgent;
         // record: position, goal, raw history values (the token is computed
@@ -380,11 +393,12 @@ __global__ __launch_bounds__(kTokThreads) void tokens_kernel(jl_mapfgpt_t b) {
             ++d_bad;  // position off the map (scatter, :336-339)
         }
     }
+    if (part != 0) d_over = d_row = d_dup = d_bad = 0;  // the env's counts come from its first slice
     if (d_over) atomicAdd(&s_diag[0], d_over);
     if (d_row) atomicAdd(&s_diag[1], d_row);
     if (d_dup) atomicAdd(&s_diag[2], d_dup);
     if (d_bad) atomicAdd(&s_diag[3], d_bad);
-    __syncthreads();
+    lds_barrier();
     // relaxed device-scope adds: the build's totals are complete when the
     // kernel is, and pass 1 of the build cleared them
     if (tid < 4 && s_diag[tid]) atomicAdd(b.diagnostics + tid, s_diag[tid]);
@@ -431,61 +445,71 @@ __global__ __launch_bounds__(kTokThreads) void tokens_kernel(jl_mapfgpt_t b) {
         return s_vals[hash_find(s_keys, hmask, cell)];
     };
 
-    // Window gather of a chunk: item p = tid + k * kTokThreads of the chunk is
-    // window cell p % 121 of the chunk's ego p / 121, so consecutive threads
-    // read consecutive columns of a window row.  Every thread issues its loads without branches (addresses clamped into
-    // the field) and keeps the values in registers; `commit` writes them to
-    // LDS, unreachable for cells off the map, after the previous chunk's
-    // tokens have been produced.  Offsets are 32-bit bytes from the env's
-    // first tiled field (the host checks that an env's fields fit).
+    // Window gather of a chunk.  Item p = tid + k * kTokThreads is segment
+    // p % 33 = (row i, tile column j) of the chunk's ego p / 33: cells
+    // (ex - 5 + i, 8 * (tyl + j) .. 8 * (tyl + j) + 7) with tyl = floor((ey - 5) / 8),
+    // one 16-byte load from the tiled field.  Rows and tile columns outside the
+    // map are clamped into it (those cells read as unreachable when used), and
+    // a third tile column the window does not reach re-reads the second, so
+    // every load is issued without a branch and touches only the window's
+    // lines.  Values stay in registers until `commit` writes them to LDS, after
+    // the previous chunk's tokens have been produced.  Offsets are 32-bit
+    // bytes from the env's first tiled field (the host checks that they fit).
     const size_t tcells = tiled_cells(W, H);
     const uint8_t* env_tiles =
         reinterpret_cast<const uint8_t*>(b.cost_tiles + (size_t)env * A * tcells);
-    uint16_t graw[kGatherPerThread];
-    uint32_t gok = 0;
+    constexpr int TH = H / 8;
+    uint4 graw[kGatherPerThread];
     auto stage = [&](int c0, int nch) {
-        gok = 0;
 #pragma unroll
         for (int k = 0; k < kGatherPerThread; ++k) {
             const int p = tid + k * kTokThreads;
-            const int el = p / kCostTokens, c = p - el * kCostTokens;
+            const int el = p / kSegPerEgo, it = p - el * kSegPerEgo;
+            const int i = it / 3, j = it - (it / 3) * 3;
+            // items past the chunk repeat the chunk's first ego (lines already fetched)
             const bool live = el < nch;
             const uint32_t pos = s_pos[c0 + (live ? el : 0)];
-            const bool ok = live && pos != kNoAgent;
-            const int x = (int)(pos & 0xFFFFu) + c / kDiam - kRadius;
-            const int y = (int)(pos >> 16) + c % kDiam - kRadius;
-            const bool in = ok && x >= 0 && x < W && y >= 0 && y < H;
-            const int xc = ok ? (x < 0 ? 0 : (x >= W ? W - 1 : x)) : 0;
-            const int yc = ok ? (y < 0 ? 0 : (y >= H ? H - 1 : y)) : 0;
+            const bool ok = pos != kNoAgent;
+            const int ex = ok ? (int)(pos & 0xFFFFu) : 0, ey = ok ? (int)(pos >> 16) : 0;
+            int x = ex - kRadius + i;
+            x = x < 0 ? 0 : (x >= W ? W - 1 : x);
+            const int tyl = ((ey - kRadius + 64) >> 3) - 8;  // floor((ey - 5) / 8)
+            int tcol = tyl + ((j == 2 && (tyl + 2) * 8 > ey + kRadius) ? 1 : j);
+            tcol = tcol < 0 ? 0 : (tcol >= TH ? TH - 1 : tcol);
             const uint32_t off =
-                ((uint32_t)(c0 + (live ? el : 0)) * (uint32_t)tcells + tile_offset<H>(xc, yc)) * 2u;
-            graw[k] = *reinterpret_cast<const uint16_t*>(env_tiles + off);
-            gok |= in ? (1u << k) : 0u;
+                ((uint32_t)(c0 + (live ? el : 0)) * (uint32_t)tcells +
+                 ((uint32_t)(x >> 3) * TH + (uint32_t)tcol) * 64u + (uint32_t)(x & 7) * 8u) * 2u;
+            graw[k] = *reinterpret_cast<const uint4*>(env_tiles + off);
         }
     };
     auto commit = [&](int nch) {
         // keep every use of the gathered values here, so that the loads stay
         // in flight across the previous chunk's token work
 #pragma unroll
-        for (int k = 0; k < kGatherPerThread; ++k) asm volatile("" : "+v"(graw[k]));
+        for (int k = 0; k < kGatherPerThread; ++k)
+            asm volatile("" : "+v"(graw[k].x), "+v"(graw[k].y), "+v"(graw[k].z), "+v"(graw[k].w));
 #pragma unroll
         for (int k = 0; k < kGatherPerThread; ++k) {
             const int p = tid + k * kTokThreads;
-            if (p < nch * kCostTokens) s_win[p] = (gok >> k) & 1u ? graw[k] : kUnreachable;
+            if (p < nch * kSegPerEgo) s_win[p] = graw[k];
         }
     };
 
     // ---- phase 2: chunks of kChunk egos, one wavefront per ego ---------------
-    const int nchunks = (A + kChunk - 1) / kChunk;
-    stage(0, A < kChunk ? A : kChunk);
+    const int nchunks = (e_end - e_begin + kChunk - 1) / kChunk;
+    stage(e_begin, (e_end - e_begin) < kChunk ? (e_end - e_begin) : kChunk);
     for (int q = 0; q < nchunks; ++q) {
-        const int c0 = q * kChunk;
-        const int nch = (A - c0) < kChunk ? (A - c0) : kChunk;
+        const int c0 = e_begin + q * kChunk;
+        const int nch = (e_end - c0) < kChunk ? (e_end - c0) : kChunk;
         commit(nch);
-        __syncthreads();
-        if (q + 1 < nchunks) {
+        lds_barrier();
+        {
+            // always staged (no branch around the loads, which would make the
+            // compiler wait for them here); after the last chunk every item
+            // is dead and repeats lines of this chunk
             const int c1 = c0 + kChunk;
-            stage(c1, (A - c1) < kChunk ? (A - c1) : kChunk);
+            const bool more = q + 1 < nchunks;
+            stage(more ? c1 : c0, more ? ((e_end - c1) < kChunk ? (e_end - c1) : kChunk) : 0);
         }
         // lane i holds the position of this wave's i-th ego of the chunk
         const int mine = wave < nch ? (nch - wave + nwaves - 1) / nwaves : 0;
@@ -497,13 +521,20 @@ __global__ __launch_bounds__(kTokThreads) void tokens_kernel(jl_mapfgpt_t b) {
             int tok[4] = {kTokPad, kTokPad, kTokPad, kTokPad};
             if (pos != kNoAgent) {
                 const int ex = (int)(pos & 0xFFFFu), ey = (int)(pos >> 16);
-                const uint16_t* win = s_win + el * kCostTokens;
+                // region row i = dx + 5, column = ey + dy - 8 * tyl (see `stage`)
+                const uint16_t* win = reinterpret_cast<const uint16_t*>(s_win + el * kSegPerEgo);
+                const int col0 = ey - 8 * (((ey - kRadius + 64) >> 3) - 8) - kRadius;
                 // all independent LDS reads of the ego first, then one wait
-                const uint32_t center = win[kCostTokens / 2];
+                const uint32_t center = win[kRadius * kRegionCols + col0 + kRadius];
                 uint32_t wv[4];
 #pragma unroll
-                for (int j = 0; j < 4; ++j)
-                    wv[j] = win[(cost_mask >> j) & 1u ? 4 * lane + j : kCostTokens / 2];
+                for (int j = 0; j < 4; ++j) {
+                    const int t = (cost_mask >> j) & 1u ? 4 * lane + j : kCostTokens / 2;
+                    const int di = t / kDiam, dj = t - (t / kDiam) * kDiam;  // dx + 5, dy + 5
+                    const int x = ex + di - kRadius, y = ey + dj - kRadius;
+                    const uint32_t v = win[di * kRegionCols + col0 + dj];
+                    wv[j] = (x >= 0 && x < W && y >= 0 && y < H) ? v : (uint32_t)kUnreachable;
+                }
                 const uint32_t id0 = agent_at(ex + qdx0, ey + qdy0);
                 const uint32_t id1r = agent_at(ex + qdx1, ey + qdy1);
                 const uint32_t id1 = qval1 ? id1r : kNoAgent;
@@ -566,7 +597,7 @@ __global__ __launch_bounds__(kTokThreads) void tokens_kernel(jl_mapfgpt_t b) {
             __builtin_nontemporal_store(
                 out, reinterpret_cast<v4i*>(b.tokens + ((size_t)env * A + e) * kContext) + lane);
         }
-        __syncthreads();  // the chunk's windows are consumed
+        lds_barrier();  // the chunk's windows are consumed
     }
 }
 
@@ -679,12 +710,11 @@ int build(const jl_mapfgpt_t* b, const int16_t* rows, const int16_t* cx, const i
             rc = status(hipEventRecord((hipEvent_t)b->token_events[0], stream));
             if (rc) return rc;
         }
+        const dim3 grid2((unsigned)b->n_envs * ((b->n_agents + kEgosPerBlock - 1) / kEgosPerBlock));
         if (L.dense) {
-            hipLaunchKernelGGL((tokens_kernel<H, true>), dim3(b->n_envs), dim3(kTokThreads), L.total,
-                               stream, *b);
+            hipLaunchKernelGGL((tokens_kernel<H, true>), grid2, dim3(kTokThreads), L.total, stream, *b);
         } else {
-            hipLaunchKernelGGL((tokens_kernel<H, false>), dim3(b->n_envs), dim3(kTokThreads),
-                               L.total, stream, *b);
+            hipLaunchKernelGGL((tokens_kernel<H, false>), grid2, dim3(kTokThreads), L.total, stream, *b);
         }
         rc = launch_status();
         if (rc) return rc;
