@@ -250,20 +250,25 @@ __global__ __launch_bounds__(kWave* kWaves) void unpack_bfs_kernel(
 // Pass 2: tokens (mapf_gpt_materialize_tokens_kernel, :350-497) plus the
 // agent scatter and its diagnostics (:328-347).
 //
-// Phase 1 (whole workgroup, one env): positions and each agent's record
-// (position, goal, raw history values and greedy mask: the ego-independent
-// part of its 10 tokens) and a cell -> agent map live in LDS; the map is
-// dense (one int32 per cell) up to 16384 cells, an occupancy bitmap + hash
-// beyond.  Phase 2 (chunks of kChunk egos): the chunk's windows are gathered
-// into LDS by every thread; then each ego is one wavefront: lane l produces
-// tokens 4l..4l+3.  Visible agents: lanes test window cells l and l+64 in the
-// map; a candidate's rank under the key (Manhattan distance, id) is the
-// number of smaller keys, counted by walking the ballot of candidates with
-// uniform readlanes; ranks 0..12 are the reference's sorted top 13 because
-// keys are unique.  The row is stored as 64 x 16-byte writes.
+// Phase 1 (whole workgroup, one env): positions, each agent's record
+// (position and goal words) and its six ego-independent tokens (five history
+// tokens and the greedy token, :437-456) and a cell -> agent map live in LDS.
+// The map is dense (one int32 per cell of the map grown by a kRadius border
+// of empty cells, so a window probe needs no bounds test) while it fits, an
+// occupancy bitmap + hash beyond.  Phase 2 (chunks of kChunk egos): the
+// chunk's windows are gathered into LDS by every thread, cells outside the
+// map staged as unreachable; then each ego is one wavefront.  Visible agents:
+// lane l probes window cells l and l + 64 in the map; a candidate's rank
+// under the key (Manhattan distance, id) is the number of smaller keys,
+// counted by walking the ballot of candidates with uniform readlanes; ranks
+// 0..12 are the reference's sorted top 13 because keys are unique.  Every
+// token of the row is computed by exactly one lane (two cost tokens per lane,
+// one coordinate token on lanes 0..51, the six copied tokens of the 13 slots
+// on lanes 0..63 and 0..13) into the wavefront's LDS row, which is then
+// stored as 64 x 16-byte writes.
 // ---------------------------------------------------------------------------
 constexpr int kTokThreads = 512;
-constexpr int kDenseCellLimit = 16384;
+constexpr int kDenseCellLimit = 16384;     // map cells up to which the agent map is dense
 constexpr int kChunk = 16;                 // egos whose windows share LDS at a time
 // A window is read as 11 rows x 3 tile columns of 16-byte tile-row segments
 // (8 cells each): the 11 columns of a row span 2 or 3 tile columns.
@@ -271,15 +276,23 @@ constexpr int kSegPerEgo = kDiam * 3;
 constexpr int kRegionCols = 24;            // cells per region row (3 tile columns)
 constexpr int kGatherPerThread = (kChunk * kSegPerEgo + kTokThreads - 1) / kTokThreads;
 constexpr int kSlotStride = 16;            // per-wave top-13 slot array (words)
-constexpr int kRecWords = 5;               // per-agent record: pos, goal, 3 words history+greedy
+constexpr int kRecWords = 2;               // per-agent record: position word, goal word
+constexpr int kCopyTokens = 6;             // per-agent tokens independent of the ego
+constexpr int kCoordLanes = kVisible * 4;  // lanes producing the 52 coordinate tokens
+constexpr int kCopyItems = kVisible * kCopyTokens;  // 78 copied tokens per row
 constexpr int kEgosPerBlock = 64;          // egos per workgroup: an env spans ceil(A / 64) workgroups
+constexpr int kEgosPerWave = kChunk / (kTokThreads / kWave);  // rows each wavefront stores per chunk
+static_assert(kEgosPerWave * (kTokThreads / kWave) == kChunk, "chunk must split evenly over waves");
+static_assert(kCostTokens + kVisible * kAgentTokens <= kContext, "row layout");
+static_assert(kCopyItems > kWave && kCopyItems <= 2 * kWave, "copied tokens take one or two per lane");
 typedef int v4i __attribute__((ext_vector_type(4)));
 
 struct TokLayout {
     bool dense;
     int hash_slots;
-    size_t map_off, occ_off, keys_off, vals_off, pos_off, rec_off, win_off, slot_off, diag_off,
-        total;
+    int map_h;  // column count of the (bordered) dense map
+    size_t map_off, occ_off, keys_off, vals_off, pos_off, rec_off, copy_off, win_off, slot_off,
+        row_off, diag_off, total;
 };
 
 __host__ __device__ inline size_t align16(size_t v) { return (v + 15) & ~(size_t)15; }
@@ -288,12 +301,13 @@ __host__ __device__ inline TokLayout tok_layout(int A, int W, int H) {
     TokLayout L;
     const size_t cells = (size_t)W * H;
     L.dense = cells <= (size_t)kDenseCellLimit;
+    L.map_h = H + 2 * kRadius;
     int s = 64;
     while (s < 2 * A) s <<= 1;
     L.hash_slots = L.dense ? 0 : s;
     size_t off = 0;
     L.map_off = off;
-    if (L.dense) off = align16(off + cells * 4);
+    if (L.dense) off = align16(off + (size_t)(W + 2 * kRadius) * L.map_h * 4);
     L.occ_off = off;
     if (!L.dense) off = align16(off + cells / 8);
     L.keys_off = off;
@@ -304,14 +318,27 @@ __host__ __device__ inline TokLayout tok_layout(int A, int W, int H) {
     off = align16(off + (size_t)A * 4);
     L.rec_off = off;
     off = align16(off + (size_t)A * kRecWords * 4);
+    L.copy_off = off;
+    off = align16(off + (size_t)A * kCopyTokens * 4);
     L.win_off = off;
     off = align16(off + (size_t)kChunk * kSegPerEgo * 16);
     L.slot_off = off;
     off = align16(off + (size_t)(kTokThreads / kWave) * kSlotStride * 4);
+    L.row_off = off;
+    off = align16(off + (size_t)(kTokThreads / kWave) * kContext * 4);
     L.diag_off = off;
     off = align16(off + 4 * 4);
     L.total = off;
     return L;
+}
+
+// Cost token of a window value (mapf_gpt_cuda.cu:413-428) without branches;
+// unreachable cells, including those outside the map, hold kUnreachable.
+__device__ __forceinline__ int cost_token_flat(uint32_t v, int center_minus_limit) {
+    const int t = (int)v - center_minus_limit;  // d + kCostLimit
+    const int clip = t < 0 ? kTokNegClip : kTokPosClip;
+    const int r = (uint32_t)t <= (uint32_t)(2 * kCostLimit) ? t : clip;
+    return v == kUnreachable ? kTokUnreachable : r;
 }
 
 template <int H, bool kDense>
@@ -329,23 +356,28 @@ __global__ __launch_bounds__(kTokThreads) void tokens_kernel(jl_mapfgpt_t b) {
     const int wave = tid / kWave;
     constexpr int nwaves = kTokThreads / kWave;
     const TokLayout L = tok_layout(A, W, H);
+    constexpr int MH = H + 2 * kRadius;  // dense map columns
     uint32_t* s_map = reinterpret_cast<uint32_t*>(smem + L.map_off);
     uint32_t* s_occ = reinterpret_cast<uint32_t*>(smem + L.occ_off);
     uint32_t* s_keys = reinterpret_cast<uint32_t*>(smem + L.keys_off);
     uint32_t* s_vals = reinterpret_cast<uint32_t*>(smem + L.vals_off);
     uint32_t* s_pos = reinterpret_cast<uint32_t*>(smem + L.pos_off);
     uint32_t* s_rec = reinterpret_cast<uint32_t*>(smem + L.rec_off);    // kRecWords per agent
+    int* s_copy = reinterpret_cast<int*>(smem + L.copy_off);            // kCopyTokens per agent
     uint4* s_win = reinterpret_cast<uint4*>(smem + L.win_off);  // [kChunk][11 rows][3 segments]
     uint32_t* s_slot = reinterpret_cast<uint32_t*>(smem + L.slot_off);
+    int* s_row = reinterpret_cast<int*>(smem + L.row_off);      // [nwaves][kContext]
     int* s_diag = reinterpret_cast<int*>(smem + L.diag_off);
     const uint32_t hmask = (uint32_t)L.hash_slots - 1;
     const size_t cells = (size_t)W * H;
+    uint32_t* my_slots = s_slot + wave * kSlotStride;
+    int* my_row = s_row + wave * kContext;
 
     // ---- phase 1 -----------------------------------------------------------
     if (kDense) {
-        uint4* m4 = reinterpret_cast<uint4*>(s_map);
-        const uint4 none = make_uint4(kNoAgent, kNoAgent, kNoAgent, kNoAgent);
-        for (int k = tid; k < (int)(cells / 4); k += kTokThreads) m4[k] = none;
+        const int mcells = (W + 2 * kRadius) * MH;  // even: MH is
+        uint2* m2 = reinterpret_cast<uint2*>(s_map);
+        for (int k = tid; k < mcells / 2; k += kTokThreads) m2[k] = make_uint2(kNoAgent, kNoAgent);
     } else {
         for (int k = tid; k < (int)(cells / 32); k += kTokThreads) s_occ[k] = 0;
         for (int k = tid; k < L.hash_slots; k += kTokThreads) {
@@ -353,6 +385,11 @@ __global__ __launch_bounds__(kTokThreads) void tokens_kernel(jl_mapfgpt_t b) {
             s_vals[k] = kNoAgent;
         }
     }
+    // slot arrays only ever hold agent ids (stale entries stay readable);
+    // row tokens past the agent section are always padding
+    if (lane < kSlotStride) my_slots[lane] = 0;
+    if (lane < kContext - (kCostTokens + kVisible * kAgentTokens))
+        my_row[kCostTokens + kVisible * kAgentTokens + lane] = kTokPad;
     if (tid < 4) s_diag[tid] = 0;
     lds_barrier();
     int d_over = 0, d_row = 0, d_dup = 0, d_bad = 0;
@@ -365,24 +402,27 @@ __global__ __launch_bounds__(kTokThreads) void tokens_kernel(jl_mapfgpt_t b) {
         if (a >= e_begin && a < e_end) b.active_mask[g] = (px != gx || py != gy) ? 1 : 0;
         const bool valid = px < (uint32_t)W && py < (uint32_t)H;
         s_pos[a] = valid ? (px | (py << 16)) : kNoAgent;
-        // record: position, goal, raw history values (the token is computed
-        // at use: any uint16 is legal in a raw row) and the greedy mask
+        s_rec[a * kRecWords + 0] = st.y;
+        s_rec[a * kRecWords + 1] = st.z;
+        // history tokens from the raw values (any uint16 is legal in a raw
+        // row, :442-451) and the greedy token (:452-456)
         const uint16_t* h = b.histories + g * 5;
-        uint32_t* rec = s_rec + a * kRecWords;
-        rec[0] = st.y;
-        rec[1] = st.z;
-        rec[2] = (uint32_t)h[0] | ((uint32_t)h[1] << 16);
-        rec[3] = (uint32_t)h[2] | ((uint32_t)h[3] << 16);
-        rec[4] = (uint32_t)h[4] | ((info & kInfoGreedy) << 16);
+        int* cp = s_copy + a * kCopyTokens;
+#pragma unroll
+        for (int k = 0; k < 5; ++k) {
+            const int v = (int)h[k];
+            cp[k] = v == 5 ? kTokEmptyAction : kTokWait + v;
+        }
+        cp[5] = kTokGreedy + (int)(info & kInfoGreedy);
         d_over += (int)(info >> kInfoOverflowShift);
         d_row += (info & kInfoBadRow) ? 1 : 0;
         d_bad += (info & kInfoBadGoal) ? 1 : 0;
         if (valid) {
-            const uint32_t cell = px * H + py;
             uint32_t prev;
             if (kDense) {
-                prev = atomicMin(&s_map[cell], (uint32_t)a);
+                prev = atomicMin(&s_map[(px + kRadius) * MH + py + kRadius], (uint32_t)a);
             } else {
+                const uint32_t cell = px * H + py;
                 atomicOr(&s_occ[cell >> 5], 1u << (cell & 31));
                 const uint32_t slot = hash_insert(s_keys, hmask, cell);
                 prev = atomicMin(&s_vals[slot], (uint32_t)a);
@@ -404,41 +444,32 @@ __global__ __launch_bounds__(kTokThreads) void tokens_kernel(jl_mapfgpt_t b) {
     if (tid < 4 && s_diag[tid]) atomicAdd(b.diagnostics + tid, s_diag[tid]);
 
     // ---- phase 2: lane constants ---------------------------------------------
-    // Lane l produces tokens 4l..4l+3: byte j of slot_pack / field_pack is
-    // the visible-agent slot / record field of token 4l+j (slot kVisible:
-    // not an agent token).
-    uint32_t cost_mask = 0, agent_mask = 0, slot_pack = 0, field_pack = 0;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int t = 4 * lane + j;
-        cost_mask |= t < kCostTokens ? (1u << j) : 0u;
-        const int u = t - kCostTokens;
-        const bool agent_tok = u >= 0 && u < kVisible * kAgentTokens;
-        agent_mask |= agent_tok ? (1u << j) : 0u;
-        slot_pack |= (uint32_t)(agent_tok ? u / kAgentTokens : kVisible) << (8 * j);
-        field_pack |= (uint32_t)(agent_tok ? u % kAgentTokens : 0) << (8 * j);
-    }
-    auto slot_of = [&](int j) { return (int)((slot_pack >> (8 * j)) & 0xFFu); };
-    const int slot_a = slot_of(0) < kVisible ? slot_of(0) : slot_of(3);
-    const int slot_b = slot_of(3) < kVisible ? slot_of(3) : slot_of(0);
-    const int q0 = lane, q1 = lane + kWave;
-    const int qdx0 = q0 / kDiam - kRadius, qdy0 = q0 % kDiam - kRadius;
-    const int qdx1 = q1 / kDiam - kRadius, qdy1 = q1 % kDiam - kRadius;
-    const bool qval1 = q1 < kCostTokens;
-    const uint32_t qd0 = (uint32_t)(abs(qdx0) + abs(qdy0)) << 16;
-    const uint32_t qd1 = (uint32_t)(abs(qdx1) + abs(qdy1)) << 16;
-    uint32_t* my_slots = s_slot + wave * kSlotStride;
+    // Window cells q0 = lane and q1 = lane + 64 (row-major over the 11x11
+    // window; q1 exists on lanes 0..56): probed for agents and turned into
+    // cost tokens q0, q1.
+    const bool has_q1 = lane + kWave < kCostTokens;
+    const int q0 = lane, q1 = has_q1 ? lane + kWave : lane;
+    const int di0 = q0 / kDiam, dj0 = q0 % kDiam, di1 = q1 / kDiam, dj1 = q1 % kDiam;
+    const int win0 = di0 * kRegionCols + dj0, win1 = di1 * kRegionCols + dj1;
+    const int map0 = (di0 - kRadius) * MH + (dj0 - kRadius);
+    const int map1 = (di1 - kRadius) * MH + (dj1 - kRadius);
+    const uint32_t qd0 = (uint32_t)(abs(di0 - kRadius) + abs(dj0 - kRadius)) << 16;
+    const uint32_t qd1 = (uint32_t)(abs(di1 - kRadius) + abs(dj1 - kRadius)) << 16;
+    constexpr uint64_t kQ1Lanes = (1ull << (kCostTokens - kWave)) - 1;
+    // coordinate token of lane l < 52: slot l / 4, field l % 4 (px, py, gx, gy)
+    const int c_slot = lane >> 2, c_field = lane & 3;
+    const int c_pos = kCostTokens + c_slot * kAgentTokens + c_field;
+    // copied tokens u = lane and u = lane + 64 (< 78): slot u / 6, token u % 6
+    const int u1 = lane + kWave < kCopyItems ? lane + kWave : lane;
+    const int k_slot0 = lane / kCopyTokens, k_tok0 = lane % kCopyTokens;
+    const int k_slot1 = u1 / kCopyTokens, k_tok1 = u1 % kCopyTokens;
+    const int k_pos0 = kCostTokens + k_slot0 * kAgentTokens + 4 + k_tok0;
+    const int k_pos1 = kCostTokens + k_slot1 * kAgentTokens + 4 + k_tok1;
+    const uint16_t* s_rec16 = reinterpret_cast<const uint16_t*>(s_rec);
 
-    // Agent at (x, y) of this env or kNoAgent.  The dense map is read at a
-    // clamped cell so the read needs no branch.
-    auto agent_at = [&](int x, int y) -> uint32_t {
+    // Agent at (x, y) of this env or kNoAgent (hash map).
+    auto agent_at_hash = [&](int x, int y) -> uint32_t {
         const bool in = x >= 0 && x < W && y >= 0 && y < H;
-        if (kDense) {
-            const int xc = x < 0 ? 0 : (x >= W ? W - 1 : x);
-            const int yc = y < 0 ? 0 : (y >= H ? H - 1 : y);
-            const uint32_t v = s_map[xc * H + yc];
-            return in ? v : kNoAgent;
-        }
         if (!in) return kNoAgent;
         const uint32_t cell = (uint32_t)(x * H + y);
         if (!((s_occ[cell >> 5] >> (cell & 31)) & 1u)) return kNoAgent;
@@ -449,8 +480,8 @@ __global__ __launch_bounds__(kTokThreads) void tokens_kernel(jl_mapfgpt_t b) {
     // p % 33 = (row i, tile column j) of the chunk's ego p / 33: cells
     // (ex - 5 + i, 8 * (tyl + j) .. 8 * (tyl + j) + 7) with tyl = floor((ey - 5) / 8),
     // one 16-byte load from the tiled field.  Rows and tile columns outside the
-    // map are clamped into it (those cells read as unreachable when used), and
-    // a third tile column the window does not reach re-reads the second, so
+    // map are clamped into it for the load and staged as unreachable, and a
+    // third tile column the window does not reach re-reads the second, so
     // every load is issued without a branch and touches only the window's
     // lines.  Values stay in registers until `commit` writes them to LDS, after
     // the previous chunk's tokens have been produced.  Offsets are 32-bit
@@ -460,6 +491,7 @@ __global__ __launch_bounds__(kTokThreads) void tokens_kernel(jl_mapfgpt_t b) {
         reinterpret_cast<const uint8_t*>(b.cost_tiles + (size_t)env * A * tcells);
     constexpr int TH = H / 8;
     uint4 graw[kGatherPerThread];
+    bool gin[kGatherPerThread];
     auto stage = [&](int c0, int nch) {
 #pragma unroll
         for (int k = 0; k < kGatherPerThread; ++k) {
@@ -471,11 +503,12 @@ __global__ __launch_bounds__(kTokThreads) void tokens_kernel(jl_mapfgpt_t b) {
             const uint32_t pos = s_pos[c0 + (live ? el : 0)];
             const bool ok = pos != kNoAgent;
             const int ex = ok ? (int)(pos & 0xFFFFu) : 0, ey = ok ? (int)(pos >> 16) : 0;
-            int x = ex - kRadius + i;
-            x = x < 0 ? 0 : (x >= W ? W - 1 : x);
+            const int xr = ex - kRadius + i;
+            const int x = xr < 0 ? 0 : (xr >= W ? W - 1 : xr);
             const int tyl = ((ey - kRadius + 64) >> 3) - 8;  // floor((ey - 5) / 8)
-            int tcol = tyl + ((j == 2 && (tyl + 2) * 8 > ey + kRadius) ? 1 : j);
-            tcol = tcol < 0 ? 0 : (tcol >= TH ? TH - 1 : tcol);
+            const int tr = tyl + ((j == 2 && (tyl + 2) * 8 > ey + kRadius) ? 1 : j);
+            const int tcol = tr < 0 ? 0 : (tr >= TH ? TH - 1 : tr);
+            gin[k] = xr == x && tr == tcol;
             const uint32_t off =
                 ((uint32_t)(c0 + (live ? el : 0)) * (uint32_t)tcells +
                  ((uint32_t)(x >> 3) * TH + (uint32_t)tcol) * 64u + (uint32_t)(x & 7) * 8u) * 2u;
@@ -491,61 +524,69 @@ __global__ __launch_bounds__(kTokThreads) void tokens_kernel(jl_mapfgpt_t b) {
 #pragma unroll
         for (int k = 0; k < kGatherPerThread; ++k) {
             const int p = tid + k * kTokThreads;
-            if (p < nch * kSegPerEgo) s_win[p] = graw[k];
+            // per-component selects (a select of the whole vector becomes a
+            // select of stack addresses)
+            const uint32_t fill = gin[k] ? 0u : 0xFFFFFFFFu;
+            const uint4 v = make_uint4(graw[k].x | fill, graw[k].y | fill, graw[k].z | fill,
+                                       graw[k].w | fill);
+            if (p < nch * kSegPerEgo) s_win[p] = v;
         }
     };
 
     // ---- phase 2: chunks of kChunk egos, one wavefront per ego ---------------
+    // Vector-memory stores count in the same in-order counter as the gather
+    // loads.  Every wavefront therefore stores exactly kEgosPerWave rows per
+    // chunk (a slot past the chunk's end repeats the chunk's first ego: the
+    // same tokens into the same row) and the next chunk's windows are
+    // committed after those stores in straight-line code, so waiting for the
+    // loads does not wait for the stores.
     const int nchunks = (e_end - e_begin + kChunk - 1) / kChunk;
-    stage(e_begin, (e_end - e_begin) < kChunk ? (e_end - e_begin) : kChunk);
+    {
+        const int n0 = (e_end - e_begin) < kChunk ? (e_end - e_begin) : kChunk;
+        stage(e_begin, n0);
+        commit(n0);
+    }
+    lds_barrier();
     for (int q = 0; q < nchunks; ++q) {
         const int c0 = e_begin + q * kChunk;
         const int nch = (e_end - c0) < kChunk ? (e_end - c0) : kChunk;
-        commit(nch);
-        lds_barrier();
-        {
-            // always staged (no branch around the loads, which would make the
-            // compiler wait for them here); after the last chunk every item
-            // is dead and repeats lines of this chunk
-            const int c1 = c0 + kChunk;
-            const bool more = q + 1 < nchunks;
-            stage(more ? c1 : c0, more ? ((e_end - c1) < kChunk ? (e_end - c1) : kChunk) : 0);
-        }
+        // always staged (no branch around the loads, which would make the
+        // compiler wait for them early); after the last chunk every item is
+        // dead and repeats lines of this chunk
+        const int c1 = c0 + kChunk;
+        const bool more = q + 1 < nchunks;
+        const int nnext = more ? ((e_end - c1) < kChunk ? (e_end - c1) : kChunk) : 0;
+        stage(more ? c1 : c0, nnext);
         // lane i holds the position of this wave's i-th ego of the chunk
-        const int mine = wave < nch ? (nch - wave + nwaves - 1) / nwaves : 0;
-        const uint32_t pos_mine = lane < mine ? s_pos[c0 + wave + lane * nwaves] : kNoAgent;
-        for (int i = 0; i < mine; ++i) {
-            const int el = wave + i * nwaves;
+        const int el_lane = wave + (lane < kEgosPerWave ? lane : 0) * nwaves;
+        const uint32_t pos_mine = s_pos[c0 + (el_lane < nch ? el_lane : 0)];
+#pragma unroll
+        for (int i = 0; i < kEgosPerWave; ++i) {
+            const int el = (wave + i * nwaves) < nch ? (wave + i * nwaves) : 0;
             const int e = c0 + el;
             const uint32_t pos = (uint32_t)__builtin_amdgcn_readlane((int)pos_mine, i);
-            int tok[4] = {kTokPad, kTokPad, kTokPad, kTokPad};
+            v4i out = {kTokPad, kTokPad, kTokPad, kTokPad};
             if (pos != kNoAgent) {
                 const int ex = (int)(pos & 0xFFFFu), ey = (int)(pos >> 16);
-                // region row i = dx + 5, column = ey + dy - 8 * tyl (see `stage`)
-                const uint16_t* win = reinterpret_cast<const uint16_t*>(s_win + el * kSegPerEgo);
-                const int col0 = ey - 8 * (((ey - kRadius + 64) >> 3) - 8) - kRadius;
-                // all independent LDS reads of the ego first, then one wait
-                const uint32_t center = win[kRadius * kRegionCols + col0 + kRadius];
-                uint32_t wv[4];
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const int t = (cost_mask >> j) & 1u ? 4 * lane + j : kCostTokens / 2;
-                    const int di = t / kDiam, dj = t - (t / kDiam) * kDiam;  // dx + 5, dy + 5
-                    const int x = ex + di - kRadius, y = ey + dj - kRadius;
-                    const uint32_t v = win[di * kRegionCols + col0 + dj];
-                    wv[j] = (x >= 0 && x < W && y >= 0 && y < H) ? v : (uint32_t)kUnreachable;
+                // region row = dx + 5, column = ey + dy - 8 * tyl (see `stage`)
+                const uint16_t* win = reinterpret_cast<const uint16_t*>(s_win + el * kSegPerEgo) +
+                                      (ey - 8 * (((ey - kRadius + 64) >> 3) - 8) - kRadius);
+                const uint32_t center = win[kRadius * kRegionCols + kRadius];
+                const uint32_t v0 = win[win0];
+                const uint32_t v1 = win[win1];
+                uint32_t id0, id1;
+                if (kDense) {
+                    const uint32_t* mrow = s_map + (ex + kRadius) * MH + (ey + kRadius);
+                    id0 = mrow[map0];
+                    id1 = mrow[map1];
+                } else {
+                    id0 = agent_at_hash(ex + di0 - kRadius, ey + dj0 - kRadius);
+                    id1 = agent_at_hash(ex + di1 - kRadius, ey + dj1 - kRadius);
                 }
-                const uint32_t id0 = agent_at(ex + qdx0, ey + qdy0);
-                const uint32_t id1r = agent_at(ex + qdx1, ey + qdy1);
-                const uint32_t id1 = qval1 ? id1r : kNoAgent;
-#pragma unroll
-                for (int j = 0; j < 4; ++j)
-                    tok[j] = (cost_mask >> j) & 1u ? cost_token(wv[j], center) : kTokPad;
-                // candidates: (distance << 16 | id), all-ones when the cell is empty
-                const uint32_t key0 = id0 == kNoAgent ? 0xFFFFFFFFu : (qd0 | id0);
-                const uint32_t key1 = id1 == kNoAgent ? 0xFFFFFFFFu : (qd1 | id1);
+                // candidates: (distance << 16 | id); an empty cell's key is all ones
+                const uint32_t key0 = qd0 | id0, key1 = qd1 | id1;
                 const uint64_t m0 = __ballot(id0 != kNoAgent);
-                const uint64_t m1 = __ballot(id1 != kNoAgent);
+                const uint64_t m1 = __ballot(id1 != kNoAgent) & kQ1Lanes;
                 int r0 = 0, r1 = 0;
                 for (uint64_t m = m0; m; m &= m - 1) {
                     const uint32_t k =
@@ -561,43 +602,42 @@ __global__ __launch_bounds__(kTokThreads) void tokens_kernel(jl_mapfgpt_t b) {
                 }
                 const int count = __popcll(m0) + __popcll(m1);
                 const int nsel = count < kVisible ? count : kVisible;
-                if (nsel > 0) {
-                    // the selected ids move through the wave's slot array in LDS
-                    if (id0 != kNoAgent && r0 < kVisible) my_slots[r0] = id0;
-                    if (id1 != kNoAgent && r1 < kVisible) my_slots[r1] = id1;
-                    wave_sync();
-                    uint32_t ida = my_slots[slot_a < kVisible ? slot_a : 0];
-                    uint32_t idb = my_slots[slot_b < kVisible ? slot_b : 0];
-                    // slots at or past nsel hold stale ids: keep the reads in bounds
-                    ida = ida < (uint32_t)A ? ida : 0u;
-                    idb = idb < (uint32_t)A ? idb : 0u;
-                    uint32_t rw[4];
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) {
-                        // record word of field f: 0 pos, 1 goal, 2.. history pairs, greedy
-                        const int f = (int)((field_pack >> (8 * j)) & 0xFFu);
-                        const uint32_t o = slot_of(j) == slot_a ? ida : idb;
-                        rw[j] = s_rec[o * kRecWords + (f < 2 ? 0 : (f < 4 ? 1 : 2 + ((f - 4) >> 1)))];
-                    }
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) {
-                        const int f = (int)((field_pack >> (8 * j)) & 0xFFu);
-                        const int shift = f < 4 ? 16 * (f & 1) : 16 * ((f - 4) & 1);
-                        const int v16 = (int)((rw[j] >> shift) & 0xFFFFu);
-                        const int coord = coord_token(v16 - ((f & 1) ? ey : ex));
-                        const int hist = v16 == 5 ? kTokEmptyAction : kTokWait + v16;
-                        const int val = f < 4 ? coord : (f < 9 ? hist : kTokGreedy + v16);
-                        tok[j] = ((agent_mask >> j) & 1u) && slot_of(j) < nsel ? val : tok[j];
-                    }
-                    wave_sync();  // slot reads done before the next ego's writes
+                // the selected ids move through the wave's slot array
+                if (id0 != kNoAgent && r0 < kVisible) my_slots[r0] = id0;
+                if (has_q1 && id1 != kNoAgent && r1 < kVisible) my_slots[r1] = id1;
+                // cost tokens
+                const int cml = (int)center - kCostLimit;
+                my_row[q0] = cost_token_flat(v0, cml);
+                if (has_q1) my_row[q1] = cost_token_flat(v1, cml);
+                wave_sync();
+                // agent tokens; a slot at or past nsel is padding
+                if (lane < kCoordLanes) {
+                    const uint32_t o = my_slots[c_slot];
+                    const int v = (int)s_rec16[o * (2 * kRecWords) + c_field];
+                    const int t = coord_token(v - ((c_field & 1) ? ey : ex));
+                    my_row[c_pos] = c_slot < nsel ? t : kTokPad;
                 }
+                {
+                    const uint32_t o = my_slots[k_slot0];
+                    const int t = s_copy[o * kCopyTokens + k_tok0];
+                    my_row[k_pos0] = k_slot0 < nsel ? t : kTokPad;
+                }
+                if (lane + kWave < kCopyItems) {
+                    const uint32_t o = my_slots[k_slot1];
+                    const int t = s_copy[o * kCopyTokens + k_tok1];
+                    my_row[k_pos1] = k_slot1 < nsel ? t : kTokPad;
+                }
+                wave_sync();
+                out = reinterpret_cast<const v4i*>(my_row)[lane];
+                wave_sync();  // row and slot reads done before the next ego's writes
             }
             // streaming store: the row is not read again by this build
-            const v4i out = {tok[0], tok[1], tok[2], tok[3]};
             __builtin_nontemporal_store(
                 out, reinterpret_cast<v4i*>(b.tokens + ((size_t)env * A + e) * kContext) + lane);
         }
         lds_barrier();  // the chunk's windows are consumed
+        commit(nnext);
+        lds_barrier();  // the next chunk's windows are visible
     }
 }
 
