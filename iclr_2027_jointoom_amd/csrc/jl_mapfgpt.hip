@@ -255,34 +255,39 @@ __global__ __launch_bounds__(kWave* kWaves) void unpack_bfs_kernel(
 // tokens and the greedy token, :437-456) and a cell -> agent map live in LDS.
 // The map is dense (one int32 per cell of the map grown by a kRadius border
 // of empty cells, so a window probe needs no bounds test) while it fits, an
-// occupancy bitmap + hash beyond.  Phase 2 (chunks of kChunk egos): the
-// chunk's windows are gathered into LDS by every thread, cells outside the
-// map staged as unreachable; then each ego is one wavefront.  Visible agents:
-// lane l probes window cells l and l + 64 in the map; a candidate's rank
-// under the key (Manhattan distance, id) is the number of smaller keys,
-// counted by walking the ballot of candidates with uniform readlanes; ranks
-// 0..12 are the reference's sorted top 13 because keys are unique.  Every
-// token of the row is computed by exactly one lane (two cost tokens per lane,
-// one coordinate token on lanes 0..51, the six copied tokens of the 13 slots
-// on lanes 0..63 and 0..13) into the wavefront's LDS row, which is then
-// stored as 64 x 16-byte writes.
+// occupancy bitmap + hash beyond.
+// Phase 2 (each wavefront on its own, no workgroup barrier): a wavefront
+// produces its egos two at a time.  Lanes 0..32 load the 33 tile-row
+// segments of both egos' 11x11 windows (cells outside the map staged as
+// unreachable) for the next pair while the current pair is turned into
+// tokens.  Visible agents: lane l probes window cells l and l + 64 in the
+// map; a candidate's rank under the key (Manhattan distance, id) is the
+// number of smaller keys, counted by walking the ballot of candidates with
+// uniform readlanes; ranks 0..12 are the reference's sorted top 13 because
+// keys are unique.  Every token of the row is computed by exactly one lane
+// (two cost tokens per lane, one coordinate token on lanes 0..51, the six
+// copied tokens of the 13 slots on lanes 0..63 and 0..13) into the
+// wavefront's LDS row, which is then stored as 64 x 16-byte writes.
 // ---------------------------------------------------------------------------
-constexpr int kTokThreads = 512;
+constexpr int kTokThreads = 1024;
+constexpr int kTokWaves = kTokThreads / kWave;
+constexpr int kEgosPerBlock = 128;         // egos per workgroup: an env spans ceil(A / 128) workgroups
 constexpr int kDenseCellLimit = 16384;     // map cells up to which the agent map is dense
-constexpr int kChunk = 16;                 // egos whose windows share LDS at a time
 // A window is read as 11 rows x 3 tile columns of 16-byte tile-row segments
 // (8 cells each): the 11 columns of a row span 2 or 3 tile columns.
 constexpr int kSegPerEgo = kDiam * 3;
 constexpr int kRegionCols = 24;            // cells per region row (3 tile columns)
-constexpr int kGatherPerThread = (kChunk * kSegPerEgo + kTokThreads - 1) / kTokThreads;
 constexpr int kSlotStride = 16;            // per-wave top-13 slot array (words)
 constexpr int kRecWords = 2;               // per-agent record: position word, goal word
 constexpr int kCopyTokens = 6;             // per-agent tokens independent of the ego
 constexpr int kCoordLanes = kVisible * 4;  // lanes producing the 52 coordinate tokens
 constexpr int kCopyItems = kVisible * kCopyTokens;  // 78 copied tokens per row
-constexpr int kEgosPerBlock = 64;          // egos per workgroup: an env spans ceil(A / 64) workgroups
-constexpr int kEgosPerWave = kChunk / (kTokThreads / kWave);  // rows each wavefront stores per chunk
-static_assert(kEgosPerWave * (kTokThreads / kWave) == kChunk, "chunk must split evenly over waves");
+// per-wavefront LDS: two egos' windows, the token row, the slot array
+constexpr int kWinBytes = 2 * kSegPerEgo * 16;
+constexpr int kRowBytes = kContext * 4;
+constexpr int kWaveBytes = kWinBytes + kRowBytes + kSlotStride * 4;
+static_assert(kWinBytes % 16 == 0 && kWaveBytes % 16 == 0, "16-byte LDS alignment");
+static_assert(kSegPerEgo <= kWave, "one window segment per lane");
 static_assert(kCostTokens + kVisible * kAgentTokens <= kContext, "row layout");
 static_assert(kCopyItems > kWave && kCopyItems <= 2 * kWave, "copied tokens take one or two per lane");
 typedef int v4i __attribute__((ext_vector_type(4)));
@@ -290,9 +295,8 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 struct TokLayout {
     bool dense;
     int hash_slots;
-    int map_h;  // column count of the (bordered) dense map
-    size_t map_off, occ_off, keys_off, vals_off, pos_off, rec_off, copy_off, win_off, slot_off,
-        row_off, diag_off, total;
+    size_t map_off, occ_off, keys_off, vals_off, pos_off, rec_off, copy_off, wave_off, diag_off,
+        total;
 };
 
 __host__ __device__ inline size_t align16(size_t v) { return (v + 15) & ~(size_t)15; }
@@ -301,13 +305,12 @@ __host__ __device__ inline TokLayout tok_layout(int A, int W, int H) {
     TokLayout L;
     const size_t cells = (size_t)W * H;
     L.dense = cells <= (size_t)kDenseCellLimit;
-    L.map_h = H + 2 * kRadius;
     int s = 64;
     while (s < 2 * A) s <<= 1;
     L.hash_slots = L.dense ? 0 : s;
     size_t off = 0;
     L.map_off = off;
-    if (L.dense) off = align16(off + (size_t)(W + 2 * kRadius) * L.map_h * 4);
+    if (L.dense) off = align16(off + (size_t)(W + 2 * kRadius) * (H + 2 * kRadius) * 4);
     L.occ_off = off;
     if (!L.dense) off = align16(off + cells / 8);
     L.keys_off = off;
@@ -320,12 +323,8 @@ __host__ __device__ inline TokLayout tok_layout(int A, int W, int H) {
     off = align16(off + (size_t)A * kRecWords * 4);
     L.copy_off = off;
     off = align16(off + (size_t)A * kCopyTokens * 4);
-    L.win_off = off;
-    off = align16(off + (size_t)kChunk * kSegPerEgo * 16);
-    L.slot_off = off;
-    off = align16(off + (size_t)(kTokThreads / kWave) * kSlotStride * 4);
-    L.row_off = off;
-    off = align16(off + (size_t)(kTokThreads / kWave) * kContext * 4);
+    L.wave_off = off;
+    off = align16(off + (size_t)kTokWaves * kWaveBytes);
     L.diag_off = off;
     off = align16(off + 4 * 4);
     L.total = off;
@@ -354,7 +353,6 @@ __global__ __launch_bounds__(kTokThreads) void tokens_kernel(jl_mapfgpt_t b) {
     const int tid = threadIdx.x;
     const int lane = tid & (kWave - 1);
     const int wave = tid / kWave;
-    constexpr int nwaves = kTokThreads / kWave;
     const TokLayout L = tok_layout(A, W, H);
     constexpr int MH = H + 2 * kRadius;  // dense map columns
     uint32_t* s_map = reinterpret_cast<uint32_t*>(smem + L.map_off);
@@ -364,14 +362,13 @@ __global__ __launch_bounds__(kTokThreads) void tokens_kernel(jl_mapfgpt_t b) {
     uint32_t* s_pos = reinterpret_cast<uint32_t*>(smem + L.pos_off);
     uint32_t* s_rec = reinterpret_cast<uint32_t*>(smem + L.rec_off);    // kRecWords per agent
     int* s_copy = reinterpret_cast<int*>(smem + L.copy_off);            // kCopyTokens per agent
-    uint4* s_win = reinterpret_cast<uint4*>(smem + L.win_off);  // [kChunk][11 rows][3 segments]
-    uint32_t* s_slot = reinterpret_cast<uint32_t*>(smem + L.slot_off);
-    int* s_row = reinterpret_cast<int*>(smem + L.row_off);      // [nwaves][kContext]
     int* s_diag = reinterpret_cast<int*>(smem + L.diag_off);
+    uint8_t* my_lds = smem + L.wave_off + (size_t)wave * kWaveBytes;
+    uint4* my_win = reinterpret_cast<uint4*>(my_lds);                  // [2 egos][11 rows][3 segments]
+    int* my_row = reinterpret_cast<int*>(my_lds + kWinBytes);           // [kContext]
+    uint32_t* my_slots = reinterpret_cast<uint32_t*>(my_lds + kWinBytes + kRowBytes);
     const uint32_t hmask = (uint32_t)L.hash_slots - 1;
     const size_t cells = (size_t)W * H;
-    uint32_t* my_slots = s_slot + wave * kSlotStride;
-    int* my_row = s_row + wave * kContext;
 
     // ---- phase 1 -----------------------------------------------------------
     if (kDense) {
@@ -476,168 +473,149 @@ __global__ __launch_bounds__(kTokThreads) void tokens_kernel(jl_mapfgpt_t b) {
         return s_vals[hash_find(s_keys, hmask, cell)];
     };
 
-    // Window gather of a chunk.  Item p = tid + k * kTokThreads is segment
-    // p % 33 = (row i, tile column j) of the chunk's ego p / 33: cells
-    // (ex - 5 + i, 8 * (tyl + j) .. 8 * (tyl + j) + 7) with tyl = floor((ey - 5) / 8),
-    // one 16-byte load from the tiled field.  Rows and tile columns outside the
-    // map are clamped into it for the load and staged as unreachable, and a
-    // third tile column the window does not reach re-reads the second, so
+    // Window gather.  Lane l < 33 loads segment l = (row i, tile column j) of
+    // an ego's window: cells (ex - 5 + i, 8 * (tyl + j) .. 8 * (tyl + j) + 7)
+    // with tyl = floor((ey - 5) / 8), one 16-byte load from the tiled field.
+    // Rows and tile columns outside the map are clamped into it for the load
+    // and staged as unreachable, a third tile column the window does not
+    // reach re-reads the second, and lanes 33..63 repeat segments 0..30, so
     // every load is issued without a branch and touches only the window's
-    // lines.  Values stay in registers until `commit` writes them to LDS, after
-    // the previous chunk's tokens have been produced.  Offsets are 32-bit
-    // bytes from the env's first tiled field (the host checks that they fit).
+    // lines.  Offsets are 32-bit bytes from the env's first tiled field (the
+    // host checks that they fit).
     const size_t tcells = tiled_cells(W, H);
     const uint8_t* env_tiles =
         reinterpret_cast<const uint8_t*>(b.cost_tiles + (size_t)env * A * tcells);
     constexpr int TH = H / 8;
-    uint4 graw[kGatherPerThread];
-    bool gin[kGatherPerThread];
-    auto stage = [&](int c0, int nch) {
-#pragma unroll
-        for (int k = 0; k < kGatherPerThread; ++k) {
-            const int p = tid + k * kTokThreads;
-            const int el = p / kSegPerEgo, it = p - el * kSegPerEgo;
-            const int i = it / 3, j = it - (it / 3) * 3;
-            // items past the chunk repeat the chunk's first ego (lines already fetched)
-            const bool live = el < nch;
-            const uint32_t pos = s_pos[c0 + (live ? el : 0)];
-            const bool ok = pos != kNoAgent;
-            const int ex = ok ? (int)(pos & 0xFFFFu) : 0, ey = ok ? (int)(pos >> 16) : 0;
-            const int xr = ex - kRadius + i;
-            const int x = xr < 0 ? 0 : (xr >= W ? W - 1 : xr);
-            const int tyl = ((ey - kRadius + 64) >> 3) - 8;  // floor((ey - 5) / 8)
-            const int tr = tyl + ((j == 2 && (tyl + 2) * 8 > ey + kRadius) ? 1 : j);
-            const int tcol = tr < 0 ? 0 : (tr >= TH ? TH - 1 : tr);
-            gin[k] = xr == x && tr == tcol;
-            const uint32_t off =
-                ((uint32_t)(c0 + (live ? el : 0)) * (uint32_t)tcells +
-                 ((uint32_t)(x >> 3) * TH + (uint32_t)tcol) * 64u + (uint32_t)(x & 7) * 8u) * 2u;
-            graw[k] = *reinterpret_cast<const uint4*>(env_tiles + off);
-        }
-    };
-    auto commit = [&](int nch) {
-        // keep every use of the gathered values here, so that the loads stay
-        // in flight across the previous chunk's token work
-#pragma unroll
-        for (int k = 0; k < kGatherPerThread; ++k)
-            asm volatile("" : "+v"(graw[k].x), "+v"(graw[k].y), "+v"(graw[k].z), "+v"(graw[k].w));
-#pragma unroll
-        for (int k = 0; k < kGatherPerThread; ++k) {
-            const int p = tid + k * kTokThreads;
-            // per-component selects (a select of the whole vector becomes a
-            // select of stack addresses)
-            const uint32_t fill = gin[k] ? 0u : 0xFFFFFFFFu;
-            const uint4 v = make_uint4(graw[k].x | fill, graw[k].y | fill, graw[k].z | fill,
-                                       graw[k].w | fill);
-            if (p < nch * kSegPerEgo) s_win[p] = v;
-        }
+    const int g_seg = lane < kSegPerEgo ? lane : lane - kSegPerEgo;
+    const int g_i = g_seg / 3, g_j = g_seg - (g_seg / 3) * 3;
+    auto seg_load = [&](uint32_t pos, int e, uint32_t& fill) -> uint4 {
+        const bool ok = pos != kNoAgent;
+        const int ex = ok ? (int)(pos & 0xFFFFu) : 0, ey = ok ? (int)(pos >> 16) : 0;
+        const int tyl = ((ey - kRadius + 64) >> 3) - 8;  // floor((ey - 5) / 8)
+        const bool third = (tyl + 2) * 8 <= ey + kRadius;
+        const int xr = ex - kRadius + g_i;
+        const int x = xr < 0 ? 0 : (xr >= W ? W - 1 : xr);
+        const int tr = tyl + ((g_j == 2 && !third) ? 1 : g_j);
+        const int tcol = tr < 0 ? 0 : (tr >= TH ? TH - 1 : tr);
+        fill = (xr == x && tr == tcol) ? 0u : 0xFFFFFFFFu;
+        const uint32_t off = (uint32_t)e * (uint32_t)tcells * 2u +
+                             ((uint32_t)(x >> 3) * TH + (uint32_t)tcol) * 128u + (uint32_t)(x & 7) * 16u;
+        return *reinterpret_cast<const uint4*>(env_tiles + off);
     };
 
-    // ---- phase 2: chunks of kChunk egos, one wavefront per ego ---------------
-    // Vector-memory stores count in the same in-order counter as the gather
-    // loads.  Every wavefront therefore stores exactly kEgosPerWave rows per
-    // chunk (a slot past the chunk's end repeats the chunk's first ego: the
-    // same tokens into the same row) and the next chunk's windows are
-    // committed after those stores in straight-line code, so waiting for the
-    // loads does not wait for the stores.
-    const int nchunks = (e_end - e_begin + kChunk - 1) / kChunk;
-    {
-        const int n0 = (e_end - e_begin) < kChunk ? (e_end - e_begin) : kChunk;
-        stage(e_begin, n0);
-        commit(n0);
-    }
-    lds_barrier();
-    for (int q = 0; q < nchunks; ++q) {
-        const int c0 = e_begin + q * kChunk;
-        const int nch = (e_end - c0) < kChunk ? (e_end - c0) : kChunk;
-        // always staged (no branch around the loads, which would make the
-        // compiler wait for them early); after the last chunk every item is
-        // dead and repeats lines of this chunk
-        const int c1 = c0 + kChunk;
-        const bool more = q + 1 < nchunks;
-        const int nnext = more ? ((e_end - c1) < kChunk ? (e_end - c1) : kChunk) : 0;
-        stage(more ? c1 : c0, nnext);
-        // lane i holds the position of this wave's i-th ego of the chunk
-        const int el_lane = wave + (lane < kEgosPerWave ? lane : 0) * nwaves;
-        const uint32_t pos_mine = s_pos[c0 + (el_lane < nch ? el_lane : 0)];
-#pragma unroll
-        for (int i = 0; i < kEgosPerWave; ++i) {
-            const int el = (wave + i * nwaves) < nch ? (wave + i * nwaves) : 0;
-            const int e = c0 + el;
-            const uint32_t pos = (uint32_t)__builtin_amdgcn_readlane((int)pos_mine, i);
-            v4i out = {kTokPad, kTokPad, kTokPad, kTokPad};
-            if (pos != kNoAgent) {
-                const int ex = (int)(pos & 0xFFFFu), ey = (int)(pos >> 16);
-                // region row = dx + 5, column = ey + dy - 8 * tyl (see `stage`)
-                const uint16_t* win = reinterpret_cast<const uint16_t*>(s_win + el * kSegPerEgo) +
-                                      (ey - 8 * (((ey - kRadius + 64) >> 3) - 8) - kRadius);
-                const uint32_t center = win[kRadius * kRegionCols + kRadius];
-                const uint32_t v0 = win[win0];
-                const uint32_t v1 = win[win1];
-                uint32_t id0, id1;
-                if (kDense) {
-                    const uint32_t* mrow = s_map + (ex + kRadius) * MH + (ey + kRadius);
-                    id0 = mrow[map0];
-                    id1 = mrow[map1];
-                } else {
-                    id0 = agent_at_hash(ex + di0 - kRadius, ey + dj0 - kRadius);
-                    id1 = agent_at_hash(ex + di1 - kRadius, ey + dj1 - kRadius);
-                }
-                // candidates: (distance << 16 | id); an empty cell's key is all ones
-                const uint32_t key0 = qd0 | id0, key1 = qd1 | id1;
-                const uint64_t m0 = __ballot(id0 != kNoAgent);
-                const uint64_t m1 = __ballot(id1 != kNoAgent) & kQ1Lanes;
-                int r0 = 0, r1 = 0;
-                for (uint64_t m = m0; m; m &= m - 1) {
-                    const uint32_t k =
-                        (uint32_t)__builtin_amdgcn_readlane((int)key0, __ffsll((unsigned long long)m) - 1);
-                    r0 += k < key0;
-                    r1 += k < key1;
-                }
-                for (uint64_t m = m1; m; m &= m - 1) {
-                    const uint32_t k =
-                        (uint32_t)__builtin_amdgcn_readlane((int)key1, __ffsll((unsigned long long)m) - 1);
-                    r0 += k < key0;
-                    r1 += k < key1;
-                }
-                const int count = __popcll(m0) + __popcll(m1);
-                const int nsel = count < kVisible ? count : kVisible;
-                // the selected ids move through the wave's slot array
-                if (id0 != kNoAgent && r0 < kVisible) my_slots[r0] = id0;
-                if (has_q1 && id1 != kNoAgent && r1 < kVisible) my_slots[r1] = id1;
-                // cost tokens
-                const int cml = (int)center - kCostLimit;
-                my_row[q0] = cost_token_flat(v0, cml);
-                if (has_q1) my_row[q1] = cost_token_flat(v1, cml);
-                wave_sync();
-                // agent tokens; a slot at or past nsel is padding
-                if (lane < kCoordLanes) {
-                    const uint32_t o = my_slots[c_slot];
-                    const int v = (int)s_rec16[o * (2 * kRecWords) + c_field];
-                    const int t = coord_token(v - ((c_field & 1) ? ey : ex));
-                    my_row[c_pos] = c_slot < nsel ? t : kTokPad;
-                }
-                {
-                    const uint32_t o = my_slots[k_slot0];
-                    const int t = s_copy[o * kCopyTokens + k_tok0];
-                    my_row[k_pos0] = k_slot0 < nsel ? t : kTokPad;
-                }
-                if (lane + kWave < kCopyItems) {
-                    const uint32_t o = my_slots[k_slot1];
-                    const int t = s_copy[o * kCopyTokens + k_tok1];
-                    my_row[k_pos1] = k_slot1 < nsel ? t : kTokPad;
-                }
-                wave_sync();
-                out = reinterpret_cast<const v4i*>(my_row)[lane];
-                wave_sync();  // row and slot reads done before the next ego's writes
+    // One ego's row: tokens into my_row, then the 16-byte store.
+    auto produce = [&](uint32_t pos, int e, const uint16_t* win_base) {
+        v4i out = {kTokPad, kTokPad, kTokPad, kTokPad};
+        if (pos != kNoAgent) {
+            const int ex = (int)(pos & 0xFFFFu), ey = (int)(pos >> 16);
+            // region row = dx + 5, column = ey + dy - 8 * tyl (see seg_load)
+            const uint16_t* win = win_base + (ey - 8 * (((ey - kRadius + 64) >> 3) - 8) - kRadius);
+            const uint32_t center = win[kRadius * kRegionCols + kRadius];
+            const uint32_t v0 = win[win0];
+            const uint32_t v1 = win[win1];
+            uint32_t id0, id1;
+            if (kDense) {
+                const uint32_t* mrow = s_map + (ex + kRadius) * MH + (ey + kRadius);
+                id0 = mrow[map0];
+                id1 = mrow[map1];
+            } else {
+                id0 = agent_at_hash(ex + di0 - kRadius, ey + dj0 - kRadius);
+                id1 = agent_at_hash(ex + di1 - kRadius, ey + dj1 - kRadius);
             }
-            // streaming store: the row is not read again by this build
-            __builtin_nontemporal_store(
-                out, reinterpret_cast<v4i*>(b.tokens + ((size_t)env * A + e) * kContext) + lane);
+            // candidates: (distance << 16 | id); an empty cell's key is all ones
+            const uint32_t key0 = qd0 | id0, key1 = qd1 | id1;
+            const uint64_t m0 = __ballot(id0 != kNoAgent);
+            const uint64_t m1 = __ballot(id1 != kNoAgent) & kQ1Lanes;
+            int r0 = 0, r1 = 0;
+            for (uint64_t m = m0; m; m &= m - 1) {
+                const uint32_t k =
+                    (uint32_t)__builtin_amdgcn_readlane((int)key0, __ffsll((unsigned long long)m) - 1);
+                r0 += k < key0;
+                r1 += k < key1;
+            }
+            for (uint64_t m = m1; m; m &= m - 1) {
+                const uint32_t k =
+                    (uint32_t)__builtin_amdgcn_readlane((int)key1, __ffsll((unsigned long long)m) - 1);
+                r0 += k < key0;
+                r1 += k < key1;
+            }
+            const int count = __popcll(m0) + __popcll(m1);
+            const int nsel = count < kVisible ? count : kVisible;
+            // the selected ids move through the wave's slot array
+            if (id0 != kNoAgent && r0 < kVisible) my_slots[r0] = id0;
+            if (has_q1 && id1 != kNoAgent && r1 < kVisible) my_slots[r1] = id1;
+            // cost tokens
+            const int cml = (int)center - kCostLimit;
+            my_row[q0] = cost_token_flat(v0, cml);
+            if (has_q1) my_row[q1] = cost_token_flat(v1, cml);
+            wave_sync();
+            // agent tokens; a slot at or past nsel is padding
+            if (lane < kCoordLanes) {
+                const uint32_t o = my_slots[c_slot];
+                const int v = (int)s_rec16[o * (2 * kRecWords) + c_field];
+                const int t = coord_token(v - ((c_field & 1) ? ey : ex));
+                my_row[c_pos] = c_slot < nsel ? t : kTokPad;
+            }
+            {
+                const uint32_t o = my_slots[k_slot0];
+                const int t = s_copy[o * kCopyTokens + k_tok0];
+                my_row[k_pos0] = k_slot0 < nsel ? t : kTokPad;
+            }
+            if (lane + kWave < kCopyItems) {
+                const uint32_t o = my_slots[k_slot1];
+                const int t = s_copy[o * kCopyTokens + k_tok1];
+                my_row[k_pos1] = k_slot1 < nsel ? t : kTokPad;
+            }
+            wave_sync();
+            out = reinterpret_cast<const v4i*>(my_row)[lane];
+            wave_sync();  // row and slot reads done before the next ego's writes
         }
-        lds_barrier();  // the chunk's windows are consumed
-        commit(nnext);
-        lds_barrier();  // the next chunk's windows are visible
+        // streaming store: the row is not read again by this build
+        __builtin_nontemporal_store(
+            out, reinterpret_cast<v4i*>(b.tokens + ((size_t)env * A + e) * kContext) + lane);
+    };
+
+    // ---- phase 2: pairs of egos, pair p on wavefront p % kTokWaves ----------
+    // Vector-memory stores count in the same in-order counter as the window
+    // loads.  Every step stores exactly two rows (an odd slice's last pair
+    // repeats its ego: the same tokens into the same row) and commits the
+    // next pair's windows after those stores in straight-line code, so
+    // waiting for the loads does not wait for the stores.
+    const int npairs = (e_end - e_begin + 1) >> 1;
+    if (wave >= npairs) return;
+    const uint16_t* win_a = reinterpret_cast<const uint16_t*>(my_win);
+    const uint16_t* win_b = reinterpret_cast<const uint16_t*>(my_win + kSegPerEgo);
+    auto ego_a = [&](int p) { return e_begin + 2 * p; };
+    auto ego_b = [&](int p) { return (e_begin + 2 * p + 1) < e_end ? e_begin + 2 * p + 1 : e_begin + 2 * p; };
+    auto uniform_pos = [&](int e) { return (uint32_t)__builtin_amdgcn_readfirstlane((int)s_pos[e]); };
+    uint4 ga, gb;
+    uint32_t fa, fb;
+    auto stage = [&](int p) {
+        ga = seg_load(uniform_pos(ego_a(p)), ego_a(p), fa);
+        gb = seg_load(uniform_pos(ego_b(p)), ego_b(p), fb);
+    };
+    auto commit = [&]() {
+        // every use of the loaded values stays here, so that the loads stay
+        // in flight across the current pair's token work
+        asm volatile("" : "+v"(ga.x), "+v"(ga.y), "+v"(ga.z), "+v"(ga.w));
+        asm volatile("" : "+v"(gb.x), "+v"(gb.y), "+v"(gb.z), "+v"(gb.w));
+        if (lane < kSegPerEgo) {
+            my_win[lane] = make_uint4(ga.x | fa, ga.y | fa, ga.z | fa, ga.w | fa);
+            my_win[kSegPerEgo + lane] = make_uint4(gb.x | fb, gb.y | fb, gb.z | fb, gb.w | fb);
+        }
+        wave_sync();
+    };
+    stage(wave);
+    commit();
+    for (int p = wave; p < npairs; p += kTokWaves) {
+        const int pn = p + kTokWaves;
+        const uint32_t pos_a = uniform_pos(ego_a(p)), pos_b = uniform_pos(ego_b(p));
+        // always staged (no branch around the loads, which would make the
+        // compiler wait for them early); after the last pair it repeats this one
+        stage(pn < npairs ? pn : p);
+        produce(pos_a, ego_a(p), win_a);
+        produce(pos_b, ego_b(p), win_b);
+        commit();
     }
 }
 
