@@ -73,13 +73,20 @@ __device__ __forceinline__ void store_state_row(uint16_t* dst, uint32_t env, uin
 // Greedy-move mask of one agent (mapf_gpt_cuda.cu:459-480): bit (3 - dir)
 // is set when the neighbour in direction dir, order (-1,0), (+1,0), (0,-1),
 // (0,+1), is reachable and strictly closer to the goal than the agent's cell.
+// The five reads are issued unconditionally (a neighbour off the map reads a
+// clamped cell and is then taken as unreachable), so a field in HBM costs one
+// round trip, not one per branch.
 template <int H, typename Field>
 __device__ __forceinline__ uint32_t greedy_mask(Field f, int x, int y, int W) {
     const uint32_t c0 = f(x, y);
-    const uint32_t n0 = x > 0 ? f(x - 1, y) : kUnreachable;
-    const uint32_t n1 = x + 1 < W ? f(x + 1, y) : kUnreachable;
-    const uint32_t n2 = y > 0 ? f(x, y - 1) : kUnreachable;
-    const uint32_t n3 = y + 1 < H ? f(x, y + 1) : kUnreachable;
+    const uint32_t r0 = f(x > 0 ? x - 1 : x, y);
+    const uint32_t r1 = f(x + 1 < W ? x + 1 : x, y);
+    const uint32_t r2 = f(x, y > 0 ? y - 1 : y);
+    const uint32_t r3 = f(x, y + 1 < H ? y + 1 : y);
+    const uint32_t n0 = x > 0 ? r0 : kUnreachable;
+    const uint32_t n1 = x + 1 < W ? r1 : kUnreachable;
+    const uint32_t n2 = y > 0 ? r2 : kUnreachable;
+    const uint32_t n3 = y + 1 < H ? r3 : kUnreachable;
     uint32_t m = 0;
     if (n0 != kUnreachable && c0 > n0) m |= 8u;
     if (n1 != kUnreachable && c0 > n1) m |= 4u;
@@ -619,17 +626,38 @@ __global__ __launch_bounds__(kTokThreads) void tokens_kernel(jl_mapfgpt_t b) {
     }
 }
 
-__global__ void append_actions_kernel(jl_mapfgpt_t b, const uint8_t* __restrict__ actions) {
+// History roll (mapf_gpt_append_actions_kernel, mapf_gpt_cuda.cu:155-178): one
+// thread per agent, 256 agents per workgroup.  The workgroup's 2560-byte
+// history segment moves between HBM and LDS as 16-byte words (element-wise
+// for a partial or unaligned last segment).
+constexpr int kAppendThreads = 256;
+constexpr int kAppendWords = kAppendThreads * 5 * 2 / 16;
+
+__global__ __launch_bounds__(kAppendThreads) void append_actions_kernel(
+    jl_mapfgpt_t b, const uint8_t* __restrict__ actions) {
+    __shared__ uint4 s_hist[kAppendWords];
+    uint16_t* sh = reinterpret_cast<uint16_t*>(s_hist);
     const int N = b.n_envs * b.n_agents;
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    const int base = blockIdx.x * kAppendThreads;
+    const int n = (N - base) < kAppendThreads ? (N - base) : kAppendThreads;
+    const int tid = threadIdx.x;
+    uint16_t* seg = b.histories + (size_t)base * 5;
+    const bool vec = n == kAppendThreads && (reinterpret_cast<uintptr_t>(seg) & 15u) == 0;
+    if (vec) {
+        if (tid < kAppendWords) s_hist[tid] = reinterpret_cast<const uint4*>(seg)[tid];
+    } else {
+        for (int k = tid; k < n * 5; k += kAppendThreads) sh[k] = seg[k];
+    }
+    __syncthreads();
     bool bad = false;
-    if (i < N) {
+    if (tid < n) {
+        const int i = base + tid;
         uint16_t a = b.active_mask[i] ? (uint16_t)actions[i] : (uint16_t)0;
         if (a >= 5) {
             bad = true;
             a = 0;
         }
-        uint16_t* h = b.histories + (size_t)i * 5;
+        uint16_t* h = sh + tid * 5;
         const uint16_t h1 = h[1], h2 = h[2], h3 = h[3], h4 = h[4];
         h[0] = h1;
         h[1] = h2;
@@ -637,8 +665,14 @@ __global__ void append_actions_kernel(jl_mapfgpt_t b, const uint8_t* __restrict_
         h[3] = h4;
         h[4] = a;
     }
+    __syncthreads();
+    if (vec) {
+        if (tid < kAppendWords) reinterpret_cast<uint4*>(seg)[tid] = s_hist[tid];
+    } else {
+        for (int k = tid; k < n * 5; k += kAppendThreads) seg[k] = sh[k];
+    }
     const uint64_t m = __ballot(bad);
-    if ((threadIdx.x & (kWave - 1)) == 0 && m) atomicAdd(b.diagnostics + 1, (int)__popcll(m));
+    if ((tid & (kWave - 1)) == 0 && m) atomicAdd(b.diagnostics + 1, (int)__popcll(m));
 }
 
 __global__ void fill_u16_kernel(uint16_t* p, size_t n, uint16_t v) {
@@ -768,8 +802,8 @@ extern "C" int jl_mapfgpt_append_actions(const jl_mapfgpt_t* b, const uint8_t* a
     if (rc) return rc;
     if (!actions) return JL_ERR_ARG;
     const int N = b->n_envs * b->n_agents;
-    hipLaunchKernelGGL(append_actions_kernel, dim3((N + 255) / 256), dim3(256), 0,
-                       (hipStream_t)stream, *b, actions);
+    hipLaunchKernelGGL(append_actions_kernel, dim3((N + kAppendThreads - 1) / kAppendThreads),
+                       dim3(kAppendThreads), 0, (hipStream_t)stream, *b, actions);
     return launch_status();
 }
 

@@ -3,15 +3,16 @@
 // step: one workgroup per env.  The reference resolves conflicts with an
 // O(A^2) pair scan per Jacobi round and three barriers per round
 // (128_agents_map_step.cu:91-169).  Here every cell an agent can occupy or
-// enter this step (its current cell and its proposal) is inserted once into
-// an LDS open-addressing hash, so a round is O(1) per agent: the only agents
-// that can reject mover i are the current occupant of i's destination and
-// the smallest id proposing it (the event-indexed form of
-// transition_adapters.py:392-449).  The smallest proposer per cell and round
-// is found with one LDS atomicMax of (round << 16 | ~id), so no table reset
-// is needed between rounds: two barriers per round.  Rejections are never
-// undone and the round structure is the reference's, so positions are
-// identical.  The table holds at most 2A keys, independent of the map size.
+// enter this step (its current cell and its proposal) gets one slot in LDS
+// tables, so a round is O(1) per agent: the only agents that can reject mover
+// i are the current occupant of i's destination and the smallest id
+// proposing it (the event-indexed form of transition_adapters.py:392-449).
+// Maps of up to 4096 cells index the tables by cell; larger ones insert the
+// cells into an open-addressing hash (at most 2A keys, independent of the map
+// size).  The smallest proposer per cell and round is found with one LDS
+// atomicMax of (round << 16 | ~id), so no table reset is needed between
+// rounds: two barriers per round.  Rejections are never undone and the round
+// structure is the reference's, so positions are identical.
 #include "jl_common.h"
 
 namespace jl {
@@ -35,40 +36,61 @@ __device__ __forceinline__ uint32_t hinsert(uint32_t* keys, uint32_t mask, uint3
 
 struct StepLayout {
     int slots;
-    size_t keys_off, owner_off, tag_off, ocp_off, cur_off, prop_off, sc_off, sp_off, mv_off, cat_off,
-        total;
+    size_t keys_off, owner_off, tag_off, ocp_off, bits_off, cur_off, prop_off, goal_off, sc_off,
+        sp_off, flag_off, mv_off, cat_off, any_off, total;
 };
 
 __host__ __device__ inline size_t a16(size_t v) { return (v + 15) & ~(size_t)15; }
 
+// Maps of at most kDenseStepCells cells index the owner and round-tag tables
+// by cell directly; larger maps go through the LDS hash.
+constexpr int kDenseStepCells = 4096;
+
+__host__ __device__ inline bool step_dense(int W, int H) { return W * H <= kDenseStepCells; }
+
 __host__ __device__ inline StepLayout step_layout(int A, int W, int H) {
     StepLayout L;
+    const bool dense = step_dense(W, H);
     int s = 64;
     while (s < 4 * A) s <<= 1;  // load factor <= 1/2 for the <= 2A distinct cells
-    L.slots = s;
+    L.slots = dense ? W * H : s;
     size_t o = 0;
     L.keys_off = o;
-    o = a16(o + (size_t)s * 4);
+    o = a16(o + (dense ? 0 : (size_t)s * 4));
     L.owner_off = o;
-    o = a16(o + (size_t)s * 4);
+    o = a16(o + (size_t)L.slots * 4);
     L.tag_off = o;
-    o = a16(o + (size_t)s * 4);
+    o = a16(o + (size_t)L.slots * 4);
     L.ocp_off = o;
     o = a16(o + (size_t)W * H / 8);
-    L.cur_off = o;
-    o = a16(o + (size_t)A * 4);
+    L.bits_off = o;  // + one spare 16-byte word (the load pass's sink)
+    o = a16(o + (size_t)W * H / 8 + 16);
+    L.cur_off = o;  // cur, goal and flag have a spare entry [A]
+    o = a16(o + (size_t)(A + 1) * 4);
     L.prop_off = o;
     o = a16(o + (size_t)A * 4);
+    L.goal_off = o;
+    o = a16(o + (size_t)(A + 1) * 4);
     L.sc_off = o;
     o = a16(o + (size_t)A * 2);
     L.sp_off = o;
     o = a16(o + (size_t)A * 2);
+    L.flag_off = o;
+    o = a16(o + (size_t)(A + 1) * 2);
     L.mv_off = o;
     o = a16(o + (size_t)A * 2);
     L.cat_off = o;
     o = a16(o + (size_t)A);
+    L.any_off = o;
+    o = a16(o + 3 * 4);
     L.total = o;
     return L;
+}
+
+// Workgroup size of a step: whole wavefronts covering the agents, at most
+// kStepThreads.
+inline int step_threads(int A) {
+    return A >= kStepThreads ? kStepThreads : (A + kWave - 1) / kWave * kWave;
 }
 
 __device__ __forceinline__ void store_row(uint16_t* dst, uint32_t env, uint32_t agent,
@@ -92,156 +114,304 @@ __device__ __forceinline__ uint64_t rng_next(uint64_t* state) {
     return x * 0x2545F4914F6CDD1Dull;
 }
 
-template <int H, bool kStandard>
+// s_flag: the action as given (low byte) and the arrival latch.
+constexpr uint16_t kFlagArrived = 0x100;
+// Agents (and bitmap words) a thread holds in registers: 1 up to
+// kStepThreads agents, else 4; agents past 4 * kStepThreads go through LDS.
+inline int step_per(int A) { return A <= kStepThreads ? 1 : 4; }
+
+// Everything the step reads from HBM is requested at its start (the env's
+// obstacle bitmap and each agent's position, goal, action and arrival latch
+// into LDS, the done flags and the step count into registers), so a step
+// costs one memory round trip and the Jacobi rounds run in LDS.
+template <int H, bool kStandard, bool kDense, int kStepPer>
 __global__ __launch_bounds__(kStepThreads) void step_kernel(jl_sim_t s) {
     extern __shared__ __align__(16) uint8_t smem[];
     const int env = blockIdx.x;
     const int A = s.n_agents, W = s.map_w;
-    const int tid = threadIdx.x;
+    const int tid = threadIdx.x, nt = blockDim.x;
     const size_t base = (size_t)env * A;
-    if (kStandard && (s.terminated[env] != 0 || s.truncated[env] != 0)) {
-        // done envs do not advance (128_agents_map_step.cu:31-34)
-        if (s.outcomes)
-            for (int a = tid; a < A; a += kStepThreads) s.outcomes[base + a] = 0;
-        return;
-    }
     const StepLayout L = step_layout(A, W, H);
     uint32_t* keys = reinterpret_cast<uint32_t*>(smem + L.keys_off);
     uint32_t* owner = reinterpret_cast<uint32_t*>(smem + L.owner_off);
     uint32_t* tag = reinterpret_cast<uint32_t*>(smem + L.tag_off);
     uint32_t* ocp = reinterpret_cast<uint32_t*>(smem + L.ocp_off);
+    uint32_t* s_bits = reinterpret_cast<uint32_t*>(smem + L.bits_off);
     uint32_t* s_cur = reinterpret_cast<uint32_t*>(smem + L.cur_off);
     uint32_t* s_prop = reinterpret_cast<uint32_t*>(smem + L.prop_off);
+    uint32_t* s_goal = reinterpret_cast<uint32_t*>(smem + L.goal_off);
     uint16_t* s_sc = reinterpret_cast<uint16_t*>(smem + L.sc_off);
     uint16_t* s_sp = reinterpret_cast<uint16_t*>(smem + L.sp_off);
+    uint16_t* s_flag = reinterpret_cast<uint16_t*>(smem + L.flag_off);
     uint8_t* s_mv = smem + L.mv_off;  // [2][A] moving flags, ping-pong by round
     uint8_t* s_cat = smem + L.cat_off;
+    uint32_t* s_any = reinterpret_cast<uint32_t*>(smem + L.any_off);  // [3] rotating round flags
     const uint32_t mask = (uint32_t)L.slots - 1;
     const int words = W * H / 32;
-    const uint32_t* env_bits = s.grid_bits + (size_t)env * words;
+    // every env's bitmap starts 16-byte aligned when its word count is a multiple of 4
+    const bool vec_words = (words & 3) == 0;
 
-    for (int k = tid; k < L.slots; k += kStepThreads) {
-        keys[k] = kEmpty;
-        owner[k] = 0;
-        tag[k] = 0;
+    // First pass: every load is issued (at clamped indices, without a
+    // branch) before the first LDS store, so they share one round trip.
+    const uint8_t term = kStandard ? s.terminated[env] : 0;
+    const uint8_t trunc = kStandard ? s.truncated[env] : 0;
+    const int steps = kStandard ? s.step_counts[env] : 0;
+    const uint4* bits4 = reinterpret_cast<const uint4*>(s.grid_bits + (size_t)env * words);
+    const int nvec = vec_words ? words / 4 : 0;
+    uint4 rb[kStepPer];
+    uint32_t rc[kStepPer], rg[kStepPer], rf[kStepPer];
+#pragma unroll
+    for (int j = 0; j < kStepPer; ++j) {
+        const int k = tid + j * nt;
+        rb[j] = bits4[k < nvec ? k : 0];
     }
-    for (int k = tid; k < words; k += kStepThreads) ocp[k] = 0;
+#pragma unroll
+    for (int j = 0; j < kStepPer; ++j) {
+        const int a = tid + j * nt;
+        const size_t g = base + (a < A ? a : A - 1);
+        rc[j] = (uint32_t)s.cur_x[g] | ((uint32_t)s.cur_y[g] << 16);
+        rg[j] = (uint32_t)s.goal_x[g] | ((uint32_t)s.goal_y[g] << 16);
+        const bool arrived = kStandard && s.arrived[g] != 0;
+        rf[j] = (uint32_t)s.actions[g] | (arrived ? kFlagArrived : 0u);
+    }
+    // out-of-range items land in the spare slot past each array: no branch
+    // for the compiler to sink the loads into
+#pragma unroll
+    for (int j = 0; j < kStepPer; ++j) {
+        const int k = tid + j * nt;
+        reinterpret_cast<uint4*>(s_bits)[k < nvec ? k : nvec] = rb[j];
+    }
+#pragma unroll
+    for (int j = 0; j < kStepPer; ++j) {
+        const int a = tid + j * nt;
+        const int d = a < A ? a : A;
+        s_cur[d] = rc[j];
+        s_goal[d] = rg[j];
+        s_flag[d] = (uint16_t)rf[j];
+    }
+    // the rest: larger maps and agent counts, and bitmaps not 16-byte aligned
+    if (vec_words) {
+        for (int k = tid + kStepPer * nt; k < nvec; k += nt)
+            reinterpret_cast<uint4*>(s_bits)[k] = bits4[k];
+    } else {
+        const uint32_t* src = s.grid_bits + (size_t)env * words;
+        for (int k = tid; k < words; k += nt) s_bits[k] = src[k];
+    }
+    for (int a = tid + kStepPer * nt; a < A; a += nt) {
+        const size_t g = base + a;
+        s_cur[a] = (uint32_t)s.cur_x[g] | ((uint32_t)s.cur_y[g] << 16);
+        s_goal[a] = (uint32_t)s.goal_x[g] | ((uint32_t)s.goal_y[g] << 16);
+        const bool arrived = kStandard && s.arrived[g] != 0;
+        s_flag[a] = (uint16_t)(s.actions[g] | (arrived ? kFlagArrived : 0));
+    }
+    const bool done = (term | trunc) != 0;
+
+    // Tables.  Dense: only the entries of cells the agents stand on or may
+    // enter are read, so each agent clears those (its cell and, when in the
+    // map, its tentative destination) instead of the whole map.
+    auto target_of = [&](uint32_t cur, uint32_t f, int& tx, int& ty) __attribute__((always_inline)) {
+        int act = (int)(f & 0xFFu);
+        if (act > 4) act = 0;
+        tx = (int)(cur & 0xFFFFu) + (act == 1 ? -1 : (act == 2 ? 1 : 0));
+        ty = (int)(cur >> 16) + (act == 3 ? -1 : (act == 4 ? 1 : 0));
+    };
+    if (kDense) {
+        for (int a = tid; a < A; a += nt) {
+            const uint32_t cur = s_cur[a];
+            int tx, ty;
+            target_of(cur, s_flag[a], tx, ty);
+            const uint32_t cc = (cur & 0xFFFFu) * H + (cur >> 16);
+            owner[cc] = 0;
+            tag[cc] = 0;
+            if (tx >= 0 && tx < W && ty >= 0 && ty < H) {
+                owner[tx * H + ty] = 0;
+                tag[tx * H + ty] = 0;
+            }
+        }
+    } else {
+        for (int k = tid; k < L.slots; k += nt) {
+            keys[k] = kEmpty;
+            owner[k] = 0;
+            tag[k] = 0;
+        }
+    }
+    for (int k = tid; k < words; k += nt) ocp[k] = 0;
+    if (tid < 3) s_any[tid] = 0;
     __syncthreads();
+    if (done) {
+        // done envs do not advance (128_agents_map_step.cu:31-34)
+        if (s.outcomes)
+            for (int a = tid; a < A; a += nt) s.outcomes[base + a] = 0;
+        return;
+    }
 
     // Proposals (:54-82): arrived agents stay; walls and the map edge stay.
-    for (int a = tid; a < A; a += kStepThreads) {
-        const size_t g = base + a;
-        const int cx = s.cur_x[g], cy = s.cur_y[g];
-        int act = s.actions[g];
-        if (act > 4) act = 0;
-        const bool was_arrived = kStandard && s.arrived[g] != 0;
-        const int dx = act == 1 ? -1 : (act == 2 ? 1 : 0);
-        const int dy = act == 3 ? -1 : (act == 4 ? 1 : 0);
-        const int tx = cx + dx, ty = cy + dy;
-        bool move = !was_arrived && act != 0;
-        uint8_t cat = 0;
+    // Agents a = tid + j * nt, j < kStepPer, keep their own state in
+    // registers for the rounds; the moving flags and slots other agents read
+    // are also in LDS.
+    uint32_t r_sc[kStepPer], r_sp[kStepPer], r_cat[kStepPer];
+    bool r_mv[kStepPer];
+    auto propose = [&](int a, uint32_t& sc_out, uint32_t& sp_out, bool& mv_out,
+                       uint32_t& cat_out) __attribute__((always_inline)) {
+        const uint32_t cur = s_cur[a];
+        const uint32_t f = s_flag[a];
+        int tx, ty;
+        target_of(cur, f, tx, ty);
+        const bool was_arrived = (f & kFlagArrived) != 0;
+        bool move = !was_arrived && (tx != (int)(cur & 0xFFFFu) || ty != (int)(cur >> 16));
+        uint32_t cat = 0;
         if (move) {
-            const bool wall = tx < 0 || tx >= W || ty < 0 || ty >= H || bit_at(env_bits, tx * H + ty);
+            const bool wall = tx < 0 || tx >= W || ty < 0 || ty >= H || bit_at(s_bits, tx * H + ty);
             if (wall) {
                 move = false;
                 cat = JL_OUTCOME_WALL;
             }
         }
-        const uint32_t cur = (uint32_t)cx | ((uint32_t)cy << 16);
-        const uint32_t prop = move ? ((uint32_t)tx | ((uint32_t)ty << 16)) : cur;
-        s_cur[a] = cur;
-        s_prop[a] = prop;
-        s_cat[a] = cat;
+        s_prop[a] = move ? ((uint32_t)tx | ((uint32_t)ty << 16)) : cur;
         s_mv[a] = move ? 1 : 0;
-        const uint32_t sc = hinsert(keys, mask, (uint32_t)(cx * H + cy));
-        s_sc[a] = (uint16_t)sc;
+        // slot of a cell: the cell itself, or its hash entry
+        const uint32_t ccell = (cur & 0xFFFFu) * H + (cur >> 16), tcell = (uint32_t)(tx * H + ty);
+        const uint32_t sc = kDense ? ccell : hinsert(keys, mask, ccell);
         // a cell shared by several agents keeps the highest id as occupant,
         // as the CPU restatement's dict does (transition_adapters.py:389-392)
         atomicMax(&owner[sc], (uint32_t)a + 1);
-        s_sp[a] = move ? (uint16_t)hinsert(keys, mask, (uint32_t)(tx * H + ty)) : (uint16_t)sc;
+        const uint32_t sp = move ? (kDense ? tcell : hinsert(keys, mask, tcell)) : sc;
+        s_sc[a] = (uint16_t)sc;
+        s_sp[a] = (uint16_t)sp;
+        sc_out = sc;
+        sp_out = sp;
+        mv_out = move;
+        cat_out = cat;
+    };
+#pragma unroll
+    for (int j = 0; j < kStepPer; ++j) {
+        const int a = tid + j * nt;
+        r_mv[j] = false;
+        r_sc[j] = r_sp[j] = r_cat[j] = 0;
+        if (a < A) propose(a, r_sc[j], r_sp[j], r_mv[j], r_cat[j]);
+    }
+    for (int a = tid + kStepPer * nt; a < A; a += nt) {
+        uint32_t sc, sp, cat;
+        bool mv;
+        propose(a, sc, sp, mv, cat);
+        s_cat[a] = (uint8_t)cat;
     }
     __syncthreads();
 
-    // Jacobi rounds (:91-169).
+    // Jacobi rounds (:91-169).  Mover a is rejected by the occupant o of its
+    // destination d (swap if o moves into a's cell; vertex if o stays and
+    // a > o, else chain) or by the smallest id proposing d this round
+    // (vertex if smaller than a); the earlier of the two in id order gives
+    // the category.
+    auto decide = [&](int a, bool mv_a, uint32_t sc_a, uint32_t sp_a,
+                      const uint8_t* mv) __attribute__((always_inline)) -> uint32_t {
+        const uint32_t own = owner[sp_a], tg = tag[sp_a];
+        const int o = (int)own - 1;
+        const int oc = o >= 0 ? o : 0;
+        const bool mv_o = mv[oc] != 0;
+        const uint32_t sp_o = s_sp[oc];
+        const int mid = (int)(0xFFFFu - (tg & 0xFFFFu));
+        int cat_o = 0;
+        if (o >= 0) cat_o = mv_o ? (sp_o == sc_a ? JL_OUTCOME_SWAP : 0)
+                                 : (a > o ? JL_OUTCOME_VERTEX : JL_OUTCOME_CHAIN);
+        const int cat_m = (mid < a && mid != o) ? JL_OUTCOME_VERTEX : 0;
+        const int c = (cat_o && cat_m) ? (o < mid ? cat_o : cat_m) : (cat_o ? cat_o : cat_m);
+        return mv_a ? (uint32_t)c : 0u;
+    };
     int cur = 0;
     for (int iter = 0; iter < A; ++iter) {
         const uint8_t* mv = s_mv + cur * A;
         uint8_t* mv_next = s_mv + (cur ^ 1) * A;
         const uint32_t stamp = (uint32_t)(iter + 1) << 16;
-        for (int a = tid; a < A; a += kStepThreads) {
+        // the flag of the next round: its previous readers have all passed
+        // the first barrier of the round before this one
+        if (tid == 0) s_any[(iter + 1) % 3] = 0;
+#pragma unroll
+        for (int j = 0; j < kStepPer; ++j) {
+            const int a = tid + j * nt;
+            if (a < A) atomicMax(&tag[r_mv[j] ? r_sp[j] : r_sc[j]], stamp | (0xFFFFu - (uint32_t)a));
+        }
+        for (int a = tid + kStepPer * nt; a < A; a += nt) {
             const uint32_t slot = mv[a] ? s_sp[a] : s_sc[a];
             atomicMax(&tag[slot], stamp | (0xFFFFu - (uint32_t)a));
         }
         __syncthreads();
-        int rejected = 0;
-        for (int a = tid; a < A; a += kStepThreads) {
-            uint8_t m = mv[a];
-            if (m) {
-                const uint32_t d = s_sp[a];
-                const int o = (int)owner[d] - 1;
-                const int mid = (int)(0xFFFFu - (tag[d] & 0xFFFFu));
-                int cat_o = 0;
-                if (o >= 0) {
-                    if (mv[o]) {
-                        if (s_sp[o] == s_sc[a]) cat_o = JL_OUTCOME_SWAP;
-                    } else {
-                        cat_o = a > o ? JL_OUTCOME_VERTEX : JL_OUTCOME_CHAIN;
-                    }
-                }
-                const int cat_m = (mid < a && mid != o) ? JL_OUTCOME_VERTEX : 0;
-                int c;
-                if (cat_o && cat_m) {
-                    c = o < mid ? cat_o : cat_m;
-                } else {
-                    c = cat_o ? cat_o : cat_m;
-                }
+        bool rejected = false;
+#pragma unroll
+        for (int j = 0; j < kStepPer; ++j) {
+            const int a = tid + j * nt;
+            if (a < A) {
+                const uint32_t c = decide(a, r_mv[j], r_sc[j], r_sp[j], mv);
                 if (c) {
-                    m = 0;
-                    if (s_cat[a] == 0) s_cat[a] = (uint8_t)c;
-                    rejected = 1;
+                    r_mv[j] = false;
+                    r_cat[j] = r_cat[j] ? r_cat[j] : c;
+                    rejected = true;
                 }
+                mv_next[a] = r_mv[j] ? 1 : 0;
             }
-            mv_next[a] = m;
         }
-        const int any = __syncthreads_or(rejected);
+        for (int a = tid + kStepPer * nt; a < A; a += nt) {
+            const bool m = mv[a] != 0;
+            const uint32_t c = decide(a, m, s_sc[a], s_sp[a], mv);
+            if (c) {
+                if (s_cat[a] == 0) s_cat[a] = (uint8_t)c;
+                rejected = true;
+            }
+            mv_next[a] = (m && !c) ? 1 : 0;
+        }
+        if (rejected) s_any[iter % 3] = 1;
+        __syncthreads();
+        const bool any = s_any[iter % 3] != 0;
         cur ^= 1;
         if (!any) break;
     }
     const uint8_t* mv = s_mv + cur * A;
+#pragma unroll
+    for (int j = 0; j < kStepPer; ++j) {
+        const int a = tid + j * nt;
+        if (a < A) s_cat[a] = (uint8_t)r_cat[j];
+    }
 
     // Outputs (:171-217): positions, rewards, occupancy, arrival latch.
     int all_arrived = 1;
-    for (int a = tid; a < A; a += kStepThreads) {
+    for (int a = tid; a < A; a += nt) {
         const size_t g = base + a;
         const uint32_t fin = mv[a] ? s_prop[a] : s_cur[a];
         const uint32_t fx = fin & 0xFFFFu, fy = fin >> 16;
         s.cur_x[g] = (uint16_t)fx;
         s.cur_y[g] = (uint16_t)fy;
-        const uint32_t gx = s.goal_x[g], gy = s.goal_y[g];
-        const bool on_goal = fx == gx && fy == gy;
+        const uint32_t goal = s_goal[a];
+        const bool on_goal = fin == goal;
         s.rewards[g] = on_goal ? 1.0f : 0.0f;
         s.goal_changed[g] = 0;
         const uint32_t cell = fx * H + fy;
         atomicOr(&ocp[cell >> 5], 1u << (cell & 31));
         if (s.outcomes) s.outcomes[g] = s_cat[a];
         if (kStandard) {
-            const uint8_t was = s.arrived[g];
-            const uint8_t now = (was != 0 || on_goal) ? 1 : 0;
-            if (now != was) s.arrived[g] = now;
+            const uint32_t f = s_flag[a];
+            const bool was = (f & kFlagArrived) != 0;
+            const bool now = was || on_goal;
+            if (now != was) s.arrived[g] = 1;
             if (!now) all_arrived = 0;
             // packed state: arrived agents report the stay action (:257-259)
-            const uint32_t action = was ? 0u : (uint32_t)s.actions[g];
-            store_row(s.state_packed + g * 8, env, a, fin, gx, gy, action, 0);
+            store_row(s.state_packed + g * 8, env, a, fin, goal & 0xFFFFu, goal >> 16,
+                      was ? 0u : (f & 0xFFu), 0);
         }
         s_cur[a] = fin;  // keep the final cell for the lifelong pass
     }
     all_arrived = __syncthreads_and(all_arrived);
-    uint32_t* gocp = s.grid_ocp + (size_t)env * words;
-    for (int k = tid; k < words; k += kStepThreads) gocp[k] = ocp[k];
+    if (vec_words) {
+        uint4* gocp = reinterpret_cast<uint4*>(s.grid_ocp + (size_t)env * words);
+        const uint4* src = reinterpret_cast<const uint4*>(ocp);
+        for (int k = tid; k < words / 4; k += nt) gocp[k] = src[k];
+    } else {
+        uint32_t* gocp = s.grid_ocp + (size_t)env * words;
+        for (int k = tid; k < words; k += nt) gocp[k] = ocp[k];
+    }
 
     if (kStandard) {
         if (tid == 0) {
-            const int next = s.step_counts[env] + 1;
+            const int next = steps + 1;
             s.step_counts[env] = next;
             if (all_arrived) {
                 s.terminated[env] = 1;
@@ -259,14 +429,12 @@ __global__ __launch_bounds__(kStepThreads) void step_kernel(jl_sim_t s) {
     // on the generator state.
     uint32_t* goal_bits = ocp;  // reuse: goals of agents not on their goal
     __syncthreads();
-    for (int k = tid; k < words; k += kStepThreads) goal_bits[k] = 0;
+    for (int k = tid; k < words; k += nt) goal_bits[k] = 0;
     __syncthreads();
-    for (int a = tid; a < A; a += kStepThreads) {
-        const size_t g = base + a;
-        const uint32_t fin = s_cur[a];
-        const uint32_t gx = s.goal_x[g], gy = s.goal_y[g];
-        if (!((fin & 0xFFFFu) == gx && (fin >> 16) == gy)) {
-            const uint32_t cell = gx * H + gy;
+    for (int a = tid; a < A; a += nt) {
+        const uint32_t goal = s_goal[a];
+        if (s_cur[a] != goal) {
+            const uint32_t cell = (goal & 0xFFFFu) * H + (goal >> 16);
             atomicOr(&goal_bits[cell >> 5], 1u << (cell & 31));
         }
     }
@@ -276,8 +444,7 @@ __global__ __launch_bounds__(kStepThreads) void step_kernel(jl_sim_t s) {
         const int offset = s.env_offsets[env];
         for (int a = 0; a < A; ++a) {
             const size_t g = base + a;
-            const uint32_t fin = s_cur[a];
-            if (!((fin & 0xFFFFu) == s.goal_x[g] && (fin >> 16) == s.goal_y[g])) continue;
+            if (s_cur[a] != s_goal[a]) continue;
             if (count <= 0) continue;
             uint64_t st = s.rng_state[g];
             int k = (int)((rng_next(&st) >> 32) % (uint64_t)count);
@@ -287,9 +454,11 @@ __global__ __launch_bounds__(kStepThreads) void step_kernel(jl_sim_t s) {
                 const uint32_t cell = x * H + y;
                 if (!((goal_bits[cell >> 5] >> (cell & 31)) & 1u)) {
                     goal_bits[cell >> 5] |= 1u << (cell & 31);
+                    s_goal[a] = x | (y << 16);
                     s.goal_x[g] = (uint16_t)x;
                     s.goal_y[g] = (uint16_t)y;
                     s.goal_changed[g] = 1;
+                    s_flag[a] |= 0x8000;  // goal changed this step
                     break;
                 }
                 if (++k >= count) k = 0;
@@ -298,10 +467,12 @@ __global__ __launch_bounds__(kStepThreads) void step_kernel(jl_sim_t s) {
         }
     }
     __syncthreads();
-    for (int a = tid; a < A; a += kStepThreads) {
+    for (int a = tid; a < A; a += nt) {
         const size_t g = base + a;
-        store_row(s.state_packed + g * 8, env, a, s_cur[a], s.goal_x[g], s.goal_y[g],
-                  s.actions[g], s.goal_changed[g]);
+        const uint32_t goal = s_goal[a];
+        const uint32_t f = s_flag[a];
+        store_row(s.state_packed + g * 8, env, a, s_cur[a], goal & 0xFFFFu, goal >> 16, f & 0xFFu,
+                  (f & 0x8000) ? 1u : 0u);
     }
 }
 
@@ -476,6 +647,22 @@ __global__ void init_agents_kernel(jl_sim_t s, const uint32_t* free_cells, const
     }
 }
 
+// Copy of the caller's actions into the simulator's buffer: 16-byte words
+// when both ends are aligned, bytes otherwise.
+template <bool kVec>
+__global__ __launch_bounds__(256) void copy_actions_kernel(uint8_t* __restrict__ dst,
+                                                           const uint8_t* __restrict__ src,
+                                                           size_t n) {
+    const size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
+    if (kVec) {
+        const size_t words = n / 16;
+        if (i < words) reinterpret_cast<uint4*>(dst)[i] = reinterpret_cast<const uint4*>(src)[i];
+        if (i < n - words * 16) dst[words * 16 + i] = src[words * 16 + i];
+    } else if (i < n) {
+        dst[i] = src[i];
+    }
+}
+
 int check_sim(const jl_sim_t* s) {
     if (!s || s->n_envs <= 0 || s->n_agents <= 0) return JL_ERR_ARG;
     if (!profile_ok(s->map_w, s->map_h)) return JL_ERR_PROFILE;
@@ -511,15 +698,47 @@ extern "C" int jl_step(const jl_sim_t* s, jl_stream_t stream) {
     if (rc) return rc;
     const StepLayout L = step_layout(s->n_agents, s->map_w, s->map_h);
     if (L.total > 160 * 1024) return JL_ERR_ARG;
+    const int nt = step_threads(s->n_agents);
+    const bool dense = step_dense(s->map_w, s->map_h);
+    const bool standard = s->task_mode == JL_TASK_STANDARD_MAPF;
+    const bool one = step_per(s->n_agents) == 1;
+#define JL_STEP_LAUNCH(STD, DENSE, PER)                                                        \
+    hipLaunchKernelGGL((step_kernel<H, STD, DENSE, PER>), dim3(s->n_envs), dim3(nt), L.total, \
+                       (hipStream_t)stream, *s)
     JL_DISPATCH_H(s->map_h, {
-        if (s->task_mode == JL_TASK_STANDARD_MAPF) {
-            hipLaunchKernelGGL((step_kernel<H, true>), dim3(s->n_envs), dim3(kStepThreads), L.total,
-                               (hipStream_t)stream, *s);
+        if (standard) {
+            if (dense) {
+                if (one) JL_STEP_LAUNCH(true, true, 1); else JL_STEP_LAUNCH(true, true, 4);
+            } else {
+                if (one) JL_STEP_LAUNCH(true, false, 1); else JL_STEP_LAUNCH(true, false, 4);
+            }
         } else {
-            hipLaunchKernelGGL((step_kernel<H, false>), dim3(s->n_envs), dim3(kStepThreads),
-                               L.total, (hipStream_t)stream, *s);
+            if (dense) {
+                if (one) JL_STEP_LAUNCH(false, true, 1); else JL_STEP_LAUNCH(false, true, 4);
+            } else {
+                if (one) JL_STEP_LAUNCH(false, false, 1); else JL_STEP_LAUNCH(false, false, 4);
+            }
         }
     });
+#undef JL_STEP_LAUNCH
+    return launch_status();
+}
+
+extern "C" int jl_update_actions(const jl_sim_t* s, const uint8_t* actions, jl_stream_t stream) {
+    int rc = check_sim(s);
+    if (rc) return rc;
+    if (!actions) return JL_ERR_ARG;
+    const size_t n = (size_t)s->n_envs * s->n_agents;
+    const bool vec = ((reinterpret_cast<uintptr_t>(actions) | reinterpret_cast<uintptr_t>(s->actions)) & 15u) == 0;
+    const size_t threads = vec ? (n + 15) / 16 : n;
+    const dim3 grid((unsigned)((threads + 255) / 256));
+    if (vec) {
+        hipLaunchKernelGGL(copy_actions_kernel<true>, grid, dim3(256), 0, (hipStream_t)stream,
+                           s->actions, actions, n);
+    } else {
+        hipLaunchKernelGGL(copy_actions_kernel<false>, grid, dim3(256), 0, (hipStream_t)stream,
+                           s->actions, actions, n);
+    }
     return launch_status();
 }
 

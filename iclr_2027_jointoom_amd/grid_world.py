@@ -541,8 +541,10 @@ class GridWorldSimulator(_Base, _PygModeMixin, _PygStorage):
             new_actions.device == self._device,
             "new_actions and simulator tensors must use the same CUDA device",
         )
-        with torch.cuda.device(self._device):
-            self.t_actions.copy_(new_actions)
+        check(
+            self._lib.jl_update_actions(self._sim_ref, _ptr(new_actions), _stream(self._device)),
+            "update_actions",
+        )
 
     def step_sim_only(self) -> None:
         """grid_world_simulator.cpp:694-705."""

@@ -96,6 +96,11 @@ int jl_encode_map(const int32_t* grids, uint32_t* grid_bits, int32_t n_envs,
  * GridWorldSimulator::step_sim_only, grid_world_simulator.cpp:694-705. */
 int jl_step(const jl_sim_t* sim, jl_stream_t stream);
 
+/* Copy the caller's actions (uint8 [E, A], device memory) into the
+ * simulator's action buffer on `stream`.  Replaces the device copy of
+ * GridWorldSimulator::update_actions, grid_world_simulator.cpp:678-688. */
+int jl_update_actions(const jl_sim_t* sim, const uint8_t* actions, jl_stream_t stream);
+
 /* Write loaded positions/goals (int16 [E, A, 2] each), arrival latches
  * (uint8 [E, A]) and step counts (int32 [E]) into the simulator: split
  * state, terminated/truncated, zero rewards and actions, occupancy, packed

@@ -277,6 +277,33 @@ def test_history_roll_kat():
     assert b.diagnostics.cpu().tolist()[1] == 1 and b.histories[0, 4].item() == 0
 
 
+@pytest.mark.parametrize("E,A", [(2, 256), (3, 100), (1, 7)])
+def test_append_actions_histories_match_oracle(oracle, E, A):
+    """Full 256-agent segments move as 16-byte words, a partial last segment
+    element by element; out-of-range actions count in diagnostics[1]."""
+    from iclr_2027_jointoom_amd import profile
+    from iclr_2027_jointoom_amd.synthetic import make_batch
+
+    grids, starts, goals = make_batch(11, E, 32, 32, A)
+    b = profile(32, 32).MapfGPTObservationBuilder(torch.from_numpy(grids.astype(np.int32)).cuda(), A)
+    ob = oracle.OracleMapfGPT(grids, A)
+    cx, cy = starts[..., 0].copy(), starts[..., 1].copy()
+    gx, gy = goals[..., 0].copy(), goals[..., 1].copy()
+    rng = np.random.default_rng(E * 1000 + A)
+    rejected = 0
+    for it in range(4):
+        b.build_tokens_from_state(*(torch.from_numpy(v).cuda() for v in (cx, cy, gx, gy)))
+        ob.build_state(cx, cy, gx, gy)
+        acts = rng.integers(0, 7, size=(E, A), dtype=np.uint8)  # 5 and 6 are rejected
+        b.append_actions(torch.from_numpy(acts).cuda())
+        ob.append(acts)
+        torch.cuda.synchronize()
+        assert np.array_equal(b.histories.cpu().numpy().view(np.uint16), ob.histories), it
+        assert b.diagnostics.cpu().tolist() == ob.diagnostics.tolist(), it
+        rejected += int(ob.diagnostics[1])
+    assert rejected > 0
+
+
 @pytest.mark.parametrize("num_agents", [256, 512])
 def test_scales_beyond_visible_cap(num_agents):
     ext = ext128()

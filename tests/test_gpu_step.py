@@ -286,6 +286,20 @@ def test_update_actions_copies_and_load_state_resets_actions():
         sim2.update_actions(noncontiguous)
 
 
+@pytest.mark.parametrize("E,A,offset", [(3, 37, 0), (3, 37, 1), (4, 64, 0), (2, 8, 5)])
+def test_update_actions_copies_every_byte(E, A, offset):
+    """Aligned sources take 16-byte words plus a byte tail, misaligned ones bytes."""
+    ext = ext_for(32, 32)
+    sim = _sim(ext, num_envs=E, num_agents=A, task_mode="standard_mapf")
+    backing = torch.randint(0, 256, (E * A + 16,), dtype=torch.uint8, device="cuda")
+    src = backing[offset:offset + E * A].view(E, A)
+    assert src.is_contiguous()
+    sim.actions.fill_(255)
+    sim.update_actions(src)
+    torch.cuda.synchronize()
+    assert torch.equal(sim.actions, src)
+
+
 def test_done_env_freezes_and_arrival_kats():
     ext = ext_for(128, 128)
     sim = _sim(ext, num_agents=2, task_mode="standard_mapf")
