@@ -1,16 +1,18 @@
 // jl_magat.hip - MAGAT node features and neighbour graph for gfx950.
 //
-// nodes: one workgroup per env.  The env's static and occupancy bitmaps,
-// agent positions and goals are staged in LDS; the 11x11 energy windows of a
-// chunk of agents are gathered into LDS with all loads independent; then one
-// wavefront writes each agent's 676-float row with 16-byte coalesced stores
-// (the reference zero-fills the row and rewrites it one float per thread,
-// 128_agents_map_stateless_step.cu:414-421, 438-478).  The clamped ctg
-// value is one of 21 float constants k/10 (the IEEE quotients), so no
-// division is evaluated on the device.
-// edges: per-env edge totals -> one-workgroup scan -> per-env writer that
-// scans its agents' counts in LDS and emits edges sorted by (source,
-// destination id) (grid_world_cuda.cu:17-110, stateless_step.cu:854-935).
+// nodes: one workgroup per (env, 64-agent slice).  The env's static and
+// occupancy bitmaps, agent positions and goals are staged in LDS; one
+// wavefront writes each agent's 676-float row, lane l owning patch cells
+// l, l + 64, l + 128: it loads its own energy byte and stores the four
+// channels of its cells as coalesced dwords (the reference zero-fills the row
+// and rewrites it one float per thread, 128_agents_map_stateless_step.cu:
+// 414-421, 438-478).  The clamped ctg value is one of 21 float constants k/10
+// (the IEEE quotients), so no division is evaluated on the device.
+// edges: per-env edge totals (from the node pass) -> one-workgroup scan ->
+// per (env, 64-source slice) writer: one wavefront per source tests the
+// others 64 at a time and the neighbours write their edges at consecutive
+// offsets, sorted by (source, destination id) (grid_world_cuda.cu:17-110,
+// stateless_step.cu:854-935).
 #include "jl_common.h"
 
 namespace jl {
@@ -23,13 +25,6 @@ __device__ __constant__ float kTenths[21] = {-1.0f, -0.9f, -0.8f, -0.7f, -0.6f, 
                                             -0.3f, -0.2f, -0.1f, 0.0f,  0.1f,  0.2f,  0.3f,
                                             0.4f,  0.5f,  0.6f,  0.7f,  0.8f,  0.9f,  1.0f};
 
-__device__ __forceinline__ float ctg_value(int center, int cell) {
-    const int d = center - cell;
-    if (d >= 10) return 1.0f;
-    if (d <= -10) return -1.0f;
-    return kTenths[d + 10];
-}
-
 // Exact round-half-even of num / den, den > 0 (stateless_step.cu:120-138).
 __device__ __forceinline__ int round_half_even(int num, int den) {
     const bool neg = num < 0;
@@ -38,6 +33,27 @@ __device__ __forceinline__ int round_half_even(int num, int den) {
     const unsigned r = mag - q * (unsigned)den;
     if (2 * r > (unsigned)den || (2 * r == (unsigned)den && (q & 1u))) ++q;
     return neg ? -(int)q : (int)q;
+}
+
+// Goal cell of the 13x13 patch (stateless_step.cu:480-509): the goal itself
+// inside the window, else its projection onto the patch border.
+__device__ __forceinline__ int goal_cell(int cx, int cy, int gx, int gy) {
+    const int rx = gx - cx, ry = gy - cy;
+    int fx, fy;
+    const int arx = rx < 0 ? -rx : rx, ary = ry < 0 ? -ry : ry;
+    if (arx <= kRadius && ary <= kRadius) {
+        fx = rx + 6;
+        fy = ry + 6;
+    } else if (ary >= arx) {
+        fy = 6 * ((ry > 0) - (ry < 0) + 1);
+        fx = 6 + round_half_even(6 * rx, ary);
+    } else {
+        fx = 6 * ((rx > 0) - (rx < 0) + 1);
+        fy = 6 + round_half_even(6 * ry, arx);
+    }
+    fx = fx < 0 ? 0 : (fx > 12 ? 12 : fx);
+    fy = fy < 0 ? 0 : (fy > 12 ? 12 : fy);
+    return fx * kPygDiam + fy;
 }
 
 __global__ __launch_bounds__(256) void occupancy_kernel(jl_magat_t m) {
@@ -63,15 +79,19 @@ __global__ __launch_bounds__(256) void occupancy_kernel(jl_magat_t m) {
 }
 
 struct NodeLayout {
-    int chunk;
-    size_t st_off, oc_off, pos_off, goal_off, valid_off, win_off, total;
+    size_t st_off, oc_off, pos_off, valid_off, part_off, win_off, row_off, tenths_off,
+        total;
 };
 
 __host__ __device__ inline size_t a16n(size_t v) { return (v + 15) & ~(size_t)15; }
 
+constexpr int kNodeEgos = 64;  // agents per node workgroup: an env spans ceil(A / 64)
+constexpr int kWinCells = kDiam * kDiam;
+constexpr int kWinStride = 128;  // LDS bytes per staged window
+constexpr int kWinItems = (kNodeEgos * kDiam + kNodeThreads - 1) / kNodeThreads;  // window rows per thread
+
 __host__ __device__ inline NodeLayout node_layout(int A, int W, int H) {
     NodeLayout L;
-    L.chunk = A < 256 ? A : 256;
     size_t o = 0;
     L.st_off = o;
     o = a16n(o + (size_t)W * H / 8);
@@ -79,29 +99,45 @@ __host__ __device__ inline NodeLayout node_layout(int A, int W, int H) {
     o = a16n(o + (size_t)W * H / 8);
     L.pos_off = o;
     o = a16n(o + (size_t)A * 4);
-    L.goal_off = o;
-    o = a16n(o + (size_t)A * 4);
     L.valid_off = o;
     o = a16n(o + (size_t)A);
-    L.win_off = o;
-    o = a16n(o + (size_t)L.chunk * 124);  // 121 window bytes + center, padded
+    L.part_off = o;  // the slice's edge counts (accumulated by the wavefronts), then goal cells
+    o = a16n(o + (size_t)kNodeEgos * 8);
+    L.win_off = o;  // the slice's 11x11 energy windows, kWinStride bytes each
+    o = a16n(o + (size_t)kNodeEgos * kWinStride);
+    L.row_off = o;  // per wavefront: one 676-float row
+    o = a16n(o + (size_t)(kNodeThreads / kWave) * kPygFeatures * 4);
+    L.tenths_off = o;  // the 21 ctg values k / 10
+    o = a16n(o + 21 * 4);
     L.total = o;
     return L;
 }
 
+// Workgroup = (env, slice of kNodeEgos agents).  Every slice stages the env's
+// bitmaps and agents in LDS; the env's first slice also counts every agent's
+// neighbours within squared radius 49 (others split over its wavefronts) and
+// writes the env total for the scan.  Then one wavefront per agent row: lane
+// l holds patch cells l, l + 64, l + 128 of the 13x13 patch, loads its own
+// energy byte and stores the four channels (obstacle, agents, goal, ctg) of
+// its cells as dwords; the next agent's energy bytes are requested before
+// the current row is produced.
 template <int H>
 __global__ __launch_bounds__(kNodeThreads) void nodes_kernel(jl_magat_t m) {
     extern __shared__ __align__(16) uint8_t smem[];
-    const int env = blockIdx.x, A = m.n_agents, W = m.map_w, E = m.n_envs;
+    const int A = m.n_agents, W = m.map_w, E = m.n_envs;
+    const int parts = (A + kNodeEgos - 1) / kNodeEgos;
+    const int env = blockIdx.x / parts;
+    const int part = blockIdx.x - env * parts;
+    const int e_begin = part * kNodeEgos;
+    const int e_end = (e_begin + kNodeEgos) < A ? (e_begin + kNodeEgos) : A;
     const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
     constexpr int nwaves = kNodeThreads / kWave;
     const NodeLayout L = node_layout(A, W, H);
     uint32_t* s_st = reinterpret_cast<uint32_t*>(smem + L.st_off);
     uint32_t* s_oc = reinterpret_cast<uint32_t*>(smem + L.oc_off);
     int32_t* s_pos = reinterpret_cast<int32_t*>(smem + L.pos_off);  // (int16 x, int16 y)
-    int32_t* s_goal = reinterpret_cast<int32_t*>(smem + L.goal_off);
     uint8_t* s_valid = smem + L.valid_off;
-    uint8_t* s_win = smem + L.win_off;
+    int32_t* s_part = reinterpret_cast<int32_t*>(smem + L.part_off);
     const int words = W * H / 32;
     const size_t cells = (size_t)W * H;
     const size_t base = (size_t)env * A;
@@ -113,150 +149,165 @@ __global__ __launch_bounds__(kNodeThreads) void nodes_kernel(jl_magat_t m) {
     for (int a = tid; a < A; a += kNodeThreads) {
         const uint4 r = *reinterpret_cast<const uint4*>(m.states + (base + a) * 8);
         s_pos[a] = (int32_t)r.y;
-        s_goal[a] = (int32_t)r.z;
         s_valid[a] = (r.x & 0xFFFFu) < (uint32_t)E ? 1 : 0;
+        if (a >= e_begin && a < e_end) {
+            s_part[a - e_begin] = 0;
+            s_part[kNodeEgos + a - e_begin] = goal_cell((int16_t)(r.y & 0xFFFFu), (int16_t)(r.y >> 16),
+                                                        (int16_t)(r.z & 0xFFFFu), (int16_t)(r.z >> 16));
+        }
     }
     __syncthreads();
 
-    // Edge counts: others within squared radius 49, all rows of the env block
-    // (stateless_step.cu:511-520).  Totals per env feed the scan; rows that
-    // are skipped keep their previous count, which the scan still reads.
-    int64_t env_total = 0;
-    for (int a = tid; a < A; a += kNodeThreads) {
-        int count;
-        if (s_valid[a]) {
+    // Edge counts of the slice: others within squared radius 49, all rows of
+    // the env block (stateless_step.cu:511-520), lane = agent of the slice,
+    // the others split over the wavefronts.  Rows that are skipped keep their
+    // previous count, which the totals still include; each slice writes its
+    // total, and the scan adds the env's slices.
+    {
+        const int a = e_begin + lane;
+        if (a < e_end) {
             const int cx = (int16_t)(s_pos[a] & 0xFFFF), cy = (int16_t)(s_pos[a] >> 16);
-            count = 0;
-            for (int o = 0; o < A; ++o) {
+            int count = 0;
+            for (int o = wave; o < A; o += nwaves) {
                 const int ox = (int16_t)(s_pos[o] & 0xFFFF), oy = (int16_t)(s_pos[o] >> 16);
                 const int dx = cx - ox, dy = cy - oy;
                 count += (o != a && dx * dx + dy * dy <= kCommRadiusSq) ? 1 : 0;
             }
-            m.edge_counts[base + a] = count;
-            m.pyg_pos[(base + a) * 2] = (float)cx;
-            m.pyg_pos[(base + a) * 2 + 1] = (float)cy;
-        } else {
-            count = m.edge_counts[base + a];
+            if (count) atomicAdd(&s_part[lane], count);
         }
-        env_total += count;
     }
-    {
-        // workgroup sum of env_total
-        __shared__ long long s_part[kNodeThreads / kWave];
-        long long v = env_total;
-        for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
-        if (lane == 0) s_part[wave] = v;
-        __syncthreads();
-        if (tid == 0) {
-            long long t = 0;
-            for (int k = 0; k < nwaves; ++k) t += s_part[k];
-            m.env_edge_base[env] = t;
+    __syncthreads();
+    if (wave == 0) {
+        const int a = e_begin + lane;
+        long long count = 0;
+        if (a < e_end) {
+            if (s_valid[a]) {
+                count = s_part[lane];
+                m.edge_counts[base + a] = (int32_t)count;
+            } else {
+                count = m.edge_counts[base + a];
+            }
         }
+        for (int off = kWave / 2; off > 0; off >>= 1) count += __shfl_xor(count, off, kWave);
+        if (lane == 0) m.env_edge_base[E + 1 + (size_t)env * parts + part] = count;
     }
 
-    for (int c0 = 0; c0 < A; c0 += L.chunk) {
-        const int nch = (A - c0) < L.chunk ? (A - c0) : L.chunk;
-        // energy windows (11x11) + centre of the chunk
-        const int pairs = nch * 122;
-#pragma unroll 4
-        for (int p = tid; p < pairs; p += kNodeThreads) {
-            const int el = p / 122;
-            const int c = p - el * 122;
-            const int a = c0 + el;
-            const int cx = (int16_t)(s_pos[a] & 0xFFFF), cy = (int16_t)(s_pos[a] >> 16);
-            int x, y;
-            if (c < 121) {
-                x = cx + c / kDiam - kRadius;
-                y = cy + c % kDiam - kRadius;
-            } else {
-                x = cx;
-                y = cy;
-            }
-            uint8_t v = 0;
-            if (s_valid[a] && x >= 0 && x < W && y >= 0 && y < H)
-                v = m.energy[(base + a) * cells + (size_t)(x * H + y)];
-            s_win[el * 124 + c] = v;
-        }
-        __syncthreads();
-        for (int el = wave; el < nch; el += nwaves) {
-            const int a = c0 + el;
-            if (!s_valid[a]) continue;
-            const int cx = (int16_t)(s_pos[a] & 0xFFFF), cy = (int16_t)(s_pos[a] >> 16);
-            const int gx = (int16_t)(s_goal[a] & 0xFFFF), gy = (int16_t)(s_goal[a] >> 16);
-            const bool center_in = cx >= 0 && cx < W && cy >= 0 && cy < H;
-            const int center = center_in ? (int)s_win[el * 124 + 121] : 0;
-            // goal cell of the 13x13 patch (stateless_step.cu:480-509)
-            const int rx = gx - cx, ry = gy - cy;
-            int fx, fy;
-            const int arx = rx < 0 ? -rx : rx, ary = ry < 0 ? -ry : ry;
-            if (arx <= kRadius && ary <= kRadius) {
-                fx = rx + 6;
-                fy = ry + 6;
-            } else if (ary >= arx) {
-                fy = 6 * ((ry > 0) - (ry < 0) + 1);
-                fx = 6 + round_half_even(6 * rx, ary);
-            } else {
-                fx = 6 * ((rx > 0) - (rx < 0) + 1);
-                fy = 6 + round_half_even(6 * ry, arx);
-            }
-            fx = fx < 0 ? 0 : (fx > 12 ? 12 : fx);
-            fy = fy < 0 ? 0 : (fy > 12 ? 12 : fy);
-            const int goal_p = fx * kPygDiam + fy;
-            float* row = m.pyg_x + (base + a) * kPygFeatures;
-            for (int q = lane; q < kPygFeatures / 4; q += kWave) {
-                float v4[4];
+    // Energy windows of the slice: item i = (agent i / 11, window row i % 11),
+    // 11 byte loads each at clamped addresses, 0 off the map.  Every thread
+    // has at most kWinItems items (a slice of kNodeEgos agents); an item past
+    // the slice repeats item 0 (same bytes, same LDS addresses), so all loads
+    // are issued before the first wait, and the row phase below reads LDS
+    // only, so its stores are never waited on.
+    uint8_t* s_win = smem + L.win_off;
+    float* s_tenths = reinterpret_cast<float*>(smem + L.tenths_off);
+    if (tid < 21) s_tenths[tid] = kTenths[tid];
+    {
+        const uint8_t* env_energy = m.energy + base * cells;
+        const int nitems = (e_end - e_begin) * kDiam;
+        uint32_t v[kWinItems][kDiam];
+        int dst[kWinItems];
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const int k = 4 * q + j;
-                    const int ch = k / kPygArea;
-                    const int p = k - ch * kPygArea;
-                    float v = 0.0f;
-                    if (ch == 2) {
-                        v = p == goal_p ? 1.0f : 0.0f;
-                    } else {
-                        const int pr = p / kPygDiam, pc = p - pr * kPygDiam;
-                        if (pr >= 1 && pr <= 11 && pc >= 1 && pc <= 11) {
-                            const int tx = cx + pr - 6;
-                            const int ty = cy + pc - 6;
-                            float obs = 0.0f, occ = 0.0f, ctg = 0.0f;
-                            if (tx < -1 || tx > W || ty < -1 || ty > H) {
-                                ctg = 1.0f;
-                            } else if (tx == -1 || tx == W || ty == -1 || ty == H) {
-                                obs = 1.0f;
-                                ctg = 1.0f;
-                            } else {
-                                const int cell = tx * H + ty;
-                                if ((s_st[cell >> 5] >> (cell & 31)) & 1u) {
-                                    obs = 1.0f;
-                                    ctg = 1.0f;
-                                } else {
-                                    if ((s_oc[cell >> 5] >> (cell & 31)) & 1u) occ = 1.0f;
-                                    ctg = ctg_value(center,
-                                                    (int)s_win[el * 124 + (pr - 1) * kDiam + (pc - 1)]);
-                                }
-                            }
-                            v = ch == 0 ? obs : (ch == 1 ? occ : ctg);
-                        }
-                    }
-                    v4[j] = v;
-                }
-                reinterpret_cast<float4*>(row)[q] = make_float4(v4[0], v4[1], v4[2], v4[3]);
+        for (int it = 0; it < kWinItems; ++it) {
+            const int i = tid + it * kNodeThreads < nitems ? tid + it * kNodeThreads : 0;
+            const int el = i / kDiam, r = i - el * kDiam;
+            const int a = e_begin + el;
+            const int32_t pos = s_pos[a];
+            const int x = (int16_t)(pos & 0xFFFF) + r - kRadius;
+            const int y0 = (int16_t)(pos >> 16) - kRadius;
+            const bool rok = s_valid[a] && x >= 0 && x < W;
+            const uint8_t* src = env_energy + (size_t)a * cells + (size_t)(rok ? x : 0) * H;
+            dst[it] = el * kWinStride + r * kDiam;
+#pragma unroll
+            for (int j = 0; j < kDiam; ++j) {
+                const int y = y0 + j;
+                const bool ok = rok && y >= 0 && y < H;
+                const uint32_t b = src[ok ? y : 0];
+                v[it][j] = ok ? b : 0u;
             }
         }
-        __syncthreads();
+#pragma unroll
+        for (int it = 0; it < kWinItems; ++it)
+#pragma unroll
+            for (int j = 0; j < kDiam; ++j) s_win[dst[it] + j] = (uint8_t)v[it][j];
+    }
+    __syncthreads();
+
+    // Rows: one wavefront per agent; lane l owns patch cells l, l + 64,
+    // l + 128 (p < 169) of the 13x13 patch, whose rows and columns 1..11 are
+    // the window, and writes their four channel values into the wavefront's
+    // LDS row (a lane past the patch on the third pass repeats its second
+    // cell); the row then leaves as 16-byte stores in address order, so the
+    // 128-byte lines it shares with the neighbouring rows are completed in the
+    // cache instead of being written twice.
+    float* my_row = reinterpret_cast<float*>(smem + L.row_off) + wave * kPygFeatures;
+    int prow[3], pcol[3], pwc[3];
+    bool pwin[3];
+#pragma unroll
+    for (int k = 0; k < 3; ++k) {
+        const int p = (lane + kWave * k) < kPygArea ? lane + kWave * k : lane + kWave;
+        prow[k] = p / kPygDiam;
+        pcol[k] = p - prow[k] * kPygDiam;
+        pwin[k] = prow[k] >= 1 && prow[k] <= kDiam && pcol[k] >= 1 && pcol[k] <= kDiam;
+        pwc[k] = pwin[k] ? (prow[k] - 1) * kDiam + (pcol[k] - 1) : 0;
+    }
+    for (int a = e_begin + wave; a < e_end; a += nwaves) {
+        if (!s_valid[a]) continue;
+        const uint8_t* win = s_win + (a - e_begin) * kWinStride;
+        const int32_t pos = s_pos[a];
+        const int cx = (int16_t)(pos & 0xFFFF), cy = (int16_t)(pos >> 16);
+        if (lane < 2) m.pyg_pos[(base + a) * 2 + lane] = (float)(lane ? cy : cx);
+        // the centre is window cell (5, 5); 0 when the agent is off the map
+        const int center = win[kRadius * kDiam + kRadius];
+        const int goal_p = s_part[kNodeEgos + a - e_begin];
+        float* row = m.pyg_x + (base + a) * kPygFeatures;
+#pragma unroll
+        for (int k = 0; k < 3; ++k) {
+            // window cell: off the map by more than one ring -> ctg 1; on the
+            // ring around the map or an obstacle -> obstacle 1, ctg 1; free ->
+            // agents bit and ctg from the energy difference (:438-478)
+            const int p = prow[k] * kPygDiam + pcol[k];
+            const int tx = cx + prow[k] - 6, ty = cy + pcol[k] - 6;
+            const bool inmap = (uint32_t)tx < (uint32_t)W && (uint32_t)ty < (uint32_t)H;
+            const bool ring = !inmap && (uint32_t)(tx + 1) <= (uint32_t)(W + 1) &&
+                              (uint32_t)(ty + 1) <= (uint32_t)(H + 1);
+            const int cell = inmap ? tx * H + ty : 0;
+            const bool wall = inmap && ((s_st[cell >> 5] >> (cell & 31)) & 1u);
+            const bool agent = (s_oc[cell >> 5] >> (cell & 31)) & 1u;
+            const bool free_cell = inmap && !wall;
+            int d = center - (int)win[pwc[k]];
+            d = d < -10 ? -10 : (d > 10 ? 10 : d);
+            const float cv = s_tenths[d + 10];
+            my_row[p] = (pwin[k] && (ring || wall)) ? 1.0f : 0.0f;
+            my_row[kPygArea + p] = (pwin[k] && free_cell && agent) ? 1.0f : 0.0f;
+            my_row[2 * kPygArea + p] = p == goal_p ? 1.0f : 0.0f;
+            my_row[3 * kPygArea + p] = pwin[k] ? (free_cell ? cv : 1.0f) : 0.0f;
+        }
+        wave_sync();
+        const float4* src = reinterpret_cast<const float4*>(my_row);
+        float4* dst = reinterpret_cast<float4*>(row);
+#pragma unroll
+        for (int k = 0; k < 3; ++k) {
+            const int q = lane + kWave * k;
+            if (q < kPygFeatures / 4) dst[q] = src[q];
+        }
+        wave_sync();  // the row buffer is rewritten by the next agent
     }
 }
 
-// One workgroup: exclusive scan of the E env totals (in place, E+1 entries).
+// One workgroup: env totals (the sum of each env's slice totals, stored past
+// the E + 1 bases) and their exclusive scan into the bases.
 __global__ __launch_bounds__(1024) void env_scan_kernel(jl_magat_t m) {
     __shared__ long long s_wave[16];
     __shared__ long long s_carry;
     const int E = m.n_envs, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int parts = (m.n_agents + kNodeEgos - 1) / kNodeEgos;
     if (tid == 0) s_carry = 0;
     __syncthreads();
     for (int b0 = 0; b0 < E; b0 += 1024) {
         const int i = b0 + tid;
-        const long long v = i < E ? m.env_edge_base[i] : 0;
+        long long v = 0;
+        if (i < E)
+            for (int p = 0; p < parts; ++p) v += m.env_edge_base[E + 1 + (size_t)i * parts + p];
         long long incl = v;
         for (int off = 1; off < 64; off <<= 1) {
             const long long t = __shfl_up(incl, off, 64);
@@ -282,54 +333,84 @@ __global__ __launch_bounds__(1024) void env_scan_kernel(jl_magat_t m) {
     }
 }
 
-__global__ __launch_bounds__(256) void edges_kernel(jl_magat_t m) {
+constexpr int kEdgeThreads = 256;
+constexpr int kEdgeSources = 64;  // sources per edge workgroup (one wavefront scans them)
+
+// Workgroup = (env, slice of kEdgeSources sources).  The env's positions are
+// staged in LDS and the slice's first edge offsets are the env's scanned base
+// plus the counts of the agents before the slice (a workgroup sum) plus a
+// scan over the slice.  One wavefront per source tests the others 64 at a
+// time; the neighbours of a chunk write their edges at the source's next
+// offsets in lane (= id) order, so edges are ordered by (source, destination
+// id), the reference's order (stateless_step.cu:854-935).
+__global__ __launch_bounds__(kEdgeThreads) void edges_kernel(jl_magat_t m) {
     extern __shared__ __align__(16) int32_t s_xy[];  // (int16 x, int16 y) per agent
-    __shared__ long long s_wave[4];
-    const int env = blockIdx.x, A = m.n_agents;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    __shared__ long long s_wave[kEdgeThreads / kWave];
+    __shared__ long long s_first[kEdgeSources];
+    const int A = m.n_agents;
+    const int parts = (A + kEdgeSources - 1) / kEdgeSources;
+    const int env = blockIdx.x / parts;
+    const int part = blockIdx.x - env * parts;
+    const int s_begin = part * kEdgeSources;
+    const int s_end = (s_begin + kEdgeSources) < A ? (s_begin + kEdgeSources) : A;
+    const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
+    constexpr int nwaves = kEdgeThreads / kWave;
     const size_t base = (size_t)env * A;
-    for (int a = tid; a < A; a += 256) {
+    for (int a = tid; a < A; a += kEdgeThreads) {
         const int x = (int16_t)m.pyg_pos[(base + a) * 2];
         const int y = (int16_t)m.pyg_pos[(base + a) * 2 + 1];
         s_xy[a] = (x & 0xFFFF) | (y << 16);
     }
-    long long carry = m.env_edge_base[env];
-    for (int a0 = 0; a0 < A; a0 += 256) {
-        const int a = a0 + tid;
-        const long long c = a < A ? m.edge_counts[base + a] : 0;
+    // counts of the agents before the slice
+    long long before = 0;
+    for (int a = tid; a < s_begin; a += kEdgeThreads) before += m.edge_counts[base + a];
+    for (int off = kWave / 2; off > 0; off >>= 1) before += __shfl_xor(before, off, kWave);
+    if (lane == 0) s_wave[wave] = before;
+    __syncthreads();
+    if (wave == 0) {
+        long long first = m.env_edge_base[env];
+        for (int k = 0; k < nwaves; ++k) first += s_wave[k];
+        const int a = s_begin + lane;
+        const long long c = a < s_end ? m.edge_counts[base + a] : 0;
         long long incl = c;
-        for (int off = 1; off < 64; off <<= 1) {
-            const long long t = __shfl_up(incl, off, 64);
+        for (int off = 1; off < kWave; off <<= 1) {
+            const long long t = __shfl_up(incl, off, kWave);
             if (lane >= off) incl += t;
         }
-        if (lane == 63) s_wave[wave] = incl;
-        __syncthreads();
-        long long before = carry;
-        for (int k = 0; k < wave; ++k) before += s_wave[k];
-        const long long first = before + incl - c;
-        if (a < A) {
-            m.edge_prefix[base + a] = first;
-            const int cx = (int16_t)(s_xy[a] & 0xFFFF), cy = s_xy[a] >> 16;
-            long long out = first;
-            const long long cap = m.edge_capacity;
-            for (int o = 0; o < A; ++o) {
-                if (o == a) continue;
-                const int dx = cx - (int16_t)(s_xy[o] & 0xFFFF);
-                const int dy = cy - (s_xy[o] >> 16);
-                if (dx * dx + dy * dy > kCommRadiusSq) continue;
-                if (out >= 0 && out < cap) {
-                    m.edge_index[out] = (int64_t)(base + a);
-                    m.edge_index[cap + out] = (int64_t)(base + o);
-                    m.edge_attr[out * 3] = (float)dx;
-                    m.edge_attr[out * 3 + 1] = (float)dy;
-                    m.edge_attr[out * 3 + 2] = (float)((dx < 0 ? -dx : dx) + (dy < 0 ? -dy : dy));
-                }
-                ++out;
-            }
+        if (a < s_end) {
+            s_first[lane] = first + incl - c;
+            m.edge_prefix[base + a] = first + incl - c;
         }
-        __syncthreads();
-        carry += s_wave[0] + s_wave[1] + s_wave[2] + s_wave[3];
-        __syncthreads();
+    }
+    __syncthreads();
+    const long long cap = m.edge_capacity;
+    for (int a = s_begin + wave; a < s_end; a += nwaves) {
+        long long out = s_first[a - s_begin];
+        const int cx = (int16_t)(s_xy[a] & 0xFFFF), cy = s_xy[a] >> 16;
+        for (int o0 = 0; o0 < A; o0 += kWave) {
+            const int o = o0 + lane;
+            int dx = 0, dy = 0;
+            bool near = false;
+            if (o < A && o != a) {
+                dx = cx - (int16_t)(s_xy[o] & 0xFFFF);
+                dy = cy - (s_xy[o] >> 16);
+                near = dx * dx + dy * dy <= kCommRadiusSq;
+            }
+            const uint64_t bal = __ballot(near);
+            if (near) {
+                const long long e = out + __builtin_amdgcn_mbcnt_hi(
+                                              (uint32_t)(bal >> 32),
+                                              __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0u));
+                if (e >= 0 && e < cap) {
+                    m.edge_index[e] = (int64_t)(base + a);
+                    m.edge_index[cap + e] = (int64_t)(base + o);
+                    m.edge_attr[e * 3] = (float)dx;
+                    m.edge_attr[e * 3 + 1] = (float)dy;
+                    m.edge_attr[e * 3 + 2] = (float)((dx < 0 ? -dx : dx) + (dy < 0 ? -dy : dy));
+                }
+            }
+            out += __popcll(bal);
+        }
     }
 }
 
@@ -361,9 +442,10 @@ extern "C" int jl_magat_nodes(const jl_magat_t* m, jl_stream_t stream) {
         return JL_ERR_ARG;
     const NodeLayout L = node_layout(m->n_agents, m->map_w, m->map_h);
     if (L.total > 160 * 1024) return JL_ERR_ARG;
+    const unsigned parts = (unsigned)((m->n_agents + kNodeEgos - 1) / kNodeEgos);
     JL_DISPATCH_H(m->map_h, {
-        hipLaunchKernelGGL((nodes_kernel<H>), dim3(m->n_envs), dim3(kNodeThreads), L.total,
-                           (hipStream_t)stream, *m);
+        hipLaunchKernelGGL((nodes_kernel<H>), dim3((unsigned)m->n_envs * parts), dim3(kNodeThreads),
+                           L.total, (hipStream_t)stream, *m);
     });
     return launch_status();
 }
@@ -379,7 +461,8 @@ extern "C" int jl_magat_edges(const jl_magat_t* m, jl_stream_t stream) {
     hipLaunchKernelGGL(env_scan_kernel, dim3(1), dim3(1024), 0, (hipStream_t)stream, *m);
     rc = launch_status();
     if (rc) return rc;
-    hipLaunchKernelGGL(edges_kernel, dim3(m->n_envs), dim3(256), (size_t)m->n_agents * 4,
-                       (hipStream_t)stream, *m);
+    const unsigned eparts = (unsigned)((m->n_agents + kEdgeSources - 1) / kEdgeSources);
+    hipLaunchKernelGGL(edges_kernel, dim3((unsigned)m->n_envs * eparts), dim3(kEdgeThreads),
+                       (size_t)m->n_agents * 4, (hipStream_t)stream, *m);
     return launch_status();
 }

@@ -132,8 +132,10 @@ class _PygStorage:
         self.t_pyg_edge_attr_storage = torch.zeros((cap, 3), dtype=torch.float32, device=device)
         self.t_pyg_edge_prefix = torch.zeros((N + 1,), dtype=torch.int64, device=device)
         self.t_pyg_num_edges = torch.zeros((1,), dtype=torch.int64, device=device)
-        # per-env edge totals and their scan (the reference's CUB workspace)
-        self.t_scan_temp_storage = torch.zeros((E + 1,), dtype=torch.int64, device=device)
+        # the reference's CUB workspace: env bases [E + 1], then one edge
+        # total per (env, 64-agent slice) from the node builder
+        slices = (A + 63) // 64
+        self.t_scan_temp_storage = torch.zeros((E + 1 + E * slices,), dtype=torch.int64, device=device)
         self.t_pyg_batch = torch.arange(E, dtype=torch.int64, device=device).repeat_interleave(A)
         self.t_pyg_ptr = torch.arange(E + 1, dtype=torch.int64, device=device) * A
         self.t_pyg_edge_index = self.t_pyg_edge_index_storage.narrow(1, 0, 0)

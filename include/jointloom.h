@@ -227,7 +227,8 @@ typedef struct jl_magat {
     int64_t* edge_index;        /* [2, edge_capacity] */
     float* edge_attr;           /* [edge_capacity, 3] */
     int64_t edge_capacity;      /* >= E * A * (A - 1) */
-    int64_t* env_edge_base;     /* [E + 1] workspace */
+    int64_t* env_edge_base;     /* [E + 1 + E * ceil(A / 64)] workspace: env bases, then
+                                   the node builder's per-64-agent-slice edge totals */
 } jl_magat_t;
 
 /* Occupancy bitmap from agent state rows (rows with env id out of range are
