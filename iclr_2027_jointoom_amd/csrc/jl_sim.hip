@@ -663,6 +663,86 @@ __global__ __launch_bounds__(256) void copy_actions_kernel(uint8_t* __restrict__
     }
 }
 
+// Inclusive int64 prefix sum of the goal_changed values and its last value
+// (the int64 cast, cumsum and count of GridWorldSimulator::
+// update_derived_state, grid_world_simulator.cpp:709-717).  Workgroup w
+// scans values [w * kScanChunk, (w + 1) * kScanChunk): it sums every value
+// before its range itself (16 bytes per load, from the L2), so workgroups
+// never wait for each other, scans its own range through LDS and writes the
+// prefixes with consecutive lanes on consecutive values.
+constexpr int kScanThreads = 256;
+constexpr int kScanPer = 4;                             // values per thread
+constexpr int kScanChunk = kScanThreads * kScanPer;     // values per workgroup
+
+__device__ __forceinline__ uint32_t byte_sum(uint32_t w) {
+    return (w & 0xFFu) + ((w >> 8) & 0xFFu) + ((w >> 16) & 0xFFu) + (w >> 24);
+}
+
+__global__ __launch_bounds__(kScanThreads) void goal_changed_scan_kernel(jl_sim_t s, int64_t* prefix,
+                                                                         int64_t* count,
+                                                                         uint16_t* changed) {
+    __shared__ int64_t s_wave[kScanThreads / kWave];
+    __shared__ int64_t s_out[kScanChunk];
+    const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
+    const int64_t N = (int64_t)s.n_envs * s.n_agents;
+    const int64_t c0 = (int64_t)blockIdx.x * kScanChunk;
+    const uint8_t* f = s.goal_changed;
+    // the changed-row buffer is cleared before the energy pass packs into it
+    // (the reference zero-fills it, grid_world_simulator.cpp:724-733)
+    if (changed) {
+        const uint4 zero = make_uint4(0, 0, 0, 0);
+#pragma unroll
+        for (int j = 0; j < kScanPer; ++j) {
+            const int64_t e = c0 + tid + j * kScanThreads;
+            if (e < N) reinterpret_cast<uint4*>(changed)[e] = zero;
+        }
+    }
+    // values before this chunk: 16-byte words up to c0, bytes for the rest
+    const bool vec = (reinterpret_cast<uintptr_t>(f) & 15u) == 0;
+    const int64_t words = vec ? c0 / 16 : 0;
+    uint64_t before = 0;
+    for (int64_t k = tid; k < words; k += kScanThreads) {
+        const uint4 w = reinterpret_cast<const uint4*>(f)[k];
+        before += byte_sum(w.x) + byte_sum(w.y) + byte_sum(w.z) + byte_sum(w.w);
+    }
+    for (int64_t k = words * 16 + tid; k < c0; k += kScanThreads) before += f[k];
+    for (int off = kWave / 2; off > 0; off >>= 1) before += __shfl_xor(before, off, kWave);
+    if (lane == 0) s_wave[wave] = (int64_t)before;
+    __syncthreads();
+    int64_t base = 0;
+    for (int k = 0; k < kScanThreads / kWave; ++k) base += s_wave[k];
+    __syncthreads();
+    // this thread's kScanPer consecutive values, scanned across the workgroup
+    const int64_t e0 = c0 + (int64_t)tid * kScanPer;
+    uint32_t v[kScanPer];
+#pragma unroll
+    for (int j = 0; j < kScanPer; ++j) v[j] = e0 + j < N ? f[e0 + j] : 0u;
+    uint32_t local = 0;
+#pragma unroll
+    for (int j = 0; j < kScanPer; ++j) local += v[j];
+    int64_t incl = local;
+    for (int off = 1; off < kWave; off <<= 1) {
+        const int64_t t = __shfl_up(incl, off, kWave);
+        if (lane >= off) incl += t;
+    }
+    if (lane == kWave - 1) s_wave[wave] = incl;
+    __syncthreads();
+    int64_t run = base + incl - local;
+    for (int k = 0; k < wave; ++k) run += s_wave[k];
+#pragma unroll
+    for (int j = 0; j < kScanPer; ++j) {
+        run += v[j];
+        s_out[tid * kScanPer + j] = run;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < kScanPer; ++j) {
+        const int64_t e = c0 + tid + j * kScanThreads;
+        if (e < N) prefix[e] = s_out[tid + j * kScanThreads];
+        if (e == N - 1) count[0] = s_out[tid + j * kScanThreads];
+    }
+}
+
 int check_sim(const jl_sim_t* s) {
     if (!s || s->n_envs <= 0 || s->n_agents <= 0) return JL_ERR_ARG;
     if (!profile_ok(s->map_w, s->map_h)) return JL_ERR_PROFILE;
@@ -739,6 +819,17 @@ extern "C" int jl_update_actions(const jl_sim_t* s, const uint8_t* actions, jl_s
         hipLaunchKernelGGL(copy_actions_kernel<false>, grid, dim3(256), 0, (hipStream_t)stream,
                            s->actions, actions, n);
     }
+    return launch_status();
+}
+
+extern "C" int jl_goal_changed_scan(const jl_sim_t* s, int64_t* prefix, int64_t* count,
+                                    uint16_t* changed_states, jl_stream_t stream) {
+    int rc = check_sim(s);
+    if (rc) return rc;
+    if (!prefix || !count) return JL_ERR_ARG;
+    const int64_t N = (int64_t)s->n_envs * s->n_agents;
+    hipLaunchKernelGGL(goal_changed_scan_kernel, dim3((unsigned)((N + kScanChunk - 1) / kScanChunk)),
+                       dim3(kScanThreads), 0, (hipStream_t)stream, *s, prefix, count, changed_states);
     return launch_status();
 }
 

@@ -558,24 +558,29 @@ class GridWorldSimulator(_Base, _PygModeMixin, _PygStorage):
 
     def update_derived_state(self) -> None:
         """Energy fields of changed goals (grid_world_simulator.cpp:707-753), no host sync."""
-        with torch.cuda.device(self._device):
-            flags = self.t_goal_changed_flags.reshape(-1).to(torch.int64)
-            torch.cumsum(flags, 0, out=self.t_goal_changed_prefix)
-            self.t_goal_changed_count.copy_(self.t_goal_changed_prefix[-1:])
-            full = self.current_step == 1
-            if not full:
-                self.t_changed_state_packed.zero_()
-            check(
-                self._lib.jl_energy_maps_flagged(
-                    self._sim_ref,
-                    self.t_energy_maps.data_ptr(),
-                    1 if full else 0,
-                    self.t_goal_changed_prefix.data_ptr(),
-                    self.t_changed_state_packed.data_ptr(),
-                    _stream(self._device),
-                ),
-                "Stateful energy map kernel",
-            )
+        full = self.current_step == 1
+        # after the first step the changed-row buffer is cleared, then packed
+        check(
+            self._lib.jl_goal_changed_scan(
+                self._sim_ref,
+                self.t_goal_changed_prefix.data_ptr(),
+                self.t_goal_changed_count.data_ptr(),
+                None if full else self.t_changed_state_packed.data_ptr(),
+                _stream(self._device),
+            ),
+            "Goal-changed scan",
+        )
+        check(
+            self._lib.jl_energy_maps_flagged(
+                self._sim_ref,
+                self.t_energy_maps.data_ptr(),
+                1 if full else 0,
+                self.t_goal_changed_prefix.data_ptr(),
+                self.t_changed_state_packed.data_ptr(),
+                _stream(self._device),
+            ),
+            "Stateful energy map kernel",
+        )
 
     def build_magat_plus_nodes(self) -> None:
         self._run_nodes()

@@ -96,6 +96,15 @@ int jl_encode_map(const int32_t* grids, uint32_t* grid_bits, int32_t n_envs,
  * GridWorldSimulator::step_sim_only, grid_world_simulator.cpp:694-705. */
 int jl_step(const jl_sim_t* sim, jl_stream_t stream);
 
+/* Inclusive int64 prefix sum of the goal_changed values (uint8, summed as
+ * int64) into prefix [E*A] and its total into count [1], on `stream` (no
+ * host synchronisation).  A non-null changed_states (int16 [E*A, 8]) is
+ * zero-filled for jl_energy_maps_flagged to pack into.  Replaces the cumsum,
+ * count and fill of GridWorldSimulator::update_derived_state,
+ * grid_world_simulator.cpp:709-733. */
+int jl_goal_changed_scan(const jl_sim_t* sim, int64_t* prefix, int64_t* count,
+                         uint16_t* changed_states, jl_stream_t stream);
+
 /* Copy the caller's actions (uint8 [E, A], device memory) into the
  * simulator's action buffer on `stream`.  Replaces the device copy of
  * GridWorldSimulator::update_actions, grid_world_simulator.cpp:678-688. */

@@ -341,6 +341,61 @@ def test_incremental_energy_refresh_matches_full_recompute():
     assert torch.equal(sim.energy_maps.cpu(), ref.energy_maps.cpu())
 
 
+@pytest.mark.parametrize("E,A,p", [(3, 37, 0.3), (2, 300, 0.05), (1, 5, 0.0)])
+def test_goal_changed_scan_and_packing(E, A, p):
+    """update_derived_state after the first step: inclusive int64 cumsum of the
+    flags, its total, changed rows packed at prefix - 1 with reset_flag 1 and
+    the rest of the buffer cleared (grid_world_simulator.cpp:707-753,
+    128_agents_map_step.cu:469-491); energy maps of the changed agents equal
+    a stateless recompute."""
+    from iclr_2027_jointoom_amd.synthetic import make_batch
+
+    grids, starts, goals = make_batch(17 + A, E, 64, 64, A)
+    ext = ext_for(64, 64)
+    g = torch.from_numpy(grids.astype(np.int32)).cuda()
+    sim = ext.GridWorldSimulator(g, A, 3, E * 64 * 64, 5, "standard_mapf", 64)
+    sim.load_state(torch.from_numpy(starts).cuda(), torch.from_numpy(goals).cuda(),
+                   torch.zeros((E, A), dtype=torch.uint8, device="cuda"),
+                   torch.zeros(E, dtype=torch.int32, device="cuda"))
+    sim.update_actions(torch.zeros((E, A), dtype=torch.uint8, device="cuda"))
+    sim.step_sim_only()
+    sim.update_derived_state()  # first step: full refresh
+    sim.step_sim_only()
+    sim.changed_state_packed.fill_(7)  # stale content the refresh must clear
+    rng = np.random.default_rng(E * A)
+    flags = (rng.random((E, A)) < p).astype(np.uint8)
+    flags[flags != 0] += (rng.random(int(flags.sum())) < 0.2).astype(np.uint8)  # values, not booleans
+    sim.goal_changed_flags.copy_(torch.from_numpy(flags).cuda())
+    # move the flagged agents' goals so their fields change
+    gx = sim.goal_x.cpu().numpy().copy()
+    gy = sim.goal_y.cpu().numpy().copy()
+    gx[flags != 0], gy[flags != 0] = starts[..., 0][flags != 0], starts[..., 1][flags != 0]
+    sim.goal_x.copy_(torch.from_numpy(gx).cuda())
+    sim.goal_y.copy_(torch.from_numpy(gy).cuda())
+    before = sim.energy_maps.clone()
+    sim.update_derived_state()
+    torch.cuda.synchronize()
+    prefix = np.cumsum(flags.reshape(-1).astype(np.int64))
+    assert np.array_equal(sim.goal_changed_prefix.cpu().numpy(), prefix)
+    assert int(sim.goal_changed_count.item()) == int(prefix[-1])
+    expect = np.zeros((E * A, 8), np.int16)
+    cx, cy = sim.cur_x.cpu().numpy(), sim.cur_y.cpu().numpy()
+    acts = sim.actions.cpu().numpy()
+    for gi in np.flatnonzero(flags.reshape(-1)):
+        e, a = divmod(int(gi), A)
+        expect[prefix[gi] - 1] = [e, a, cx[e, a], cy[e, a], gx[e, a], gy[e, a], acts[e, a], 1]
+    assert np.array_equal(sim.changed_state_packed.cpu().numpy(), expect)
+    # the flagged agents' fields are refreshed (a gap row left by a value above
+    # 1 is not run: in the reference it would recompute env 0 agent 0)
+    rows = expect[prefix[flags.reshape(-1) != 0] - 1]
+    if len(rows):
+        ref = ext.StatelessGridWorldSimulator(g, A, 3)
+        ref.energy_maps.copy_(before)
+        ref.update_energy_maps(torch.from_numpy(rows).cuda(), len(rows))
+        torch.cuda.synchronize()
+        assert torch.equal(sim.energy_maps.cpu(), ref.energy_maps.cpu())
+
+
 def test_more_than_256_agents():
     """test_compact_state_api.py:262-285."""
     A = 300
