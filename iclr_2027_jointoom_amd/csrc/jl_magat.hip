@@ -130,7 +130,8 @@ __global__ __launch_bounds__(kNodeThreads) void nodes_kernel(jl_magat_t m) {
     const int part = blockIdx.x - env * parts;
     const int e_begin = part * kNodeEgos;
     const int e_end = (e_begin + kNodeEgos) < A ? (e_begin + kNodeEgos) : A;
-    const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
+    const int tid = threadIdx.x, lane = tid & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);  // uniform per wavefront
     constexpr int nwaves = kNodeThreads / kWave;
     const NodeLayout L = node_layout(A, W, H);
     uint32_t* s_st = reinterpret_cast<uint32_t*>(smem + L.st_off);
@@ -334,44 +335,66 @@ __global__ __launch_bounds__(1024) void env_scan_kernel(jl_magat_t m) {
 }
 
 constexpr int kEdgeThreads = 256;
-constexpr int kEdgeSources = 64;  // sources per edge workgroup (one wavefront scans them)
+constexpr int kEdgeSources = 64;  // sources per edge workgroup
+constexpr int kEdgeUnroll = 4;    // 64-candidate chunks tested per step
+constexpr int kEdgeSpan = kWave * kEdgeUnroll;
 
-// Workgroup = (env, slice of kEdgeSources sources).  The env's positions are
-// staged in LDS and the slice's first edge offsets are the env's scanned base
-// plus the counts of the agents before the slice (a workgroup sum) plus a
-// scan over the slice.  One wavefront per source tests the others 64 at a
-// time; the neighbours of a chunk write their edges at the source's next
-// offsets in lane (= id) order, so edges are ordered by (source, destination
+// Edge workgroup LDS: positions padded to a multiple of kEdgeSpan with cells
+// far off every map (never within the radius), the env's counts, and one
+// neighbour list of up to A ids per wavefront.
+__host__ __device__ inline size_t edge_lds(int A) {
+    const size_t padded = (size_t)(A + kEdgeSpan - 1) / kEdgeSpan * kEdgeSpan;
+    return padded * 4 + (size_t)A * 4 + (size_t)(kEdgeThreads / kWave) * A * 4;
+}
+
+// Workgroup = (env, slice of kEdgeSources sources).  The env's positions and
+// counts are staged in LDS in one round trip; the slice's first edge offsets
+// are the env's scanned base plus the counts before the slice plus a scan
+// over the slice.  One wavefront per source tests the others kEdgeSpan at a
+// time (32-bit differences: positions are any int16), appends each chunk's
+// neighbours to its LDS list in lane (= id) order, then writes the source's
+// edges from consecutive lanes: edges are ordered by (source, destination
 // id), the reference's order (stateless_step.cu:854-935).
 __global__ __launch_bounds__(kEdgeThreads) void edges_kernel(jl_magat_t m) {
-    extern __shared__ __align__(16) int32_t s_xy[];  // (int16 x, int16 y) per agent
+    extern __shared__ __align__(16) int32_t s_xy[];  // (int16 x, int16 y) per agent, padded
     __shared__ long long s_wave[kEdgeThreads / kWave];
     __shared__ long long s_first[kEdgeSources];
     const int A = m.n_agents;
+    const int padded = (A + kEdgeSpan - 1) / kEdgeSpan * kEdgeSpan;
+    int32_t* s_cnt = s_xy + padded;
     const int parts = (A + kEdgeSources - 1) / kEdgeSources;
     const int env = blockIdx.x / parts;
     const int part = blockIdx.x - env * parts;
     const int s_begin = part * kEdgeSources;
     const int s_end = (s_begin + kEdgeSources) < A ? (s_begin + kEdgeSources) : A;
-    const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
+    const int tid = threadIdx.x, lane = tid & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);  // uniform per wavefront
     constexpr int nwaves = kEdgeThreads / kWave;
+    int32_t* my_list = s_cnt + A + wave * A;
     const size_t base = (size_t)env * A;
-    for (int a = tid; a < A; a += kEdgeThreads) {
-        const int x = (int16_t)m.pyg_pos[(base + a) * 2];
-        const int y = (int16_t)m.pyg_pos[(base + a) * 2 + 1];
-        s_xy[a] = (x & 0xFFFF) | (y << 16);
+    for (int a = tid; a < padded; a += kEdgeThreads) {
+        int32_t xy = 0x40004000;  // padding: (16384, 16384)
+        if (a < A) {
+            const float2 p = reinterpret_cast<const float2*>(m.pyg_pos)[base + a];
+            const int x = (int16_t)p.x, y = (int16_t)p.y;
+            xy = (x & 0xFFFF) | (y << 16);
+            s_cnt[a] = m.edge_counts[base + a];
+        }
+        s_xy[a] = xy;
     }
+    const long long env_base = m.env_edge_base[env];
+    __syncthreads();
     // counts of the agents before the slice
     long long before = 0;
-    for (int a = tid; a < s_begin; a += kEdgeThreads) before += m.edge_counts[base + a];
+    for (int a = tid; a < s_begin; a += kEdgeThreads) before += s_cnt[a];
     for (int off = kWave / 2; off > 0; off >>= 1) before += __shfl_xor(before, off, kWave);
     if (lane == 0) s_wave[wave] = before;
     __syncthreads();
     if (wave == 0) {
-        long long first = m.env_edge_base[env];
+        long long first = env_base;
         for (int k = 0; k < nwaves; ++k) first += s_wave[k];
         const int a = s_begin + lane;
-        const long long c = a < s_end ? m.edge_counts[base + a] : 0;
+        const long long c = a < s_end ? s_cnt[a] : 0;
         long long incl = c;
         for (int off = 1; off < kWave; off <<= 1) {
             const long long t = __shfl_up(incl, off, kWave);
@@ -384,33 +407,54 @@ __global__ __launch_bounds__(kEdgeThreads) void edges_kernel(jl_magat_t m) {
     }
     __syncthreads();
     const long long cap = m.edge_capacity;
+    int64_t* dst_index = m.edge_index + cap;
     for (int a = s_begin + wave; a < s_end; a += nwaves) {
-        long long out = s_first[a - s_begin];
-        const int cx = (int16_t)(s_xy[a] & 0xFFFF), cy = s_xy[a] >> 16;
-        for (int o0 = 0; o0 < A; o0 += kWave) {
-            const int o = o0 + lane;
-            int dx = 0, dy = 0;
-            bool near = false;
-            if (o < A && o != a) {
-                dx = cx - (int16_t)(s_xy[o] & 0xFFFF);
-                dy = cy - (s_xy[o] >> 16);
-                near = dx * dx + dy * dy <= kCommRadiusSq;
+        const long long first = s_first[a - s_begin];
+        const int32_t sxy = s_xy[a];
+        const int cx = (int16_t)(sxy & 0xFFFF), cy = sxy >> 16;
+        int n = 0;
+        for (int o0 = 0; o0 < padded; o0 += kEdgeSpan) {
+            const int32_t* row = s_xy + o0 + lane;
+            uint64_t bal[kEdgeUnroll];
+#pragma unroll
+            for (int u = 0; u < kEdgeUnroll; ++u) {
+                const int32_t oxy = row[u * kWave];
+                const int dx = cx - (int16_t)(oxy & 0xFFFF);
+                const int dy = cy - (oxy >> 16);
+                bal[u] = __ballot(dx * dx + dy * dy <= kCommRadiusSq);
+                // the source itself
+                const int self = a - (o0 + u * kWave);
+                if (self >= 0 && self < kWave) bal[u] &= ~(1ull << self);
             }
-            const uint64_t bal = __ballot(near);
-            if (near) {
-                const long long e = out + __builtin_amdgcn_mbcnt_hi(
-                                              (uint32_t)(bal >> 32),
-                                              __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0u));
-                if (e >= 0 && e < cap) {
-                    m.edge_index[e] = (int64_t)(base + a);
-                    m.edge_index[cap + e] = (int64_t)(base + o);
-                    m.edge_attr[e * 3] = (float)dx;
-                    m.edge_attr[e * 3 + 1] = (float)dy;
-                    m.edge_attr[e * 3 + 2] = (float)((dx < 0 ? -dx : dx) + (dy < 0 ? -dy : dy));
+#pragma unroll
+            for (int u = 0; u < kEdgeUnroll; ++u) {
+                if (bal[u]) {
+                    if ((bal[u] >> lane) & 1ull)
+                        my_list[n + (int)__builtin_amdgcn_mbcnt_hi(
+                                        (uint32_t)(bal[u] >> 32),
+                                        __builtin_amdgcn_mbcnt_lo((uint32_t)bal[u], 0u))] =
+                            o0 + u * kWave + lane;
+                    n += __popcll(bal[u]);
                 }
             }
-            out += __popcll(bal);
         }
+        wave_sync();
+        for (int i = lane; i < n; i += kWave) {
+            const int o = my_list[i];
+            const long long e = first + i;
+            if (e >= 0 && e < cap) {
+                const int32_t oxy = s_xy[o];
+                const int dx = cx - (int16_t)(oxy & 0xFFFF);
+                const int dy = cy - (oxy >> 16);
+                m.edge_index[e] = (int64_t)(base + a);
+                dst_index[e] = (int64_t)(base + o);
+                float* attr = m.edge_attr + e * 3;
+                attr[0] = (float)dx;
+                attr[1] = (float)dy;
+                attr[2] = (float)((dx < 0 ? -dx : dx) + (dy < 0 ? -dy : dy));
+            }
+        }
+        wave_sync();  // the list is rewritten by the next source
     }
 }
 
@@ -462,7 +506,9 @@ extern "C" int jl_magat_edges(const jl_magat_t* m, jl_stream_t stream) {
     rc = launch_status();
     if (rc) return rc;
     const unsigned eparts = (unsigned)((m->n_agents + kEdgeSources - 1) / kEdgeSources);
-    hipLaunchKernelGGL(edges_kernel, dim3((unsigned)m->n_envs * eparts), dim3(kEdgeThreads),
-                       (size_t)m->n_agents * 4, (hipStream_t)stream, *m);
+    const size_t elds = edge_lds(m->n_agents);
+    if (elds > 160 * 1024) return JL_ERR_ARG;
+    hipLaunchKernelGGL(edges_kernel, dim3((unsigned)m->n_envs * eparts), dim3(kEdgeThreads), elds,
+                       (hipStream_t)stream, *m);
     return launch_status();
 }

@@ -359,7 +359,7 @@ __global__ __launch_bounds__(kTokThreads) void tokens_kernel(jl_mapfgpt_t b) {
     const int e_end = (e_begin + kEgosPerBlock) < A ? (e_begin + kEgosPerBlock) : A;
     const int tid = threadIdx.x;
     const int lane = tid & (kWave - 1);
-    const int wave = tid / kWave;
+    const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);  // uniform per wavefront
     const TokLayout L = tok_layout(A, W, H);
     constexpr int MH = H + 2 * kRadius;  // dense map columns
     uint32_t* s_map = reinterpret_cast<uint32_t*>(smem + L.map_off);

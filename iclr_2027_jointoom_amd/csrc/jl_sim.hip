@@ -683,7 +683,8 @@ __global__ __launch_bounds__(kScanThreads) void goal_changed_scan_kernel(jl_sim_
                                                                          uint16_t* changed) {
     __shared__ int64_t s_wave[kScanThreads / kWave];
     __shared__ int64_t s_out[kScanChunk];
-    const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
+    const int tid = threadIdx.x, lane = tid & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);  // uniform per wavefront
     const int64_t N = (int64_t)s.n_envs * s.n_agents;
     const int64_t c0 = (int64_t)blockIdx.x * kScanChunk;
     const uint8_t* f = s.goal_changed;
