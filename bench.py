@@ -18,6 +18,12 @@ Prints one JSON line with the metric, a `roofline` object for the token
 kernel (algorithmic bytes / event-timed duration) and a `cpu_baseline`
 object (the Python restatement of the reference's cached CPU builder +
 step resolver on this host's cores, oracle/host_builder.py).
+
+`--workload magat` measures BASELINE.json's C4 instead (the MAGAT stateful
+step of fixed_magat_plus_runtime.py: step_sim_only -> update_derived_state ->
+build_magat_plus_nodes -> finalize_magat_plus_graph, plus update_actions) at
+512 envs x 256 agents on 64x64 maps with obstacle density 0.3, with the node
+kernel's roofline and the C restatement of the same step as CPU baseline.
 """
 from __future__ import annotations
 
@@ -41,9 +47,13 @@ PEAK_HBM_BPS = 8.0e12
 # WRITE_SIZE on this workload, scaled by the copy calibration (file header).
 TRAFFIC_FILE = ROOT / "profiles" / "tokens_kernel_pmc_1024x128_64.txt"
 
+MAGAT_TRAFFIC_FILE = ROOT / "profiles" / "magat_nodes_pmc_512x256_64.txt"
+
 # Algorithmic bytes per agent (derivation in DESIGN.md).
 B_TOKEN_KERNEL = 8 + 10 + 242 + 1024 + 1  # pos+goal, history, 11x11 u16 window, tokens, mask
 B_STEP_NORTH_STAR = 1385  # step + token build + append + update_actions per agent-step
+# MAGAT node pass: state row, bitmaps share, 11x11 u8 window, 676-float row, pos, count
+B_MAGAT_NODES = 16 + 4 + 121 + 2704 + 8 + 4
 
 
 def cpu_baseline(args) -> dict:
@@ -113,10 +123,10 @@ class HipEvents:
         return float(ms.value)
 
 
-def measured_traffic() -> int | None:
-    """traffic_bytes from the committed PMC summary, or None."""
+def measured_traffic(path: Path = TRAFFIC_FILE) -> int | None:
+    """traffic_bytes from a committed PMC summary, or None."""
     try:
-        for line in TRAFFIC_FILE.read_text().splitlines():
+        for line in path.read_text().splitlines():
             if line.startswith("traffic_bytes="):
                 return int(float(line.split("=", 1)[1]))
     except OSError:
@@ -227,6 +237,146 @@ def run_gpu(args) -> dict:
     }
 
 
+def cpu_baseline_magat(args) -> dict:
+    """The C restatement of the stateful MAGAT step, one env per worker."""
+    from iclr_2027_jointoom_amd.synthetic import make_batch, random_actions
+    from oracle.host_builder import run_magat_worker
+
+    cores = len(os.sched_getaffinity(0))
+    workers = max(1, min(cores, 16))
+    jobs = []
+    for w in range(workers):
+        grids, starts, goals = make_batch(7000 + w, 1, args.map, args.map, args.agents, density=0.3)
+        acts = random_actions(np.random.default_rng(w), args.cpu_steps, 1, args.agents)
+        jobs.append((grids, starts, goals, acts, args.cpu_steps))
+    ctx = mp.get_context("fork")  # before any HIP call in this process
+    t1 = run_magat_worker(jobs[0])
+    t0 = time.perf_counter()
+    with ctx.Pool(workers) as pool:
+        results = pool.map(run_magat_worker, jobs)
+    wall = time.perf_counter() - t0
+    total = sum(n for _, n in results)
+    timed = max(t for t, _ in results)
+    return {
+        "value": total / timed,
+        "unit": "agent-steps/s",
+        "cores": workers,
+        "kind": "port",
+        "value_1core": t1[1] / t1[0],
+        "sample": (
+            f"{workers} workers x 1 env x {args.agents} agents on {args.map}x{args.map} p=0.3, "
+            f"{args.cpu_steps} steps each: C restatement (oracle/jl_oracle.c) of step, occupancy, "
+            f"nodes and edges; pool wall {wall:.1f}s"
+        ),
+    }
+
+
+def run_gpu_magat(args) -> dict:
+    import torch
+
+    from iclr_2027_jointoom_amd import profile
+    from iclr_2027_jointoom_amd.synthetic import make_batch
+
+    E, A, W = args.envs, args.agents, args.map
+    print(f"[bench] generating {E} maps {W}x{W} (p=0.3), {A} agents", file=sys.stderr, flush=True)
+    grids, starts, goals = make_batch(args.seed, E, W, W, A, density=0.3)
+    dev = torch.device("cuda:0")
+    g = torch.from_numpy(grids.astype(np.int32)).to(dev)
+    sim = profile(W, W).GridWorldSimulator(g, A, 3, E * W * W, 20260728, "standard_mapf", 1 << 30)
+    sim.load_state(
+        torch.from_numpy(starts).to(dev),
+        torch.from_numpy(goals).to(dev),
+        torch.zeros((E, A), dtype=torch.uint8, device=dev),
+        torch.zeros(E, dtype=torch.int32, device=dev),
+    )
+    total_steps = args.warmup + args.steps
+    gen = torch.Generator(device=dev).manual_seed(args.seed)
+    actions = torch.randint(0, 5, (total_steps, E, A), dtype=torch.uint8, device=dev, generator=gen)
+
+    def one_step(s, ev=None):
+        sim.update_actions(actions[s])
+        sim.step_sim_only()
+        sim.update_derived_state()
+        if ev is not None:
+            ev[0].record()
+        sim.build_magat_plus_nodes()
+        if ev is not None:
+            ev[1].record()
+        sim.finalize_magat_plus_graph()
+
+    print("[bench] warmup (the first step builds every energy field)", file=sys.stderr, flush=True)
+    for s in range(args.warmup):
+        one_step(s)
+    torch.cuda.synchronize()
+    # all kernels run on torch's current stream, so torch events bracket the node pass
+    node_events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+                   for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        one_step(args.warmup + i, node_events[i])
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    node_ms = [a.elapsed_time(b) for a, b in node_events]
+    N = E * A
+    value = N * args.steps / wall
+    node_s = float(np.mean(node_ms)) / 1000.0
+    node_bytes = B_MAGAT_NODES * N
+    achieved = node_bytes / node_s
+    return {
+        "value": value,
+        "ms_per_step": wall * 1000.0 / args.steps,
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "nodes_kernel<64>",
+            "achieved": achieved / 1e9,
+            "peak": PEAK_HBM_BPS / 1e9,
+            "unit": "GB/s",
+            "frac": achieved / PEAK_HBM_BPS,
+            "traffic": measured_traffic(MAGAT_TRAFFIC_FILE),
+            "bytes_per_launch": node_bytes,
+            "avg_launch_us": node_s * 1e6,
+        },
+        "edges_per_step": int(sim.pyg_num_edges.item()),
+        "device": torch.cuda.get_device_name(0),
+    }
+
+
+def main_magat(args) -> int:
+    base = None
+    if not args.no_cpu_baseline:
+        print("[bench] cpu baseline", file=sys.stderr, flush=True)
+        base = cpu_baseline_magat(args)
+    res = run_gpu_magat(args)
+    line = {
+        "metric": "agent-steps/sec incl. obs/token build on 1 GPU; % of HBM roofline",
+        "value": res["value"],
+        "unit": "agent-steps/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": res["ms_per_step"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int16/int32 (integer) + float32 node features",
+        "data": "synthetic (seeded i.i.d. maps p=0.3, largest component; distinct starts/goals; uniform random actions)",
+        "config": {
+            "workload": "MAGAT stateful step + FOV/graph build (C4)",
+            "envs": args.envs,
+            "agents": args.agents,
+            "map": f"{args.map}x{args.map}",
+            "task_mode": "standard_mapf",
+        },
+        "roofline": res["roofline"],
+        "cpu_baseline": base,
+        "edges_per_step": res["edges_per_step"],
+        "device": res["device"],
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
 def main() -> int:
     p = argparse.ArgumentParser(description=__doc__.split("\n", 1)[0])
     p.add_argument("--gpus", type=int, default=1)
@@ -241,7 +391,19 @@ def main() -> int:
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--copy-calibration", action="store_true",
                    help="only run 3 device copies of 256 MiB (PMC byte-counter calibration)")
+    p.add_argument("--workload", choices=("resident", "magat"), default="resident",
+                   help="resident: the north-star MAPF-GPT loop (C2+C3); magat: the C4 MAGAT stateful step")
     args = p.parse_args()
+    if args.workload == "magat":
+        # C4 defaults unless given explicitly
+        if "--envs" not in sys.argv:
+            args.envs = 512
+        if "--agents" not in sys.argv:
+            args.agents = 256
+        if "--steps" not in sys.argv:
+            args.steps = 50
+        if "--cpu-steps" not in sys.argv:
+            args.cpu_steps = 2000  # ~2 s per worker of the C restatement
     if args.copy_calibration:
         copy_calibration()
         return 0
@@ -252,6 +414,8 @@ def main() -> int:
             file=sys.stderr,
         )
         return 2
+    if args.workload == "magat":
+        return main_magat(args)
     base = None
     if not args.no_cpu_baseline:
         print("[bench] cpu baseline", file=sys.stderr, flush=True)

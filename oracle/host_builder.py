@@ -13,7 +13,9 @@ that its timing is a fair baseline:
   (expert/transition_adapters.py:361-455) plus the standard-MAPF bookkeeping
   of _predict_backend_step (:663-707);
 * ``run_stage_worker`` runs one whole stage (all envs of the sample) per
-  worker process, as HostPrefetch does (host_inputs.py:181-232).
+  worker process, as HostPrefetch does (host_inputs.py:181-232);
+* ``run_magat_worker`` does the same for the stateful MAGAT step with the C
+  restatement of the step, occupancy, node and edge passes.
 """
 from __future__ import annotations
 
@@ -201,4 +203,29 @@ def run_stage_worker(args):
             new_pos, new_arr = resolve_step(grids[e], pos[e], goals[e], arrived[e], act[e])
             pos[e] = new_pos
             arrived[e] = new_arr
+    return time.perf_counter() - t0, E * A * steps
+
+
+def run_magat_worker(args):
+    """Worker body: `steps` stateful MAGAT steps of one stage (step, occupancy
+    refresh, nodes, edges; goals are fixed in standard_mapf, so no energy
+    refresh after the first) with the C restatement, oracle/jl_oracle.c."""
+    grids, starts, goals, actions, steps = args
+    import time
+
+    from oracle.oracle import OracleMagat, OracleSim
+
+    E, A = starts.shape[:2]
+    osim = OracleSim(grids, A, task_mode=1, max_episode_steps=1 << 30)
+    osim.load_state(starts, goals)
+    m = OracleMagat(grids, A)
+    rows = osim.state_packed.copy()
+    rows[:, 7] = 1
+    m.update_energy(rows, len(rows))  # every goal fresh (untimed)
+    t0 = time.perf_counter()
+    for s in range(steps):
+        osim.step(actions[s])
+        m.refresh(osim.state_packed)
+        m.nodes()
+        m.edges()
     return time.perf_counter() - t0, E * A * steps
