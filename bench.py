@@ -176,17 +176,28 @@ def run_gpu(args) -> dict:
     actions = torch.randint(0, 5, (total_steps, E, A), dtype=torch.uint8, device=dev, generator=gen)
     hip = HipEvents()
 
-    def one_step(s):
+    def eager_step(s):
         builder.build_tokens_from_state(sim.cur_x, sim.cur_y, sim.goal_x, sim.goal_y)
         a = actions[s]
         builder.append_actions(a)
         sim.update_actions(a)
         sim.step_sim_only()
 
+    one_step = eager_step
+    graph = None
+
     print("[bench] warmup (first build refreshes every goal)", file=sys.stderr, flush=True)
     for s in range(args.warmup):
         one_step(s)
     torch.cuda.synchronize()
+    if args.graph:
+        from iclr_2027_jointoom_amd.graphs import MapfGPTResidentGraph
+
+        graph = MapfGPTResidentGraph(sim, builder)
+
+        def one_step(s):
+            graph.actions.copy_(actions[s])
+            graph.replay()
     diag = builder.diagnostics.cpu().tolist()
     if any(diag):
         raise RuntimeError(f"builder diagnostics non-zero after warmup: {diag}")
@@ -198,13 +209,24 @@ def run_gpu(args) -> dict:
     t0 = time.perf_counter()
     start.record()
     for i in range(args.steps):
-        builder._desc.token_events[0], builder._desc.token_events[1] = tok_events[i]
+        if graph is None:
+            builder._desc.token_events[0], builder._desc.token_events[1] = tok_events[i]
         one_step(args.warmup + i)
     end.record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     builder._desc.token_events[0] = builder._desc.token_events[1] = None
     gpu_ms = start.elapsed_time(end)
+    if graph is not None:
+        # events cannot be recorded inside the graph: time the token kernel on
+        # eager steps after the timed region
+        n_ev = min(args.steps, 20)
+        tok_events = tok_events[:n_ev]
+        for i in range(n_ev):
+            builder._desc.token_events[0], builder._desc.token_events[1] = tok_events[i]
+            eager_step((args.warmup + i) % total_steps)
+        torch.cuda.synchronize()
+        builder._desc.token_events[0] = builder._desc.token_events[1] = None
     tok_ms = [hip.elapsed_ms(a, b) for a, b in tok_events]
     diag = builder.diagnostics.cpu().tolist()
     if any(diag):
@@ -308,15 +330,31 @@ def run_gpu_magat(args) -> dict:
     for s in range(args.warmup):
         one_step(s)
     torch.cuda.synchronize()
+    graph = None
+    if args.graph:
+        from iclr_2027_jointoom_amd.graphs import MagatStatefulGraph
+
+        graph = MagatStatefulGraph(sim)
     # all kernels run on torch's current stream, so torch events bracket the node pass
     node_events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
                    for _ in range(args.steps)]
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(args.steps):
-        one_step(args.warmup + i, node_events[i])
+        if graph is None:
+            one_step(args.warmup + i, node_events[i])
+        else:
+            graph.actions.copy_(actions[args.warmup + i])
+            graph.replay()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
+    if graph is not None:
+        # events cannot be recorded inside the graph: time the node pass on
+        # eager steps after the timed region
+        node_events = node_events[: min(args.steps, 20)]
+        for i, ev in enumerate(node_events):
+            one_step((args.warmup + i) % total_steps, ev)
+        torch.cuda.synchronize()
     node_ms = [a.elapsed_time(b) for a, b in node_events]
     N = E * A
     value = N * args.steps / wall
@@ -363,6 +401,7 @@ def main_magat(args) -> int:
         "data": "synthetic (seeded i.i.d. maps p=0.3, largest component; distinct starts/goals; uniform random actions)",
         "config": {
             "workload": "MAGAT stateful step + FOV/graph build (C4)",
+            "launch": "hip-graph replay" if args.graph else "eager",
             "envs": args.envs,
             "agents": args.agents,
             "map": f"{args.map}x{args.map}",
@@ -391,6 +430,8 @@ def main() -> int:
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--copy-calibration", action="store_true",
                    help="only run 3 device copies of 256 MiB (PMC byte-counter calibration)")
+    p.add_argument("--graph", action="store_true",
+                   help="replay each step from a captured HIP graph (iclr_2027_jointoom_amd/graphs.py)")
     p.add_argument("--workload", choices=("resident", "magat"), default="resident",
                    help="resident: the north-star MAPF-GPT loop (C2+C3); magat: the C4 MAGAT stateful step")
     args = p.parse_args()
@@ -436,6 +477,7 @@ def main() -> int:
         "data": "synthetic (seeded i.i.d. maps p=0.2, largest component; distinct starts/goals; uniform random actions)",
         "config": {
             "workload": "resident step + MAPF-GPT token build (C2+C3 shape)",
+            "launch": "hip-graph replay" if args.graph else "eager",
             "envs": args.envs,
             "agents": args.agents,
             "map": f"{args.map}x{args.map}",
