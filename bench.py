@@ -157,7 +157,7 @@ def run_gpu(args) -> dict:
 
     E, W, A = args.envs, args.map, args.agents
     print(f"[bench] generating {E} maps {W}x{W}, {A} agents", file=sys.stderr, flush=True)
-    grids, starts, goals = make_batch(args.seed, E, W, W, A)
+    grids, starts, goals = make_batch(args.seed, E, W, W, A, kind=args.map_kind)
     dev = torch.device("cuda:0")
     ext = profile(W, W)
     g = torch.from_numpy(grids.astype(np.int32)).to(dev)
@@ -244,12 +244,13 @@ def run_gpu(args) -> dict:
         "gpu_ms_per_step": gpu_ms / args.steps,
         "roofline": {
             "bound": "hbm",
-            "kernel": "tokens_kernel<64>",
+            "kernel": f"tokens_kernel<{W}>",
             "achieved": achieved / 1e9,
             "peak": PEAK_HBM_BPS / 1e9,
             "unit": "GB/s",
             "frac": achieved / PEAK_HBM_BPS,
-            "traffic": measured_traffic(),
+            # the committed PMC summary is for the default workload only
+            "traffic": measured_traffic() if (E, A, W, args.map_kind) == (1024, 128, 64, "iid") else None,
             "bytes_per_launch": tok_bytes,
             "avg_launch_us": tok_avg_s * 1e6,
         },
@@ -366,12 +367,12 @@ def run_gpu_magat(args) -> dict:
         "ms_per_step": wall * 1000.0 / args.steps,
         "roofline": {
             "bound": "hbm",
-            "kernel": "nodes_kernel<64>",
+            "kernel": f"nodes_kernel<{W}>",
             "achieved": achieved / 1e9,
             "peak": PEAK_HBM_BPS / 1e9,
             "unit": "GB/s",
             "frac": achieved / PEAK_HBM_BPS,
-            "traffic": measured_traffic(MAGAT_TRAFFIC_FILE),
+            "traffic": measured_traffic(MAGAT_TRAFFIC_FILE) if (E, A, W) == (512, 256, 64) else None,
             "bytes_per_launch": node_bytes,
             "avg_launch_us": node_s * 1e6,
         },
@@ -432,9 +433,21 @@ def main() -> int:
                    help="only run 3 device copies of 256 MiB (PMC byte-counter calibration)")
     p.add_argument("--graph", action="store_true",
                    help="replay each step from a captured HIP graph (iclr_2027_jointoom_amd/graphs.py)")
-    p.add_argument("--workload", choices=("resident", "magat"), default="resident",
-                   help="resident: the north-star MAPF-GPT loop (C2+C3); magat: the C4 MAGAT stateful step")
+    p.add_argument("--workload", choices=("resident", "magat", "c5"), default="resident",
+                   help="resident: the north-star MAPF-GPT loop (C2+C3); magat: the C4 MAGAT stateful "
+                        "step; c5: the resident loop at C5 (256 envs x 1024 agents, 256x256 warehouses)")
+    p.add_argument("--map-kind", choices=("iid", "maze", "warehouse"), default="iid")
     args = p.parse_args()
+    if args.workload == "c5":
+        for flag, name, value in (("--envs", "envs", 256), ("--agents", "agents", 1024),
+                                  ("--map", "map", 256), ("--map-kind", "map_kind", "warehouse"),
+                                  ("--steps", "steps", 50), ("--warmup", "warmup", 3),
+                                  ("--cpu-envs", "cpu_envs", 1), ("--cpu-steps", "cpu_steps", 2)):
+            if flag not in sys.argv:
+                setattr(args, name, value)
+        # the Python CPU builder needs minutes for one 256x256 env's first
+        # 1024 BFS fields: no CPU baseline on this line
+        args.no_cpu_baseline = True
     if args.workload == "magat":
         # C4 defaults unless given explicitly
         if "--envs" not in sys.argv:
@@ -474,9 +487,17 @@ def main() -> int:
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "int16/int32 (integer)",
-        "data": "synthetic (seeded i.i.d. maps p=0.2, largest component; distinct starts/goals; uniform random actions)",
+        "data": (
+            "synthetic (seeded "
+            + {"iid": "i.i.d. maps p=0.2", "maze": "recursive-backtracker mazes",
+               "warehouse": "warehouse maps (2x8 shelves, 2-wide aisles)"}[args.map_kind]
+            + ", largest component; distinct starts/goals; uniform random actions)"
+        ),
         "config": {
-            "workload": "resident step + MAPF-GPT token build (C2+C3 shape)",
+            "workload": (
+                "resident step + MAPF-GPT token build (C5 shape)" if args.workload == "c5"
+                else "resident step + MAPF-GPT token build (C2+C3 shape)"
+            ),
             "launch": "hip-graph replay" if args.graph else "eager",
             "envs": args.envs,
             "agents": args.agents,
