@@ -1,21 +1,22 @@
 // jl_mapfgpt.hip - MAPF-GPT observation builder for gfx950.
 //
-// A build is two launches:
-//   1. unpack_bfs: one lane per agent, 1-4 wavefronts per workgroup.  Unpacks
-//      the state (raw rows or resident split arrays), refreshes the goal
-//      cache, runs the bit-parallel BFS (jl_bfs.h) for each agent whose reset
-//      flag is set in the wavefront's own LDS region, stores the field both
-//      row-major (cost_to_go, the API tensor) and in 8x8 tiles (cost_tiles),
-//      and writes every agent's info word: greedy-move mask + diagnostic
-//      flags.  It also clears `diagnostics` for the build.
-//   2. tokens: one 512-thread workgroup per env.  Phase 1 stages the env's
-//      agents (position, goal, history, greedy mask) and a cell -> agent map
-//      in LDS and sums the env's diagnostics.  Phase 2 takes the egos in
-//      chunks: all threads gather the chunk's 11x11 windows from the tiled
-//      fields into LDS (the next chunk's loads are in flight while the
-//      current chunk is turned into tokens), then one wavefront per ego ranks
-//      the visible agents with ballots and writes the 1 KB token row as
-//      64 x 16-byte stores.
+// A build is three launches (two on maps of up to 4096 cells, where 1a and
+// 1b are one kernel):
+//   1a. unpack: one lane per agent, no LDS.  Unpacks the state (raw rows or
+//      resident split arrays), refreshes the goal cache and writes every
+//      agent's info word: the greedy-move mask from the kept tiled field, or a
+//      mark when the reset flag is set.  It also clears `diagnostics`.
+//   1b. bfs: a grid sized to the CUs; each wavefront scans a range of info
+//      words and runs the bit-parallel BFS (jl_bfs.h) for the marked agents
+//      in its own LDS field, stores the field row-major (cost_to_go, the API
+//      tensor) and in 8x8 tiles (cost_tiles), and completes the info word.
+//   2. tokens: one 1024-thread workgroup per 128 egos of an env.  Phase 1
+//      stages the env's agents (position, goal, the six ego-independent
+//      tokens) and a cell -> agent map in LDS and sums the env's diagnostics.
+//      Phase 2: every wavefront on its own gathers the 11x11 windows of its
+//      next ego pair from the tiled fields while it turns the current pair
+//      into tokens (visible agents ranked with ballots), each row assembled
+//      in LDS and written as 64 x 16-byte stores.
 // The reference runs four kernels plus a 16 KB/env memset per build
 // (mapf_gpt_builder.cpp:108-110, mapf_gpt_cuda.cu:544-610) with the
 // top-13 search done serially by one lane per ego (:395-496) and every
@@ -106,9 +107,178 @@ __device__ __forceinline__ uint32_t tile_offset(int x, int y) {
 }
 
 // ---------------------------------------------------------------------------
-// Pass 1: unpack + goal-cache refresh + BFS of refreshed goals + agent info.
-// kRows: raw 13-column rows (mapf_gpt_unpack_kernel, mapf_gpt_cuda.cu:75-118);
-// otherwise resident split arrays (mapf_gpt_state_unpack_kernel, :121-152).
+// Pass 1a: unpack + goal-cache refresh + agent info, one lane per agent, no
+// LDS.  kRows: raw 13-column rows (mapf_gpt_unpack_kernel,
+// mapf_gpt_cuda.cu:75-118); otherwise resident split arrays
+// (mapf_gpt_state_unpack_kernel, :121-152).  An agent whose field is kept
+// gets its greedy mask from the tiled field; one whose reset flag is set is
+// marked for pass 1b.
+// ---------------------------------------------------------------------------
+constexpr uint32_t kInfoNeedsBfs = 1u << 6;  // agent_info: field to refresh in pass 1b
+constexpr int kUnpackThreads = 256;
+
+template <int H, bool kRows>
+__global__ __launch_bounds__(kUnpackThreads) void unpack_kernel(
+    jl_mapfgpt_t b, const int16_t* __restrict__ raw_rows, const int16_t* __restrict__ cur_x,
+    const int16_t* __restrict__ cur_y, const int16_t* __restrict__ goal_x,
+    const int16_t* __restrict__ goal_y) {
+    const int A = b.n_agents, W = b.map_w;
+    const int N = b.n_envs * A;
+    const int i = blockIdx.x * kUnpackThreads + threadIdx.x;
+    // the build's diagnostics start from zero; pass 2 and append_actions add
+    if (blockIdx.x == 0 && threadIdx.x < 4) b.diagnostics[threadIdx.x] = 0;
+    if (i >= N) return;
+
+    bool reset = false;
+    uint32_t px = kUnreachable, py = kUnreachable;  // position of the row this lane now holds
+    uint32_t info = 0;
+    uint16_t* st = b.state_packed + (size_t)i * 8;
+    if (kRows) {
+        const uint16_t* row = reinterpret_cast<const uint16_t*>(raw_rows) + (size_t)i * 13;
+        uint16_t c[13];
+#pragma unroll
+        for (int k = 0; k < 13; ++k) c[k] = row[k];
+        if (c[0] >= b.n_envs || c[1] >= A || i != (int)c[0] * A + c[1]) {
+            // rejected row: every output of this agent keeps its old value,
+            // including the reset flag the BFS pass reads (:90-92, :186-189)
+            info = kInfoBadRow;
+            const uint4 old = *reinterpret_cast<const uint4*>(st);
+            px = old.y & 0xFFFFu;
+            py = old.y >> 16;
+            reset = (old.w >> 16) != 0;
+        } else {
+            uint16_t* gc = b.goal_cache + (size_t)i * 2;
+            const uint32_t cache = *reinterpret_cast<const uint32_t*>(gc);
+            const uint32_t goal = (uint32_t)c[4] | ((uint32_t)c[5] << 16);
+            const bool changed = cache != goal;
+            if (changed) *reinterpret_cast<uint32_t*>(gc) = goal;
+            reset = c[7] != 0 || changed;
+            px = c[2];
+            py = c[3];
+            store_state_row(st, c[0], c[1], c[2], c[3], c[4], c[5], c[6], reset ? 1u : 0u);
+            uint16_t* h = b.histories + (size_t)i * 5;
+#pragma unroll
+            for (int k = 0; k < 5; ++k) h[k] = c[8 + k];
+            b.labels[i] = (int64_t)c[6];
+        }
+    } else {
+        const uint32_t env = (uint32_t)(i / A);
+        const uint32_t agent = (uint32_t)(i - (int)env * A);
+        px = (uint16_t)cur_x[i];
+        py = (uint16_t)cur_y[i];
+        const uint32_t tx = (uint16_t)goal_x[i], ty = (uint16_t)goal_y[i];
+        uint16_t* gc = b.goal_cache + (size_t)i * 2;
+        const uint32_t cache = *reinterpret_cast<const uint32_t*>(gc);
+        const uint32_t goal = tx | (ty << 16);
+        reset = cache != goal;
+        if (reset) *reinterpret_cast<uint32_t*>(gc) = goal;
+        store_state_row(st, env, agent, px, py, tx, ty, 0u, reset ? 1u : 0u);
+        b.labels[i] = 0;
+    }
+    if (reset) {
+        info |= kInfoNeedsBfs;
+    } else if (px < (uint32_t)W && py < (uint32_t)H) {
+        // a kept field is read from the tiled copy (written by an earlier
+        // build), where the cross of five cells spans 1-3 lines
+        const uint16_t* f = b.cost_tiles + (size_t)i * tiled_cells(W, H);
+        info |= greedy_mask<H>([f](int x, int y) { return (uint32_t)f[tile_offset<H>(x, y)]; },
+                               (int)px, (int)py, W);
+    }
+    b.agent_info[i] = info;
+}
+
+// ---------------------------------------------------------------------------
+// Pass 1b: BFS of the marked agents (mapf_gpt_cost_to_go_kernel, :181-325).
+// A fixed grid sized to the CUs the LDS fields allow; wavefront g scans agents
+// [g * per_wave, (g + 1) * per_wave) for the mark, so a build without a
+// changed goal costs one scan of agent_info.  Each refresh runs the
+// bit-parallel BFS (jl_bfs.h) in the wavefront's LDS field, stores it
+// row-major (cost_to_go, the API tensor) and in 8x8 tiles (cost_tiles), and
+// completes the agent's info word (greedy mask, overflow count or bad goal).
+// ---------------------------------------------------------------------------
+template <int H, int R, int kWaves>
+__global__ __launch_bounds__(kWave* kWaves) void bfs_kernel(jl_mapfgpt_t b, int per_wave) {
+    extern __shared__ __align__(16) uint16_t s_dist_all[];
+    const int A = b.n_agents, W = b.map_w;
+    const int N = b.n_envs * A;
+    (void)A;
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    const int cells = W * H;
+    uint16_t* s_dist = s_dist_all + (size_t)wave * cells;  // this wavefront's field
+    constexpr int HW = RowWords<H>::HW;
+    const int words = cells / 32;
+    const size_t tcells = tiled_cells(W, H);
+    const int begin = (blockIdx.x * kWaves + wave) * per_wave;
+    const int end = (begin + per_wave) < N ? (begin + per_wave) : N;
+    for (int c0 = begin; c0 < end; c0 += kWave) {
+        const int i = c0 + lane;
+        const uint32_t mine = i < end ? b.agent_info[i] : 0u;
+        uint64_t todo = __ballot((mine & kInfoNeedsBfs) != 0);
+        while (todo) {
+            const int src = __ffsll((unsigned long long)todo) - 1;
+            todo &= todo - 1;
+            const size_t agent_index = (size_t)c0 + src;
+            // the agent's state row as pass 1a left it
+            const uint4 row = *reinterpret_cast<const uint4*>(b.state_packed + agent_index * 8);
+            const uint32_t e = row.x & 0xFFFFu;
+            const int spx = (int)(row.y & 0xFFFFu), spy = (int)(row.y >> 16);
+            const int gx = (int)(row.z & 0xFFFFu), gy = (int)(row.z >> 16);
+            for (int c = lane; c < cells; c += kWave) s_dist[c] = kUnreachable;
+            wave_sync();
+            bool ok = e < (uint32_t)b.n_envs && gx < W && gy < H;
+            const uint32_t* env_bits = b.grid_bits + (size_t)(ok ? e : 0) * words;
+            if (ok && bit_at(env_bits, gx * H + gy)) ok = false;
+            int overflow = 0;
+            if (ok) {
+                uint64_t fr[R][HW];
+                load_free_rows<H, R>(env_bits, W, fr);
+                if (lane == 0) s_dist[gx * H + gy] = 0;
+                wave_sync();
+                if (W * H > kMaxFrontier + 1) {
+                    overflow = wave_bfs<H, R, uint16_t, true>(fr, gx, gy, 0x7FFFFFFF, s_dist);
+                } else {
+                    overflow = wave_bfs<H, R, uint16_t, false>(fr, gx, gy, 0x7FFFFFFF, s_dist);
+                }
+            }
+            wave_sync();
+            if (lane == src) {
+                // goal off the map or on an obstacle: all-unreachable field (:224-236)
+                uint32_t info = mine & ~(kInfoNeedsBfs | kInfoGreedy);
+                info |= ok ? (uint32_t)(overflow < 0xFFFFFF ? overflow : 0xFFFFFF) << kInfoOverflowShift
+                           : kInfoBadGoal;
+                if (spx < W && spy < H)
+                    info |= greedy_mask<H>([s_dist](int x, int y) { return (uint32_t)s_dist[x * H + y]; },
+                                           spx, spy, W);
+                b.agent_info[agent_index] = info;
+            }
+            // row-major field (the API tensor) and the tiled copy, 16-byte stores
+            const uint4* lds4 = reinterpret_cast<const uint4*>(s_dist);
+            uint4* out = reinterpret_cast<uint4*>(b.cost_to_go + agent_index * (size_t)cells);
+            for (int c = lane; c < cells / 8; c += kWave) out[c] = lds4[c];
+            uint4* tout = reinterpret_cast<uint4*>(b.cost_tiles + agent_index * tcells);
+            for (int c = lane; c < (int)(tcells / 8); c += kWave) {
+                const int t = c >> 3, r = c & 7;  // tile, row inside the tile
+                const int x = (t / (H / 8)) * 8 + r, y0 = (t % (H / 8)) * 8;
+                const bool in = x < W;  // rows past the map in the last tile row: unreachable
+                uint4 v = lds4[((in ? x : 0) * H + y0) >> 3];
+                v.x = in ? v.x : 0xFFFFFFFFu;
+                v.y = in ? v.y : 0xFFFFFFFFu;
+                v.z = in ? v.z : 0xFFFFFFFFu;
+                v.w = in ? v.w : 0xFFFFFFFFu;
+                tout[c] = v;
+            }
+            wave_sync();  // the LDS field is rewritten by the next refresh
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Pass 1 for small maps (a field of at most kCombinedField bytes): 1a and 1b
+// in one launch, one lane per agent and 4 wavefronts per workgroup, each
+// wavefront refreshing the fields of its own marked agents in its LDS field
+// (the fields are small enough not to limit occupancy, and one launch saves
+// a kernel boundary).
 // ---------------------------------------------------------------------------
 template <int H, int R, bool kRows, int kWaves>
 __global__ __launch_bounds__(kWave* kWaves) void unpack_bfs_kernel(
@@ -119,7 +289,7 @@ __global__ __launch_bounds__(kWave* kWaves) void unpack_bfs_kernel(
     const int A = b.n_agents, W = b.map_w;
     const int N = b.n_envs * A;
     const int lane = threadIdx.x & (kWave - 1);
-    const int wave = threadIdx.x / kWave;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
     const int i = blockIdx.x * (kWave * kWaves) + threadIdx.x;
     const int cells = W * H;
     uint16_t* s_dist = s_dist_all + (size_t)wave * cells;  // this wavefront's field
@@ -713,30 +883,58 @@ int check_builder(const jl_mapfgpt_t* b) {
     return JL_OK;
 }
 
-// Pass 1 wavefronts per workgroup: each owns a W*H uint16 LDS field; up to
+// Largest field (bytes) for which pass 1 runs as one launch.
+constexpr size_t kCombinedField = 8192;
+
+// Pass 1b wavefronts per workgroup: each owns a W*H uint16 LDS field; up to
 // 64 KB of them per workgroup, at most 4.
 inline int pass1_waves(int W, int H) {
     const size_t field = (size_t)W * H * 2;
     return field <= 16384 ? 4 : (field <= 32768 ? 2 : 1);
 }
 
+// Compute units of the current device (the BFS grid is sized to them).
+inline int device_cus() {
+    int dev = 0, cus = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return 256;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+        return 256;
+    return cus > 0 ? cus : 256;
+}
+
 template <int H, int R, bool kRows>
 int launch_pass1(const jl_mapfgpt_t* b, const int16_t* rows, const int16_t* cx, const int16_t* cy,
                  const int16_t* gx, const int16_t* gy, hipStream_t stream) {
     const int N = b->n_envs * b->n_agents;
+    if ((size_t)b->map_w * H * sizeof(uint16_t) <= kCombinedField) {
+        const dim3 grid((N + kWave * 4 - 1) / (kWave * 4));
+        const size_t lds = (size_t)4 * b->map_w * H * sizeof(uint16_t);
+        hipLaunchKernelGGL((unpack_bfs_kernel<H, R, kRows, 4>), grid, dim3(kWave * 4), lds, stream,
+                           *b, rows, cx, cy, gx, gy);
+        return launch_status();
+    }
+    hipLaunchKernelGGL((unpack_kernel<H, kRows>), dim3((N + kUnpackThreads - 1) / kUnpackThreads),
+                       dim3(kUnpackThreads), 0, stream, *b, rows, cx, cy, gx, gy);
+    int rc = launch_status();
+    if (rc) return rc;
     const int waves = pass1_waves(b->map_w, H);
     const size_t lds = (size_t)waves * b->map_w * H * sizeof(uint16_t);
-    const int per_block = kWave * waves;
-    const dim3 grid((N + per_block - 1) / per_block);
+    const int per_cu = (int)(160 * 1024 / lds) < 8 ? (int)(160 * 1024 / lds) : 8;
+    // whole-wavefront ranges of at least one wavefront of agents
+    const int max_waves = (N + kWave - 1) / kWave;
+    int total_waves = device_cus() * (per_cu > 0 ? per_cu : 1) * waves;
+    if (total_waves > max_waves) total_waves = max_waves;
+    const int per_wave = ((N + total_waves - 1) / total_waves + kWave - 1) / kWave * kWave;
+    const int blocks = ((N + per_wave - 1) / per_wave + waves - 1) / waves;
     if (waves == 4) {
-        hipLaunchKernelGGL((unpack_bfs_kernel<H, R, kRows, 4>), grid, dim3(per_block), lds, stream,
-                           *b, rows, cx, cy, gx, gy);
+        hipLaunchKernelGGL((bfs_kernel<H, R, 4>), dim3(blocks), dim3(kWave * 4), lds, stream, *b,
+                           per_wave);
     } else if (waves == 2) {
-        hipLaunchKernelGGL((unpack_bfs_kernel<H, R, kRows, 2>), grid, dim3(per_block), lds, stream,
-                           *b, rows, cx, cy, gx, gy);
+        hipLaunchKernelGGL((bfs_kernel<H, R, 2>), dim3(blocks), dim3(kWave * 2), lds, stream, *b,
+                           per_wave);
     } else {
-        hipLaunchKernelGGL((unpack_bfs_kernel<H, R, kRows, 1>), grid, dim3(per_block), lds, stream,
-                           *b, rows, cx, cy, gx, gy);
+        hipLaunchKernelGGL((bfs_kernel<H, R, 1>), dim3(blocks), dim3(kWave), lds, stream, *b,
+                           per_wave);
     }
     return launch_status();
 }
