@@ -448,7 +448,10 @@ __global__ __launch_bounds__(kWave* kWaves) void unpack_bfs_kernel(
 // ---------------------------------------------------------------------------
 constexpr int kTokThreads = 1024;
 constexpr int kTokWaves = kTokThreads / kWave;
-constexpr int kEgosPerBlock = 128;         // egos per workgroup: an env spans ceil(A / 128) workgroups
+// Egos per workgroup: every workgroup stages its whole env, so a workgroup
+// takes the whole env (in steps of 128) up to 1024 egos; larger envs span
+// ceil(A / 1024) workgroups.
+__host__ __device__ inline int ego_slice(int A) { return A > 1024 ? 1024 : (A + 127) / 128 * 128; }
 constexpr int kDenseCellLimit = 16384;     // map cells up to which the agent map is dense
 // A window is read as 11 rows x 3 tile columns of 16-byte tile-row segments
 // (8 cells each): the 11 columns of a row span 2 or 3 tile columns.
@@ -521,12 +524,13 @@ template <int H, bool kDense>
 __global__ __launch_bounds__(kTokThreads) void tokens_kernel(jl_mapfgpt_t b) {
     extern __shared__ __align__(16) uint8_t smem[];
     const int A = b.n_agents, W = b.map_w;
-    // workgroup = (env, slice of kEgosPerBlock egos); every slice stages the whole env
-    const int parts = (A + kEgosPerBlock - 1) / kEgosPerBlock;
+    // workgroup = (env, slice of egos); every slice stages the whole env
+    const int slice = ego_slice(A);
+    const int parts = (A + slice - 1) / slice;
     const int env = blockIdx.x / parts;
     const int part = blockIdx.x - env * parts;
-    const int e_begin = part * kEgosPerBlock;
-    const int e_end = (e_begin + kEgosPerBlock) < A ? (e_begin + kEgosPerBlock) : A;
+    const int e_begin = part * slice;
+    const int e_end = (e_begin + slice) < A ? (e_begin + slice) : A;
     const int tid = threadIdx.x;
     const int lane = tid & (kWave - 1);
     const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);  // uniform per wavefront
@@ -960,7 +964,8 @@ int build(const jl_mapfgpt_t* b, const int16_t* rows, const int16_t* cx, const i
             rc = status(hipEventRecord((hipEvent_t)b->token_events[0], stream));
             if (rc) return rc;
         }
-        const dim3 grid2((unsigned)b->n_envs * ((b->n_agents + kEgosPerBlock - 1) / kEgosPerBlock));
+        const int slice = ego_slice(b->n_agents);
+        const dim3 grid2((unsigned)b->n_envs * ((b->n_agents + slice - 1) / slice));
         if (L.dense) {
             hipLaunchKernelGGL((tokens_kernel<H, true>), grid2, dim3(kTokThreads), L.total, stream, *b);
         } else {
