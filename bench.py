@@ -24,6 +24,12 @@ step of fixed_magat_plus_runtime.py: step_sim_only -> update_derived_state ->
 build_magat_plus_nodes -> finalize_magat_plus_graph, plus update_actions) at
 512 envs x 256 agents on 64x64 maps with obstacle density 0.3, with the node
 kernel's roofline and the C restatement of the same step as CPU baseline.
+
+`--workload ring` streams C5-sized frozen records (256 envs x 1024 agents,
+256x256 warehouses) from RingStageSource producer processes through the host
+ring and the HBM ring into build_tokens, once in the compact format (5 bytes
+per agent-step over the host link, rows rebuilt on the device) and once in the
+reference's 13-column row format, with the expansion kernel's roofline.
 """
 from __future__ import annotations
 
@@ -417,6 +423,200 @@ def main_magat(args) -> int:
     return 0
 
 
+def _ring_row_stages(positions, actions, goals, E: int, A: int) -> np.ndarray:
+    """Full 13-column rows of one episode per env starting at stage 0 (the rows
+    mapf_gpt_expert_worker_loop writes, mapf_gpt_online.py:215-258)."""
+    S, N = actions.shape
+    rows = np.empty((S, N, 13), np.uint16)
+    rows[:, :, 0] = np.repeat(np.arange(E, dtype=np.uint16), A)[None]
+    rows[:, :, 1] = np.tile(np.arange(A, dtype=np.uint16), E)[None]
+    rows[:, :, 2:4] = positions
+    rows[:, :, 4:6] = goals.reshape(N, 2)[None]
+    rows[:, :, 6] = actions
+    rows[:, :, 7] = 0
+    rows[0, :, 7] = 1
+    for k in range(5):  # history slot k at stage s holds the action of stage s - 5 + k
+        lag = 5 - k
+        rows[:lag, :, 8 + k] = 5
+        rows[lag:, :, 8 + k] = actions[:S - lag]
+    return rows
+
+
+def run_gpu_ring(args) -> dict:
+    """Frozen records -> RingStageSource producers -> host ring -> HBM ring ->
+    build_tokens, for the compact format and the reference's row format."""
+    import shutil
+    import tempfile
+
+    import torch
+
+    from iclr_2027_jointoom_amd import profile
+    from iclr_2027_jointoom_amd.records import CompactRecords, write_compact_records
+    from iclr_2027_jointoom_amd.ring import MapfGPTOnlinePipeline, RingStageSource, save_records
+    from iclr_2027_jointoom_amd.synthetic import make_batch
+
+    E, W, A = args.envs, args.map, args.agents
+    N = E * A
+    S = args.warmup + args.steps
+    print(f"[bench] ring: generating {E} maps {W}x{W}, {A} agents, {S} stages", file=sys.stderr, flush=True)
+    grids, starts, goals = make_batch(args.seed, E, W, W, A, kind=args.map_kind)
+    rng = np.random.default_rng(args.seed)
+    positions = np.empty((S, N, 2), np.uint16)
+    pos = starts.astype(np.uint16)
+    for s in range(S):
+        positions[s] = pos.reshape(N, 2)
+        pos = np.roll(pos, 1, axis=1)  # distinct free cells at every stage
+    actions = rng.integers(0, 5, size=(S, N)).astype(np.uint8)
+    episode_starts = np.zeros((S, E), np.uint8)
+    episode_starts[0] = 1
+    tmp = Path(tempfile.mkdtemp(prefix="jl_ring_", dir=os.environ.get("TMPDIR", "/tmp")))
+    archives = {}
+    try:
+        rec = CompactRecords(positions, actions, episode_starts, goals.astype(np.uint16))
+        write_compact_records(tmp / "compact", backend="mapf_gpt", grids=grids, records=rec, metadata={})
+        archives["compact"] = tmp / "compact"
+        if not args.ring_compact_only:
+            save_records(tmp / "rows", backend="mapf_gpt", grids=grids,
+                         stages=_ring_row_stages(positions, actions, goals, E, A), metadata={})
+            archives["rows"] = tmp / "rows"
+        dev = torch.device("cuda:0")
+        g = torch.from_numpy(grids.astype(np.int32)).to(dev)
+        ext = profile(W, W)
+        hip = HipEvents()
+        config = {"num_agents": A, "num_steps": S, "map_names": [f"env{e}" for e in range(E)]}
+        out = {}
+        for fmt, path in archives.items():
+            builder = ext.MapfGPTObservationBuilder(g, A)
+            tok_events = [(hip.create(), hip.create()) for _ in range(args.steps)]
+
+            class _Build:
+                n = 0
+
+                def train_step(self, b, raw):
+                    i = self.n - args.warmup
+                    if 0 <= i < len(tok_events):
+                        b._desc.token_events[0], b._desc.token_events[1] = tok_events[i]
+                    else:
+                        b._desc.token_events[0] = b._desc.token_events[1] = None
+                    b.build_tokens(raw)
+                    self.n += 1
+                    return {}
+
+            runtime = _Build()
+            pipe = MapfGPTOnlinePipeline(builder, runtime, capacity=args.ring_slots * N, batch_threshold=N,
+                                         device=str(dev), record_format=fmt).initialize()
+            pipe.dma_worker.timing = []
+            src = RingStageSource(pipe.ring_buffer, "mapf_gpt", config, records=path, timeout=600,
+                                  workers=args.ring_workers)
+            print(f"[bench] ring {fmt}: {len(src.processes)} producer processes", file=sys.stderr, flush=True)
+            try:
+                src.start()
+                pipe.dma_worker_loop()
+                done = 0
+                t0 = None
+                busy = 0.0
+                while done < S:
+                    if done == args.warmup and t0 is None:
+                        torch.cuda.synchronize()
+                        t0 = time.perf_counter()
+                        dma_host0 = pipe.dma_worker.host_seconds
+                    tc = time.perf_counter()
+                    if pipe.consume_once() is None:
+                        src.check()
+                        time.sleep(0.00005)
+                    else:
+                        done += 1
+                        if t0 is not None:
+                            busy += time.perf_counter() - tc
+                torch.cuda.synchronize()
+                wall = time.perf_counter() - t0
+                dma_host = pipe.dma_worker.host_seconds - dma_host0
+            finally:
+                pipe.shutdown()
+                src.close()
+            builder._desc.token_events[0] = builder._desc.token_events[1] = None
+            diag = builder.diagnostics.cpu().tolist()
+            if any(diag):
+                raise RuntimeError(f"builder diagnostics non-zero: {diag}")
+            timing = pipe.dma_worker.timing[args.warmup:]
+            up_bytes = float(np.mean([t[0] for t in timing]))
+            up_s = float(np.mean([t[1].elapsed_time(t[2]) for t in timing])) / 1e3
+            res = {
+                "value": N * args.steps / wall,
+                "ms_per_stage": wall * 1e3 / args.steps,
+                "host_link_bytes_per_stage": up_bytes,
+                "host_link_bytes_per_agent_step": up_bytes / N,
+                "upload_us_per_stage": up_s * 1e6,
+                "upload_GBps": up_bytes / up_s / 1e9,
+                "token_us": float(np.mean([hip.elapsed_ms(a, b) for a, b in tok_events])) * 1e3,
+                "consumer_host_us_per_stage": busy * 1e6 / args.steps,
+                "dma_host_us_per_stage": dma_host * 1e6 / args.steps,
+                "producers": len(src.processes),
+            }
+            if fmt == "compact":
+                res["expand_us"] = float(np.mean([t[2].elapsed_time(t[3]) for t in timing])) * 1e3
+            out[fmt] = res
+            print(f"[bench] ring {fmt}: {json.dumps(res)}", file=sys.stderr, flush=True)
+            del pipe, builder, runtime
+            torch.cuda.empty_cache()
+        out["device"] = torch.cuda.get_device_name(0)
+        return out
+    finally:
+        shutil.rmtree(tmp, ignore_errors=True)
+
+
+# expansion of one steady-state 13-column stage per agent: positions + action
+# read (5), running goal read (4), history read + write (8 + 8), row write (26)
+B_EXPAND_13 = 5 + 4 + 8 + 8 + 26
+
+
+def main_ring(args) -> int:
+    res = run_gpu_ring(args)
+    c = res["compact"]
+    N = args.envs * args.agents
+    exp_s = c["expand_us"] / 1e6
+    line = {
+        "metric": "agent-steps/sec incl. obs/token build on 1 GPU; % of HBM roofline",
+        "value": c["value"],
+        "unit": "agent-steps/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": c["ms_per_stage"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int16/int32 (integer)",
+        "data": "synthetic frozen records (seeded warehouse maps, distinct positions and goals, uniform actions)",
+        "config": {
+            "workload": "frozen records streamed through the HBM ring into build_tokens (C5 ring)",
+            "record_format": "compact (5 B per agent-step, rows rebuilt on the device)",
+            "envs": args.envs,
+            "agents": args.agents,
+            "map": f"{args.map}x{args.map}",
+            "producers": c["producers"],
+            "ring_slots": args.ring_slots,
+        },
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "expand_records_kernel<13>",
+            "achieved": B_EXPAND_13 * N / exp_s / 1e9,
+            "peak": PEAK_HBM_BPS / 1e9,
+            "unit": "GB/s",
+            "frac": B_EXPAND_13 * N / exp_s / PEAK_HBM_BPS,
+            "traffic": None,
+            "bytes_per_launch": B_EXPAND_13 * N,
+            "avg_launch_us": c["expand_us"],
+        },
+        "cpu_baseline": None,
+        "compact": c,
+        "rows": res.get("rows"),
+        "device": res["device"],
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
 def main() -> int:
     p = argparse.ArgumentParser(description=__doc__.split("\n", 1)[0])
     p.add_argument("--gpus", type=int, default=1)
@@ -433,11 +633,22 @@ def main() -> int:
                    help="only run 3 device copies of 256 MiB (PMC byte-counter calibration)")
     p.add_argument("--graph", action="store_true",
                    help="replay each step from a captured HIP graph (iclr_2027_jointoom_amd/graphs.py)")
-    p.add_argument("--workload", choices=("resident", "magat", "c5"), default="resident",
+    p.add_argument("--workload", choices=("resident", "magat", "c5", "ring"), default="resident",
                    help="resident: the north-star MAPF-GPT loop (C2+C3); magat: the C4 MAGAT stateful "
-                        "step; c5: the resident loop at C5 (256 envs x 1024 agents, 256x256 warehouses)")
+                        "step; c5: the resident loop at C5 (256 envs x 1024 agents, 256x256 warehouses); "
+                        "ring: C5 frozen records streamed through the HBM ring into build_tokens")
     p.add_argument("--map-kind", choices=("iid", "maze", "warehouse"), default="iid")
+    p.add_argument("--ring-workers", type=int, default=8, help="record producer processes (ring workload)")
+    p.add_argument("--ring-slots", type=int, default=4, help="stage slots of the ring (ring workload)")
+    p.add_argument("--ring-compact-only", action="store_true",
+                   help="skip the row-format comparison run (ring workload)")
     args = p.parse_args()
+    if args.workload == "ring":
+        for flag, name, value in (("--envs", "envs", 256), ("--agents", "agents", 1024),
+                                  ("--map", "map", 256), ("--map-kind", "map_kind", "warehouse"),
+                                  ("--steps", "steps", 40), ("--warmup", "warmup", 4)):
+            if flag not in sys.argv:
+                setattr(args, name, value)
     if args.workload == "c5":
         for flag, name, value in (("--envs", "envs", 256), ("--agents", "agents", 1024),
                                   ("--map", "map", 256), ("--map-kind", "map_kind", "warehouse"),
@@ -470,6 +681,8 @@ def main() -> int:
         return 2
     if args.workload == "magat":
         return main_magat(args)
+    if args.workload == "ring":
+        return main_ring(args)
     base = None
     if not args.no_cpu_baseline:
         print("[bench] cpu baseline", file=sys.stderr, flush=True)

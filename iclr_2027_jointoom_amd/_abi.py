@@ -99,6 +99,25 @@ class MagatDesc(ctypes.Structure):
     ]
 
 
+class RecordsDesc(ctypes.Structure):
+    """``jl_records_t``: one stage of compact expert records and the running
+    goals/histories it expands against (frozen_stage_source.py:23-156)."""
+
+    _fields_ = [
+        ("n_envs", c_int32),
+        ("n_agents", c_int32),
+        ("features", c_int32),
+        ("reserved", c_int32),
+        ("positions", c_void_p),
+        ("actions", c_void_p),
+        ("episode_start", c_void_p),
+        ("new_goals", c_void_p),
+        ("goals", c_void_p),
+        ("history", c_void_p),
+        ("rows", c_void_p),
+    ]
+
+
 # name -> (restype, argtypes); the exact set of symbols include/jointloom.h declares
 SIGNATURES = {
     "jl_encode_map": (c_int32, [c_void_p, c_void_p, c_int32, c_int32, c_int32, c_void_p]),
@@ -133,6 +152,7 @@ SIGNATURES = {
     "jl_magat_occupancy": (c_int32, [ctypes.POINTER(MagatDesc), c_void_p]),
     "jl_magat_nodes": (c_int32, [ctypes.POINTER(MagatDesc), c_void_p]),
     "jl_magat_edges": (c_int32, [ctypes.POINTER(MagatDesc), c_void_p]),
+    "jl_expand_records": (c_int32, [ctypes.POINTER(RecordsDesc), c_void_p]),
     "jl_decode_to_uint8": (c_int32, [c_void_p, c_void_p, c_int64, c_int32, c_void_p]),
     "jl_error_string": (ctypes.c_char_p, [c_int32]),
     "jl_version": (ctypes.c_char_p, []),

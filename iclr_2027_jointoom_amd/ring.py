@@ -100,8 +100,9 @@ class RingBuffer:
                     f"stage-based ring requires at least one stage slot, got capacity={capacity}"
                 )
         # shared with forked producer processes; see the module docstring for pinning
-        self.cpu_buffer = torch.zeros((capacity, feature_dim), dtype=torch.int16).share_memory_()
+        self.cpu_buffer = self._allocate_host_buffer()
         self.ready_flags = mp.Array("B", capacity)
+        self._flags_view = None
         self.shared_reserve_ptr = mp.Value("Q", 0)
         self.shared_compute_ptr = mp.Value("Q", 0)
         self.reserve_lock = mp.Lock()
@@ -113,6 +114,21 @@ class RingBuffer:
             self.env_write_seq = None
             self.stage_ready_counts = None
             self.stage_seq_tags = None
+
+    def _allocate_host_buffer(self) -> torch.Tensor:
+        return torch.zeros((self.capacity, self.feature_dim), dtype=torch.int16).share_memory_()
+
+    def _set_flags(self, start: int, end: int, value: int) -> None:
+        """ready_flags[start:end] = value through a numpy view of the shared
+        bytes (one memset instead of a Python list per call)."""
+        if self._flags_view is None:
+            self._flags_view = np.frombuffer(self.ready_flags.get_obj(), dtype=np.uint8)
+        self._flags_view[start:end] = value
+
+    def __getstate__(self):
+        state = self.__dict__.copy()
+        state["_flags_view"] = None
+        return state
 
     def _stage_row_bounds(self, stage_seq: int, env_id: int | None = None) -> tuple[int, int]:
         if not self.stage_mode:
@@ -152,9 +168,17 @@ class RingBuffer:
         one the consumer has passed.  The stage stays invisible until every
         env has called ``_publish_stage_block``.
         """
+        return self._reserve_stage_range(env_id, env_id + 1)
+
+    def _reserve_stage_range(self, env_lo: int, env_hi: int) -> tuple[int, int, int]:
+        """``_reserve_stage_block`` for the contiguous envs [env_lo, env_hi),
+        written by one producer that keeps them at the same stage."""
         while True:
             with self.reserve_lock:
-                write_seq = int(self.env_write_seq[env_id])
+                seqs = self.env_write_seq[env_lo:env_hi]
+                write_seq = int(seqs[0])
+                if any(int(q) != write_seq for q in seqs):
+                    raise ValueError("envs of one producer range are at different stages")
                 consumed_seq = self.shared_compute_ptr.value // self.stage_rows
                 if write_seq - consumed_seq < self.num_stage_slots:
                     stage_idx = write_seq % self.num_stage_slots
@@ -163,23 +187,26 @@ class RingBuffer:
                         if stage_tag != write_seq:
                             self.stage_seq_tags[stage_idx] = write_seq
                             self.stage_ready_counts[stage_idx] = 0
-                        row_start, row_end = self._stage_row_bounds(write_seq, env_id=env_id)
-                        return write_seq, row_start, row_end
+                        row_start = self._stage_row_bounds(write_seq, env_id=env_lo)[0]
+                        return write_seq, row_start, row_start + (env_hi - env_lo) * self.agents_per_env
             time.sleep(_POLL_S)
 
     def _publish_stage_block(self, env_id: int, write_seq: int) -> None:
         """Publish one fully written env block into its stage."""
+        self._publish_stage_range(env_id, env_id + 1, write_seq)
+
+    def _publish_stage_range(self, env_lo: int, env_hi: int, write_seq: int) -> None:
         with self.reserve_lock:
             stage_idx = write_seq % self.num_stage_slots
-            self.stage_ready_counts[stage_idx] += 1
-            self.env_write_seq[env_id] = write_seq + 1
-            self.shared_reserve_ptr.value += self.agents_per_env
+            self.stage_ready_counts[stage_idx] += env_hi - env_lo
+            self.env_write_seq[env_lo:env_hi] = [write_seq + 1] * (env_hi - env_lo)
+            self.shared_reserve_ptr.value += (env_hi - env_lo) * self.agents_per_env
 
     def _stage_reserve_and_write(self, data: np.ndarray):
         env_id, block = self._validate_stage_block(data)
         write_seq, row_start, row_end = self._reserve_stage_block(env_id)
         self.cpu_buffer[row_start:row_end].copy_(block)
-        self.ready_flags[row_start:row_end] = [1] * self.agents_per_env
+        self._set_flags(row_start, row_end, 1)
         self._publish_stage_block(env_id, write_seq)
         return (row_start, row_end)
 
@@ -205,13 +232,13 @@ class RingBuffer:
         if idx_start < idx_end or idx_end == 0:
             end = self.capacity if idx_end == 0 else idx_end
             self.cpu_buffer[idx_start:end].copy_(rows)
-            self.ready_flags[idx_start:end] = [1] * n
+            self._set_flags(idx_start, end, 1)
             return (idx_start, end)
         first = self.capacity - idx_start
         self.cpu_buffer[idx_start:self.capacity].copy_(rows[:first])
         self.cpu_buffer[0:idx_end].copy_(rows[first:])
-        self.ready_flags[idx_start:self.capacity] = [1] * first
-        self.ready_flags[0:idx_end] = [1] * idx_end
+        self._set_flags(idx_start, self.capacity, 1)
+        self._set_flags(0, idx_end, 1)
         return (idx_start, idx_end)
 
     def is_stage_ready(self, stage_seq: int) -> bool:
@@ -232,7 +259,7 @@ class RingBuffer:
         with self.reserve_lock:
             self.stage_ready_counts[stage_idx] = 0
             self.stage_seq_tags[stage_idx] = -1
-        self.ready_flags[row_start:row_end] = [0] * self.stage_rows
+        self._set_flags(row_start, row_end, 0)
 
     def scan_ready_range(self, start_ptr: int, max_scan: int) -> int:
         idx_start = start_ptr % self.capacity
@@ -242,7 +269,7 @@ class RingBuffer:
         return max_scan
 
     def clear_flags(self, start: int, end: int) -> None:
-        self.ready_flags[start:end] = [0] * (end - start)
+        self._set_flags(start, end, 0)
 
 
 # ============================================================
@@ -268,6 +295,14 @@ class DMAWorker:
         ]
         self.staging_events = [None] * len(self.staging)
         self._slot = 0
+        # set to a list to collect (bytes, upload events) per stage for measurement
+        self.timing = None
+        self.host_seconds = 0.0  # host time moving stages (staging copy + enqueue), waits excluded
+
+    def _timing_event(self, stream):
+        ev = torch.cuda.Event(enable_timing=True)
+        ev.record(stream)
+        return ev
 
     def _copy_rows(self, idx_start: int, idx_end: int) -> None:
         """cpu_buffer[idx_start:idx_end] -> gpu_buffer[idx_start:idx_end] through a pinned slot."""
@@ -276,15 +311,21 @@ class DMAWorker:
         pending = self.staging_events[slot]
         if pending is not None:
             pending.synchronize()  # the slot's previous upload has left host memory
+        t_host = time.perf_counter()
         n = idx_end - idx_start
         staged = self.staging[slot][:n]
         staged.copy_(self.ring_buffer.cpu_buffer[idx_start:idx_end])
         with torch.cuda.stream(self.copy_stream):
+            t0 = self._timing_event(self.copy_stream) if self.timing is not None else None
             self.gpu_buffer[idx_start:idx_end].copy_(staged, non_blocking=True)
+            if t0 is not None:
+                self.timing.append((staged.numel() * staged.element_size(), t0,
+                                    self._timing_event(self.copy_stream), None))
             done = torch.cuda.Event(enable_timing=False)
             done.record(self.copy_stream)
             self.dma_event.record(self.copy_stream)
         self.staging_events[slot] = done
+        self.host_seconds += time.perf_counter() - t_host
 
     def run_once(self):
         ring = self.ring_buffer
@@ -333,6 +374,220 @@ class DMAWorker:
 
 
 # ============================================================
+# Compact stage ring - 5 bytes per agent and step over the host link
+# ============================================================
+def _align(n: int, a: int) -> int:
+    return (n + a - 1) // a * a
+
+
+class CompactRingBuffer(RingBuffer):
+    """Stage ring whose slots hold compact records (records.py) instead of rows.
+
+    Same stage protocol, sequence tags, counters and pointers (counted in rows)
+    as ``RingBuffer``; a slot of N = num_envs * agents_per_env agents is::
+
+        [0, 4N)                 positions   uint16 [N, 2]
+        [4N, 5N)                actions     uint8  [N]
+        [5N, 5N + E)            episode start flags, one byte per env
+        [goals, goals + 4N)     goals       uint16 [N, 2], written for starting envs only
+
+    ``cpu_buffer`` is uint8 [num_stage_slots, slot_bytes].  Producers either
+    call ``write_compact`` with compact blocks or keep calling
+    ``reserve_and_write`` with full env blocks (the reference producer API):
+    those are compacted here, and rows that the compact form cannot carry
+    (records.py) raise ValueError in the producer.
+    """
+
+    def __init__(self, capacity: int, feature_dim: int = FEATURE_DIM, *, num_envs: int, agents_per_env: int):
+        if feature_dim not in (FEATURE_DIM, MAPFGPT_FEATURE_DIM):
+            raise ValueError(f"feature_dim must be {FEATURE_DIM} or {MAPFGPT_FEATURE_DIM}, got {feature_dim}")
+        n = int(num_envs) * int(agents_per_env)
+        self.off_actions = 4 * n
+        self.off_starts = 5 * n
+        self.head_bytes = 5 * n + int(num_envs)
+        self.off_goals = _align(self.head_bytes, 16)
+        self.slot_bytes = _align(self.off_goals + 4 * n, 64)
+        super().__init__(capacity, feature_dim, num_envs=num_envs, agents_per_env=agents_per_env)
+        self._tracked = {}  # producer-side: env -> (goals, history) of its running episode
+
+    def _allocate_host_buffer(self) -> torch.Tensor:
+        if not self.stage_mode:
+            raise ValueError("a compact ring needs num_envs and agents_per_env")
+        return torch.zeros((self.num_stage_slots, self.slot_bytes), dtype=torch.uint8).share_memory_()
+
+    def slot_view(self, stage_seq: int) -> np.ndarray:
+        """uint8 view of the host slot of a stage."""
+        return self.cpu_buffer[int(stage_seq) % self.num_stage_slots].numpy()
+
+    def write_compact(self, env_lo: int, positions, actions, episode_start, goals=None):
+        """Write the compact blocks of the contiguous envs [env_lo, env_lo + n)
+        (n = len(episode_start)) into their next stage with one reservation.
+        ``positions`` [n*A, 2] and ``goals`` [n*A, 2] are 16-bit, ``actions``
+        [n*A] 0..4; goals are required when any env starts an episode."""
+        A = self.agents_per_env
+        starts = np.asarray(episode_start, dtype=np.uint8).reshape(-1)
+        n_env = starts.shape[0]
+        env_lo = int(env_lo)
+        if n_env <= 0 or env_lo < 0 or env_lo + n_env > self.num_envs:
+            raise ValueError(f"env range out of bounds: [{env_lo}, {env_lo + n_env}) of {self.num_envs}")
+        pos = np.asarray(positions)
+        act = np.asarray(actions)
+        if pos.shape != (n_env * A, 2) or act.shape != (n_env * A,):
+            raise ValueError(f"compact block must hold {n_env * A} positions [.,2] and actions")
+        if np.any(act > 4) or np.any(starts > 1):
+            raise ValueError("invalid action or refresh flag")
+        if starts.any():
+            if goals is None or np.asarray(goals).shape != (n_env * A, 2):
+                raise ValueError("goals [n*A, 2] are required for envs that start an episode")
+        write_seq, row_start, row_end = self._reserve_stage_range(env_lo, env_lo + n_env)
+        slot = self.slot_view(write_seq)
+        a0, a1 = env_lo * A, (env_lo + n_env) * A
+        slot[4 * a0:4 * a1].view(np.uint16)[:] = pos.astype(np.uint16, copy=False).reshape(-1)
+        slot[self.off_actions + a0:self.off_actions + a1] = act
+        slot[self.off_starts + env_lo:self.off_starts + env_lo + n_env] = starts
+        if starts.any():
+            g = np.asarray(goals).astype(np.uint16, copy=False).reshape(n_env, A * 2)
+            dst = slot[self.off_goals + 4 * a0:self.off_goals + 4 * a1].view(np.uint16).reshape(n_env, A * 2)
+            dst[starts == 1] = g[starts == 1]
+        self._set_flags(row_start, row_end, 1)
+        self._publish_stage_range(env_lo, env_lo + n_env, write_seq)
+        return (row_start, row_end)
+
+    def _stage_reserve_and_write(self, data: np.ndarray):
+        """A full env block (reference producer API), compacted."""
+        if data.ndim != 2 or data.shape[1] != self.feature_dim:
+            raise ValueError(f"shape must be [N, {self.feature_dim}] in stage mode, got {data.shape}")
+        env_id, _ = self._validate_stage_block(data)
+        rows = data.astype(np.int64)
+        refresh = rows[:, RESET_FLAG_COL]
+        if np.any(refresh > 1) or np.any(rows[:, 6] > 4):
+            raise ValueError("invalid action or refresh flag")
+        start = int(refresh[0])
+        if np.any(refresh != start):
+            raise ValueError("compact records need one refresh flag per env and stage")
+        goals = rows[:, 4:6]
+        tracked = self._tracked.get(env_id)
+        if start:
+            history = np.full((self.agents_per_env, 5), 5, np.int64)
+        else:
+            if tracked is None:
+                raise ValueError("compact records need every env to start an episode first")
+            if not np.array_equal(goals, tracked[0]):
+                raise ValueError("compact records need goals that change only at an episode start")
+            history = tracked[1]
+        if self.feature_dim == MAPFGPT_FEATURE_DIM and not np.array_equal(rows[:, 8:13], history):
+            raise ValueError("history columns are not the previous actions of the episode")
+        history = np.concatenate([history[:, 1:], rows[:, 6:7]], axis=1)
+        out = self.write_compact(env_id, rows[:, 2:4], rows[:, 6], [start], goals if start else None)
+        self._tracked[env_id] = (goals, history)
+        return out
+
+
+class CompactDMAWorker(DMAWorker):
+    """Moves ready compact stages to the device and expands them there into
+    ``gpu_buffer`` rows (the same rows a row ring would deliver).
+
+    Per stage: the slot's head (positions, actions, start flags: 5N + E bytes)
+    and the goal range of the envs that start an episode are copied
+    shm -> pinned slot on the host, then host -> HBM on ``copy_stream``, where
+    ``jl_expand_records`` writes the stage's rows into ``gpu_buffer`` and
+    advances the running goals and histories; ``dma_event`` follows."""
+
+    def __init__(self, ring_buffer: CompactRingBuffer, gpu_buffer: torch.Tensor, batch_threshold=4096,
+                 device="cuda:0", *, staging_slots: int = 2):
+        from .records import RecordExpander
+
+        if not isinstance(ring_buffer, CompactRingBuffer):
+            raise TypeError("CompactDMAWorker needs a CompactRingBuffer")
+        self.ring_buffer = ring_buffer
+        self.gpu_buffer = gpu_buffer
+        self.batch_threshold = batch_threshold
+        self.device = torch.device(device)
+        self.copy_stream = torch.cuda.Stream(device=self.device)
+        self.dma_event = torch.cuda.Event(enable_timing=False)
+        self.dma_read_ptr = 0
+        self._running = False
+        k = max(1, int(staging_slots))
+        L = ring_buffer.slot_bytes
+        self.staging = [torch.empty(L, dtype=torch.uint8).pin_memory() for _ in range(k)]
+        self.device_slots = torch.empty((k, L), dtype=torch.uint8, device=self.device)
+        self.staging_events = [None] * k
+        self._slot = 0
+        self.expander = RecordExpander(ring_buffer.num_envs, ring_buffer.agents_per_env,
+                                       ring_buffer.feature_dim, self.device)
+        self.bytes_uploaded = 0
+        self.host_seconds = 0.0  # host time moving stages (staging copy + enqueue), waits excluded
+        # per ring slot: an event after the consumer's copy out of the slot's rows
+        self._consumed = [None] * ring_buffer.num_stage_slots
+        # set to a list to collect (bytes, upload events, expansion end event) per stage
+        self.timing = None
+
+    def mark_slot_consumed(self, stage_seq: int, stream) -> None:
+        """Record on the consumer's stream that the stage's rows have been
+        copied out of ``gpu_buffer``: the slot's next expansion waits for it."""
+        ev = torch.cuda.Event(enable_timing=False)
+        ev.record(stream)
+        self._consumed[int(stage_seq) % len(self._consumed)] = ev
+
+    def _copy_stage(self, stage_seq: int) -> tuple[int, int]:
+        ring = self.ring_buffer
+        slot = self._slot
+        self._slot = (slot + 1) % len(self.staging)
+        pending = self.staging_events[slot]
+        if pending is not None:
+            pending.synchronize()  # the slot's previous upload has left host memory
+        t_host = time.perf_counter()
+        src_t = ring.cpu_buffer[int(stage_seq) % ring.num_stage_slots]
+        src = src_t.numpy()
+        staged = self.staging[slot]
+        head = ring.head_bytes
+        # torch's host copy runs without the interpreter lock (and in parallel
+        # for large spans), so the consumer thread keeps running meanwhile
+        staged[:head].copy_(src_t[:head])
+        starting = np.flatnonzero(src[ring.off_starts:ring.off_starts + ring.num_envs])
+        g0 = g1 = 0
+        if starting.size:
+            A4 = 4 * ring.agents_per_env
+            g0 = ring.off_goals + int(starting[0]) * A4
+            g1 = ring.off_goals + (int(starting[-1]) + 1) * A4
+            staged[g0:g1].copy_(src_t[g0:g1])
+        row_start, row_end = ring._stage_row_bounds(stage_seq)
+        dev = self.device_slots[slot]
+        base = dev.data_ptr()
+        timed = self.timing is not None
+        consumed = self._consumed[int(stage_seq) % len(self._consumed)]
+        with torch.cuda.stream(self.copy_stream):
+            if consumed is not None:
+                self.copy_stream.wait_event(consumed)
+            t0 = self._timing_event(self.copy_stream) if timed else None
+            dev[:head].copy_(staged[:head], non_blocking=True)
+            if g1 > g0:
+                dev[g0:g1].copy_(staged[g0:g1], non_blocking=True)
+            t1 = self._timing_event(self.copy_stream) if timed else None
+            rows = self.gpu_buffer[row_start:row_end]
+            self.expander.expand_ptrs(base, base + ring.off_actions, base + ring.off_starts,
+                                      base + ring.off_goals, rows.data_ptr(), self.copy_stream.cuda_stream)
+            if timed:
+                self.timing.append((head + (g1 - g0), t0, t1, self._timing_event(self.copy_stream)))
+            done = torch.cuda.Event(enable_timing=False)
+            done.record(self.copy_stream)
+            self.dma_event.record(self.copy_stream)
+        self.staging_events[slot] = done
+        self.bytes_uploaded += head + (g1 - g0)
+        self.host_seconds += time.perf_counter() - t_host
+        return row_start, row_end
+
+    def run_once(self):
+        ring = self.ring_buffer
+        stage_seq = self.dma_read_ptr // ring.stage_rows
+        if not ring.is_stage_ready(stage_seq):
+            return None
+        bounds = self._copy_stage(stage_seq)
+        self.dma_read_ptr += ring.stage_rows
+        return bounds
+
+
+# ============================================================
 # GPUComputeHandler
 # ============================================================
 class GPUComputeHandler:
@@ -357,7 +612,10 @@ class ExtremeMAPFPipeline:
     """Ring + DMA + stage consumer for a MAGAT simulator (expert_running.py:602-808)."""
 
     def __init__(self, simulator, capacity=16384 * 128, batch_threshold=16384,
-                 feature_dim=FEATURE_DIM, device="cuda:0"):
+                 feature_dim=FEATURE_DIM, device="cuda:0", *, record_format: str = "rows"):
+        if record_format not in ("rows", "compact"):
+            raise ValueError(f"record_format must be 'rows' or 'compact', got {record_format!r}")
+        self.record_format = record_format
         self.device = torch.device(device)
         self.capacity = capacity
         self.batch_threshold = batch_threshold
@@ -389,12 +647,15 @@ class ExtremeMAPFPipeline:
         return agents_per_env, num_envs
 
     def _make_ring(self, feature_dim: int) -> None:
-        self.ring_buffer = RingBuffer(self.capacity, feature_dim, num_envs=self.num_envs,
-                                      agents_per_env=self.agents_per_env)
+        compact = self.record_format == "compact"
+        ring_cls = CompactRingBuffer if compact else RingBuffer
+        self.ring_buffer = ring_cls(self.capacity, feature_dim, num_envs=self.num_envs,
+                                    agents_per_env=self.agents_per_env)
         self.gpu_buffer = torch.zeros((self.capacity, feature_dim), dtype=torch.int16, device=self.device)
         stage_rows = self.ring_buffer.stage_rows if self.ring_buffer.stage_mode else self.batch_threshold
         self.stage_batch_buffer = torch.empty((stage_rows, feature_dim), dtype=torch.int16, device=self.device)
-        self.dma_worker = DMAWorker(self.ring_buffer, self.gpu_buffer, self.batch_threshold, str(self.device))
+        dma_cls = CompactDMAWorker if compact else DMAWorker
+        self.dma_worker = dma_cls(self.ring_buffer, self.gpu_buffer, self.batch_threshold, str(self.device))
         self.dma_event = self.dma_worker.dma_event
         self.compute_stream = torch.cuda.Stream(device=self.device)
 
@@ -465,7 +726,14 @@ class ExtremeMAPFPipeline:
         # ordered after the stage's upload by the caller's wait on dma_event
         torch.cuda.current_stream(self.gpu_buffer.device).wait_event(self.dma_event)
         raw_batch.copy_(self.gpu_buffer[row_start:row_end], non_blocking=False)
-        self._validate_env_aligned_batch(raw_batch, agents_per_env, num_envs)
+        if isinstance(self.dma_worker, CompactDMAWorker):
+            # env and agent ids were written by the device expansion from the
+            # row index, so there is nothing to validate; the slot's next
+            # expansion is ordered after this copy on the device instead of
+            # by a host synchronisation
+            self.dma_worker.mark_slot_consumed(stage_seq, torch.cuda.current_stream(self.gpu_buffer.device))
+        else:
+            self._validate_env_aligned_batch(raw_batch, agents_per_env, num_envs)
         self.compute_ptr += chunk_size
         self.dma_worker.release_completed_stage(stage_seq)
         return raw_batch
@@ -528,9 +796,10 @@ class ExtremeMAPFPipeline:
 class MapfGPTOnlinePipeline(ExtremeMAPFPipeline):
     """13-column stages into a MapfGPTObservationBuilder (mapf_gpt_online.py:97-184)."""
 
-    def __init__(self, builder, runtime, *, capacity: int, batch_threshold: int, device: str = "cuda:0"):
+    def __init__(self, builder, runtime, *, capacity: int, batch_threshold: int, device: str = "cuda:0",
+                 record_format: str = "rows"):
         super().__init__(builder, capacity=capacity, batch_threshold=batch_threshold,
-                         feature_dim=MAPFGPT_FEATURE_DIM, device=device)
+                         feature_dim=MAPFGPT_FEATURE_DIM, device=device, record_format=record_format)
         self.runtime = runtime
 
     def initialize(self):
@@ -658,31 +927,68 @@ class _WorkerGate:
         self.stop.wait()
 
 
-def _produce(e, ring, backend, config, records, gate):
-    """One env's producer: stream its block of every frozen stage into the ring."""
+def _produce(envs, ring, backend, config, records, gate):
+    """One producer: stream the blocks of envs [lo, hi) of every frozen stage
+    into the ring, stage by stage."""
     if records is None:
         raise NotImplementedError("live expert producers (LaCAM + POGEMA) are not part of this build")
-    stages = np.load(Path(records) / "stages.npy", mmap_mode="r", allow_pickle=False)
+    lo, hi = envs
     a = config["num_agents"]
+    n = config["num_steps"]
+    if isinstance(ring, CompactRingBuffer) and _is_compact(records):
+        from .records import CompactRecords
+
+        arrays = {name: np.load(Path(records) / f"{name}.npy", mmap_mode="r", allow_pickle=False)
+                  for name in ("positions", "actions", "episode_starts", "goals")}
+        rec = CompactRecords(**arrays)
+        goals = np.zeros(((hi - lo) * a, 2), np.uint16)
+        gate.mark_ready()
+        for s in range(min(n, rec.num_stages)):
+            starts = np.asarray(rec.episode_starts[s, lo:hi])
+            for k in np.flatnonzero(starts):
+                goals[k * a:(k + 1) * a] = rec.env_goals(s, lo + int(k))
+            ring.write_compact(lo, rec.positions[s, lo * a:hi * a], rec.actions[s, lo * a:hi * a], starts,
+                               goals if starts.any() else None)
+        gate.mark_complete_and_wait()
+        return
+    stages = np.load(Path(records) / "stages.npy", mmap_mode="r", allow_pickle=False)
     gate.mark_ready()
-    for stage in stages[: config["num_steps"]]:
-        ring.reserve_and_write(np.array(stage[e * a:(e + 1) * a], copy=True))
+    for stage in stages[:n]:
+        for e in range(lo, hi):
+            ring.reserve_and_write(np.array(stage[e * a:(e + 1) * a], copy=True))
     gate.mark_complete_and_wait()
 
 
-class RingStageSource:
-    """One producer process per env streaming frozen records (frozen_stage_source.py:105-156)."""
+def _is_compact(records) -> bool:
+    from .records import is_compact_archive
 
-    def __init__(self, ring, backend, config, *, records=None, timeout=120):
+    return is_compact_archive(records)
+
+
+class RingStageSource:
+    """Producer processes streaming frozen records (frozen_stage_source.py:105-156).
+
+    As in the reference, by default one process per env; ``workers`` (an
+    addition) runs that many processes instead, each owning a contiguous env
+    range, for archives with more envs than host cores.  Compact archives
+    (records.py) stream into a ``CompactRingBuffer``: one compact write per
+    worker and stage."""
+
+    def __init__(self, ring, backend, config, *, records=None, timeout=120, workers=None):
         self.ring, self.timeout, self.seq = ring, timeout, 0
         self.count = config["num_steps"]
+        n_env = len(config["map_names"])
+        if records is not None and _is_compact(records) and not isinstance(ring, CompactRingBuffer):
+            raise ValueError("compact records stream through a CompactRingBuffer (record_format='compact')")
+        workers = n_env if workers is None else max(1, min(int(workers), n_env))
+        bounds = [(w * n_env // workers, (w + 1) * n_env // workers) for w in range(workers)]
         ctx = mp.get_context("fork")
         self.go, self.stop = ctx.Event(), ctx.Event()
-        self.ready = [ctx.Event() for _ in config["map_names"]]
+        self.ready = [ctx.Event() for _ in bounds]
         self.processes = [
-            ctx.Process(target=_produce, args=(e, ring, backend, config, records,
+            ctx.Process(target=_produce, args=(envs, ring, backend, config, records,
                                                _WorkerGate(ready, self.go, self.stop)), daemon=True)
-            for e, ready in enumerate(self.ready)
+            for envs, ready in zip(bounds, self.ready)
         ]
         for p in self.processes:
             p.start()
@@ -706,6 +1012,8 @@ class RingStageSource:
 
     def next_rows(self):
         """Host copy of the next complete stage (the CPU consumer of the same ring)."""
+        if isinstance(self.ring, CompactRingBuffer):
+            raise RuntimeError("compact stages are expanded on the device: consume them through the pipeline")
         if self.seq >= self.count:
             raise StopIteration
         deadline = time.monotonic() + self.timeout

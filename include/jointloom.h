@@ -257,6 +257,39 @@ int jl_magat_nodes(const jl_magat_t* m, jl_stream_t stream);
 int jl_magat_edges(const jl_magat_t* m, jl_stream_t stream);
 
 /* ------------------------------------------------------------------------ */
+/* Compact expert records (one stage = one joint step of every env)          */
+/* ------------------------------------------------------------------------ */
+
+/* A stage of compact records and the running state it is expanded against.
+ * The full rows it stands for are the ones the reference's producers write
+ * (mapf_gpt_online.py:215-258 with mapf_gpt_schema.py:43-66, 118-126 for 13
+ * columns; topology_async.py:90-102, 235-278 for 8): env, agent, position,
+ * goal, action, refresh flag (1 for every agent of an env whose episode starts
+ * at this stage, else 0) and, for 13 columns, the 5 previous actions of the
+ * running episode (oldest first, 5 = none).  `goals` and `history` carry the
+ * running episode of every agent from one stage to the next; stages must be
+ * expanded in order, and the first stage must start an episode in every env.
+ * Device pointers; positions/goals 4-byte, history 8-byte aligned. */
+typedef struct jl_records {
+    int32_t n_envs;
+    int32_t n_agents;
+    int32_t features;               /* 8 or 13 */
+    int32_t reserved;
+    const uint16_t* positions;      /* [N, 2] x, y at this stage */
+    const uint8_t* actions;         /* [N] action taken at this stage, 0..4 */
+    const uint8_t* episode_start;   /* [E] 1 = env e starts an episode here */
+    const uint16_t* new_goals;      /* [N, 2] goals; read for starting envs only */
+    uint16_t* goals;                /* [N, 2] running goals (in/out) */
+    uint8_t* history;               /* [N, 8] running histories, bytes 0..4 (in/out; 13 only) */
+    int16_t* rows;                  /* out [N, features] */
+} jl_records_t;
+
+/* Rebuild one stage's rows of a frozen archive from its compact records
+ * (the device side of RingStageSource streaming, frozen_stage_source.py:
+ * 83-156; the rows equal the stages.npy rows save_records writes, :23-42). */
+int jl_expand_records(const jl_records_t* r, jl_stream_t stream);
+
+/* ------------------------------------------------------------------------ */
 /* Misc                                                                      */
 /* ------------------------------------------------------------------------ */
 

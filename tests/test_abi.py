@@ -63,12 +63,22 @@ def test_host_side_argument_checks_return_before_device_work(lib):
     assert lib.jl_energy_maps(1, 1, None, 0, 1, 1, 64, 64, 0, None) == 0  # empty batch: nothing to do
     assert lib.jl_seed_rng(None, 4, 1, None) == -1
     assert lib.jl_decode_to_uint8(1, 1, 1, 17, None) == -1
+    from iclr_2027_jointoom_amd._abi import RecordsDesc
+
+    r = RecordsDesc(n_envs=2, n_agents=4, features=13, positions=16, actions=16, episode_start=16,
+                    new_goals=16, goals=16, history=None, rows=16)
+    assert lib.jl_expand_records(ctypes.byref(r), None) == -1  # 13 columns need the histories
+    r.features, r.history = 9, 16
+    assert lib.jl_expand_records(ctypes.byref(r), None) == -1
+    r.features, r.positions = 8, 18  # positions are read as 32-bit words
+    assert lib.jl_expand_records(ctypes.byref(r), None) == -1
 
 
 def test_ctypes_structs_match_the_c_layout(tmp_path):
-    from iclr_2027_jointoom_amd._abi import MagatDesc, MapfGPTDesc, SimDesc
+    from iclr_2027_jointoom_amd._abi import MagatDesc, MapfGPTDesc, RecordsDesc, SimDesc
 
-    structs = {"jl_sim_t": SimDesc, "jl_mapfgpt_t": MapfGPTDesc, "jl_magat_t": MagatDesc}
+    structs = {"jl_sim_t": SimDesc, "jl_mapfgpt_t": MapfGPTDesc, "jl_magat_t": MagatDesc,
+               "jl_records_t": RecordsDesc}
     lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{HEADER}"', "int main(void) {"]
     for cname, py in structs.items():
         lines.append(f'printf("{cname} size %zu\\n", sizeof({cname}));')
