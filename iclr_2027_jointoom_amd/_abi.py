@@ -48,6 +48,12 @@ class SimDesc(ctypes.Structure):
         ("env_offsets", c_void_p),
         ("env_counts", c_void_p),
         ("rng_state", c_void_p),
+        ("goal_candidates", c_void_p),
+        ("candidate_cells", c_void_p),
+        ("candidate_counts", c_void_p),
+        ("goal_cursors", c_void_p),
+        ("candidate_length", c_int32),
+        ("candidate_stride", c_int32),
     ]
 
 

@@ -37,8 +37,18 @@ __device__ __forceinline__ uint32_t hinsert(uint32_t* keys, uint32_t mask, uint3
 struct StepLayout {
     int slots;
     size_t keys_off, owner_off, tag_off, ocp_off, bits_off, cur_off, prop_off, goal_off, sc_off,
-        sp_off, flag_off, mv_off, cat_off, any_off, total;
+        sp_off, flag_off, mv_off, cat_off, any_off, life_off, total;
 };
+
+// Step modes (JL_TASK_*) as a template argument.
+constexpr int kModeLifelong = JL_TASK_LIFELONG;
+constexpr int kModeStandard = JL_TASK_STANDARD_MAPF;
+constexpr int kModeCost = JL_TASK_COSTTRACER;
+
+// Words of the lifelong candidate pass: reached list, start index, cursor,
+// two prefetched candidates per reached agent, the reached count and one
+// count per 64-agent chunk.
+__host__ __device__ inline int life_words(int A) { return 5 * A + 1 + (A + 63) / 64; }
 
 __host__ __device__ inline size_t a16(size_t v) { return (v + 15) & ~(size_t)15; }
 
@@ -48,7 +58,7 @@ constexpr int kDenseStepCells = 4096;
 
 __host__ __device__ inline bool step_dense(int W, int H) { return W * H <= kDenseStepCells; }
 
-__host__ __device__ inline StepLayout step_layout(int A, int W, int H) {
+__host__ __device__ inline StepLayout step_layout(int A, int W, int H, bool life) {
     StepLayout L;
     const bool dense = step_dense(W, H);
     int s = 64;
@@ -83,6 +93,8 @@ __host__ __device__ inline StepLayout step_layout(int A, int W, int H) {
     o = a16(o + (size_t)A);
     L.any_off = o;
     o = a16(o + 3 * 4);
+    L.life_off = o;
+    o = a16(o + (life ? (size_t)life_words(A) * 4 : 0));
     L.total = o;
     return L;
 }
@@ -124,14 +136,15 @@ inline int step_per(int A) { return A <= kStepThreads ? 1 : 4; }
 // obstacle bitmap and each agent's position, goal, action and arrival latch
 // into LDS, the done flags and the step count into registers), so a step
 // costs one memory round trip and the Jacobi rounds run in LDS.
-template <int H, bool kStandard, bool kDense, int kStepPer>
+template <int H, int kMode, bool kDense, int kStepPer>
 __global__ __launch_bounds__(kStepThreads) void step_kernel(jl_sim_t s) {
+    constexpr bool kStandard = kMode == kModeStandard;
     extern __shared__ __align__(16) uint8_t smem[];
     const int env = blockIdx.x;
     const int A = s.n_agents, W = s.map_w;
     const int tid = threadIdx.x, nt = blockDim.x;
     const size_t base = (size_t)env * A;
-    const StepLayout L = step_layout(A, W, H);
+    const StepLayout L = step_layout(A, W, H, kMode == kModeLifelong);
     uint32_t* keys = reinterpret_cast<uint32_t*>(smem + L.keys_off);
     uint32_t* owner = reinterpret_cast<uint32_t*>(smem + L.owner_off);
     uint32_t* tag = reinterpret_cast<uint32_t*>(smem + L.tag_off);
@@ -155,7 +168,9 @@ __global__ __launch_bounds__(kStepThreads) void step_kernel(jl_sim_t s) {
     // branch) before the first LDS store, so they share one round trip.
     const uint8_t term = kStandard ? s.terminated[env] : 0;
     const uint8_t trunc = kStandard ? s.truncated[env] : 0;
-    const int steps = kStandard ? s.step_counts[env] : 0;
+    const int steps = s.step_counts[env];
+    const bool by_candidates = kMode == kModeLifelong && s.goal_candidates != nullptr;
+    const int cand_count = by_candidates ? min(s.candidate_counts[env], s.candidate_stride) : 0;
     const uint4* bits4 = reinterpret_cast<const uint4*>(s.grid_bits + (size_t)env * words);
     const int nvec = vec_words ? words / 4 : 0;
     uint4 rb[kStepPer];
@@ -409,6 +424,13 @@ __global__ __launch_bounds__(kStepThreads) void step_kernel(jl_sim_t s) {
         for (int k = tid; k < words; k += nt) gocp[k] = ocp[k];
     }
 
+    if (kMode == kModeCost) {
+        // CostTracer steps move agents and count steps only (the goal stream
+        // is advanced by the reward pass), 128_agents_map_step.cu:219-222 of
+        // rebuttal/online-rl/native/src/cuda_backend
+        if (tid == 0) s.step_counts[env] = steps + 1;
+        return;
+    }
     if (kStandard) {
         if (tid == 0) {
             const int next = steps + 1;
@@ -439,7 +461,100 @@ __global__ __launch_bounds__(kStepThreads) void step_kernel(jl_sim_t s) {
         }
     }
     __syncthreads();
-    if (tid == 0) {
+    if (by_candidates) {
+        // Canonical agent order over per-agent candidate lists
+        // (128_agents_map_step.cu:303-330 of rebuttal/online-rl/native/src/
+        // cuda_backend; its CPU twin assign_goals, rebuttal/online-il/
+        // tasks.py:51-65): agent i on its goal takes the first cell of its
+        // env's list, from candidates[i][cursor % length] on, that is neither
+        // its own cell nor the goal of an agent off its goal or of an agent
+        // before it.  The reached agents are listed in id order, their first
+        // two candidates fetched in parallel, and one thread settles them in
+        // order against the goal bitmap.
+        uint32_t* life = reinterpret_cast<uint32_t*>(smem + L.life_off);
+        uint32_t* r_list = life;
+        int32_t* r_start = reinterpret_cast<int32_t*>(life + A);
+        int32_t* r_cursor = reinterpret_cast<int32_t*>(life + 2 * A);
+        uint32_t* r_pref = life + 3 * A;  // [2A]: candidates, then the chosen cell
+        uint32_t* r_meta = life + 5 * A;  // [0] reached count, [1 + c] count of chunk c
+        const int lane = tid & (kWave - 1);
+        const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+        const int nwaves = nt / kWave;
+        const int nchunks = (A + kWave - 1) / kWave;
+        for (int c = wave; c < nchunks; c += nwaves) {
+            const int a = c * kWave + lane;
+            const uint64_t m = __ballot(a < A && s_cur[a] == s_goal[a]);
+            if (lane == 0) r_meta[1 + c] = (uint32_t)__popcll(m);
+        }
+        __syncthreads();
+        for (int c = wave; c < nchunks; c += nwaves) {
+            uint32_t before = 0;
+            for (int k = 0; k < c; ++k) before += r_meta[1 + k];
+            const int a = c * kWave + lane;
+            const bool hit = a < A && s_cur[a] == s_goal[a];
+            const uint64_t m = __ballot(hit);
+            if (hit) r_list[before + __popcll(m & ((1ull << lane) - 1ull))] = (uint32_t)a;
+            if (c == nchunks - 1 && lane == 0) r_meta[0] = before + (uint32_t)__popcll(m);
+        }
+        __syncthreads();
+        const int nr = (int)r_meta[0];
+        const int count = cand_count;
+        const int clen = s.candidate_length;
+        const uint16_t* cells = s.candidate_cells + (size_t)env * s.candidate_stride * 2;
+        auto cand = [&](int64_t k) -> uint32_t {
+            const int64_t i = k % count;
+            return (uint32_t)cells[2 * i] | ((uint32_t)cells[2 * i + 1] << 16);
+        };
+        if (count > 0) {
+            for (int j = tid; j < nr; j += nt) {
+                const size_t g = base + r_list[j];
+                const int cursor = s.goal_cursors[g];
+                int ci = cursor % clen;
+                ci += ci < 0 ? clen : 0;
+                int start = s.goal_candidates[g * clen + ci] % count;
+                start += start < 0 ? count : 0;
+                r_cursor[j] = cursor;
+                r_start[j] = start;
+                r_pref[2 * j] = cand(start);
+                r_pref[2 * j + 1] = cand((int64_t)start + 1);
+            }
+        }
+        __syncthreads();
+        if (tid == 0) {
+            for (int j = 0; j < nr && count > 0; ++j) {
+                const int a = (int)r_list[j];
+                const uint32_t cur = s_cur[a];
+                uint32_t chosen = kEmpty;
+                for (int attempt = 0; attempt < count; ++attempt) {
+                    const uint32_t c = attempt < 2 ? r_pref[2 * j + attempt]
+                                                   : cand((int64_t)r_start[j] + attempt);
+                    const uint32_t x = c & 0xFFFFu, y = c >> 16;
+                    if (c == cur || x >= (uint32_t)W || y >= (uint32_t)H) continue;
+                    const uint32_t cell = x * H + y;
+                    if ((goal_bits[cell >> 5] >> (cell & 31)) & 1u) continue;
+                    goal_bits[cell >> 5] |= 1u << (cell & 31);
+                    chosen = c;
+                    break;
+                }
+                r_pref[2 * j] = chosen;
+                if (chosen != kEmpty) {
+                    s_goal[a] = chosen;
+                    s_flag[a] |= 0x8000;  // goal changed this step
+                }
+            }
+            s.step_counts[env] = steps + 1;
+        }
+        __syncthreads();
+        for (int j = tid; j < nr && count > 0; j += nt) {
+            const uint32_t c = r_pref[2 * j];
+            if (c == kEmpty) continue;
+            const size_t g = base + r_list[j];
+            s.goal_x[g] = (uint16_t)(c & 0xFFFFu);
+            s.goal_y[g] = (uint16_t)(c >> 16);
+            s.goal_changed[g] = 1;
+            s.goal_cursors[g] = r_cursor[j] + 1;
+        }
+    } else if (tid == 0) {
         const int count = s.env_counts[env];
         const int offset = s.env_offsets[env];
         for (int a = 0; a < A; ++a) {
@@ -752,10 +867,18 @@ int check_sim(const jl_sim_t* s) {
         !s->actions || !s->arrived || !s->goal_changed || !s->rewards || !s->terminated ||
         !s->truncated || !s->step_counts || !s->state_packed)
         return JL_ERR_ARG;
-    if (s->task_mode != JL_TASK_LIFELONG && s->task_mode != JL_TASK_STANDARD_MAPF) return JL_ERR_ARG;
-    if (s->task_mode == JL_TASK_LIFELONG &&
-        (!s->free_cells || !s->env_offsets || !s->env_counts || !s->rng_state))
+    if (s->task_mode != JL_TASK_LIFELONG && s->task_mode != JL_TASK_STANDARD_MAPF &&
+        s->task_mode != JL_TASK_COSTTRACER)
         return JL_ERR_ARG;
+    if (s->task_mode == JL_TASK_LIFELONG) {
+        if (s->goal_candidates) {
+            if (!s->candidate_cells || !s->candidate_counts || !s->goal_cursors ||
+                s->candidate_length <= 0 || s->candidate_stride <= 0)
+                return JL_ERR_ARG;
+        } else if (!s->free_cells || !s->env_offsets || !s->env_counts || !s->rng_state) {
+            return JL_ERR_ARG;
+        }
+    }
     return JL_OK;
 }
 
@@ -777,30 +900,31 @@ extern "C" int jl_encode_map(const int32_t* grids, uint32_t* grid_bits, int32_t 
 extern "C" int jl_step(const jl_sim_t* s, jl_stream_t stream) {
     int rc = check_sim(s);
     if (rc) return rc;
-    const StepLayout L = step_layout(s->n_agents, s->map_w, s->map_h);
+    const StepLayout L =
+        step_layout(s->n_agents, s->map_w, s->map_h, s->task_mode == JL_TASK_LIFELONG);
     if (L.total > 160 * 1024) return JL_ERR_ARG;
     const int nt = step_threads(s->n_agents);
     const bool dense = step_dense(s->map_w, s->map_h);
-    const bool standard = s->task_mode == JL_TASK_STANDARD_MAPF;
     const bool one = step_per(s->n_agents) == 1;
-#define JL_STEP_LAUNCH(STD, DENSE, PER)                                                        \
-    hipLaunchKernelGGL((step_kernel<H, STD, DENSE, PER>), dim3(s->n_envs), dim3(nt), L.total, \
+#define JL_STEP_LAUNCH(MODE, DENSE, PER)                                                        \
+    hipLaunchKernelGGL((step_kernel<H, MODE, DENSE, PER>), dim3(s->n_envs), dim3(nt), L.total, \
                        (hipStream_t)stream, *s)
+#define JL_STEP_SHAPES(MODE)                                                            \
+    if (dense) {                                                                        \
+        if (one) JL_STEP_LAUNCH(MODE, true, 1); else JL_STEP_LAUNCH(MODE, true, 4);     \
+    } else {                                                                            \
+        if (one) JL_STEP_LAUNCH(MODE, false, 1); else JL_STEP_LAUNCH(MODE, false, 4);   \
+    }
     JL_DISPATCH_H(s->map_h, {
-        if (standard) {
-            if (dense) {
-                if (one) JL_STEP_LAUNCH(true, true, 1); else JL_STEP_LAUNCH(true, true, 4);
-            } else {
-                if (one) JL_STEP_LAUNCH(true, false, 1); else JL_STEP_LAUNCH(true, false, 4);
-            }
+        if (s->task_mode == JL_TASK_STANDARD_MAPF) {
+            JL_STEP_SHAPES(kModeStandard)
+        } else if (s->task_mode == JL_TASK_COSTTRACER) {
+            JL_STEP_SHAPES(kModeCost)
         } else {
-            if (dense) {
-                if (one) JL_STEP_LAUNCH(false, true, 1); else JL_STEP_LAUNCH(false, true, 4);
-            } else {
-                if (one) JL_STEP_LAUNCH(false, false, 1); else JL_STEP_LAUNCH(false, false, 4);
-            }
+            JL_STEP_SHAPES(kModeLifelong)
         }
     });
+#undef JL_STEP_SHAPES
 #undef JL_STEP_LAUNCH
     return launch_status();
 }

@@ -26,6 +26,9 @@ from ._abi import MagatDesc, MapfGPTDesc, SimDesc, check, load_library
 
 TASK_LIFELONG = 0
 TASK_STANDARD_MAPF = 1
+# CostTracer steps (rebuttal/online-rl/native/src/cuda_backend/grid_world_cuda.h:44-46)
+TASK_COSTTRACER = 2
+_TASK_NAMES = {TASK_LIFELONG: "lifelong", TASK_STANDARD_MAPF: "standard_mapf", TASK_COSTTRACER: "costtracer"}
 PYG_OBS_DIAM = 13
 PYG_OBS_AREA = PYG_OBS_DIAM * PYG_OBS_DIAM
 RADIUS = 5
@@ -47,6 +50,10 @@ def _stream(device: torch.device) -> int:
 
 
 def _parse_task_mode(mode: str) -> int:
+    """grid_world_simulator.cpp:30-40 of rebuttal/online-rl/native/src/cuda_backend
+    (the main tree's parser without "costtracer" has the same message)."""
+    if mode == "costtracer":
+        return TASK_COSTTRACER
     if mode == "lifelong":
         return TASK_LIFELONG
     if mode == "standard_mapf":
@@ -459,6 +466,11 @@ class GridWorldSimulator(_Base, _PygModeMixin, _PygStorage):
             self.t_changed_state_packed = torch.zeros((N, 8), **i16)
             self.t_goal_changed_count = torch.zeros((1,), dtype=torch.int64, device=device)
             self.t_rng_states = torch.zeros((E * max(n_agents, 32),), dtype=torch.int64, device=device)
+        # deterministic lifelong goals (set_goal_candidates); unset = generator draws
+        self.t_goal_candidates = None
+        self.t_candidate_cells = None
+        self.t_candidate_counts = None
+        self.t_goal_cursors = None
         self._sim = self._make_sim_desc()
         self._sim_ref = ctypes.byref(self._sim)
         self._magat = self._magat_desc(self.t_state_packed, self.t_energy_maps)
@@ -491,7 +503,45 @@ class GridWorldSimulator(_Base, _PygModeMixin, _PygStorage):
             env_offsets=_ptr(self.t_offsets),
             env_counts=_ptr(self.t_counts),
             rng_state=_ptr(self.t_rng_states),
+            goal_candidates=_ptr(self.t_goal_candidates),
+            candidate_cells=_ptr(self.t_candidate_cells),
+            candidate_counts=_ptr(self.t_candidate_counts),
+            goal_cursors=_ptr(self.t_goal_cursors),
+            candidate_length=0 if self.t_goal_candidates is None else int(self.t_goal_candidates.size(2)),
+            candidate_stride=0 if self.t_candidate_cells is None else int(self.t_candidate_cells.size(1)),
         )
+
+    def set_goal_candidates(self, candidates: torch.Tensor, cells: torch.Tensor, counts: torch.Tensor) -> None:
+        """Deterministic lifelong goals (grid_world_simulator.cpp:901-918 of
+        rebuttal/online-rl/native/src/cuda_backend): agent i on its goal takes
+        the first cell of its env's list ``cells[e, :counts[e]]``, starting at
+        ``candidates[e, i, cursor % K]``, that is neither its own cell nor a
+        goal held by another agent; agents are served in id order, so the
+        result is the one the CPU twin (rebuttal/online-il/tasks.py:51-65)
+        computes.  Resets ``goal_cursors`` to zero."""
+        dev = self._device
+        _require(candidates.is_cuda and cells.is_cuda and counts.is_cuda, "goal candidates must be CUDA")
+        _require(candidates.device == dev and cells.device == dev and counts.device == dev,
+                 "goal source device mismatch")
+        _require(candidates.dtype == torch.int32 and cells.dtype == torch.int16 and counts.dtype == torch.int32,
+                 "goal source dtype mismatch")
+        _require(candidates.dim() == 3 and candidates.size(0) == self.n_envs
+                 and candidates.size(1) == self.n_agents and candidates.size(2) > 0, "candidates must be [N,A,K]")
+        _require(cells.dim() == 3 and cells.size(0) == self.n_envs and cells.size(2) == 2, "cells must be [N,F,2]")
+        _require(counts.numel() == self.n_envs and int(counts.min().item()) > self.n_agents
+                 and int(counts.max().item()) <= cells.size(1), "invalid free-cell counts")
+        with torch.cuda.device(dev):
+            self.t_goal_candidates = candidates.contiguous()
+            self.t_candidate_cells = cells.contiguous()
+            self.t_candidate_counts = counts.contiguous()
+            self.t_goal_cursors = torch.zeros((self.n_envs, self.n_agents), dtype=torch.int32, device=dev)
+        self._sim = self._make_sim_desc()
+        self._sim_ref = ctypes.byref(self._sim)
+
+    @property
+    def goal_cursors(self):
+        """Goals taken per agent since set_goal_candidates (bind.cpp:135 of the online-rl fork)."""
+        return self.t_goal_cursors
 
     # -- lifecycle ---------------------------------------------------------
     def init_rng(self, seed) -> None:
@@ -687,7 +737,7 @@ class GridWorldSimulator(_Base, _PygModeMixin, _PygStorage):
     # -- properties --------------------------------------------------------
     @property
     def task_mode(self) -> str:
-        return "lifelong" if self._task_mode == TASK_LIFELONG else "standard_mapf"
+        return _TASK_NAMES[self._task_mode]
 
     @property
     def max_episode_steps(self) -> int:

@@ -41,7 +41,11 @@ enum {
     JL_ERR_CAPACITY = -3     /* an edge buffer too small for the worst case */
 };
 
-enum { JL_TASK_LIFELONG = 0, JL_TASK_STANDARD_MAPF = 1 };
+/* Task modes (grid_world_cuda.h:44-46 of rebuttal/online-rl/native/src/cuda_backend):
+ * lifelong goal resampling, standard MAPF with arrival latches and horizon,
+ * and CostTracer (moves and step counts only; goals are advanced by
+ * jl_costtracer_reward_goals). */
+enum { JL_TASK_LIFELONG = 0, JL_TASK_STANDARD_MAPF = 1, JL_TASK_COSTTRACER = 2 };
 
 /* Conflict outcome per agent and step (transition_adapters.py:361-455). */
 enum {
@@ -83,6 +87,17 @@ typedef struct jl_sim {
     const int32_t* env_offsets; /* [E] first free cell of each env in free_cells */
     const int32_t* env_counts;  /* [E] number of free cells of each env */
     uint64_t* rng_state;        /* [E*A] per-agent generator state */
+    /* Deterministic lifelong goals: when goal_candidates is not NULL, agents
+     * on their goal take new goals in agent order from per-agent candidate
+     * start lists instead of the generator (set_goal_candidates and the
+     * canonical-order branch of rebuttal/online-rl/native/src/cuda_backend/
+     * grid_world_simulator.cpp:901-918, 128_agents_map_step.cu:303-330). */
+    const int32_t* goal_candidates;  /* [E, A, candidate_length] start indices */
+    const uint16_t* candidate_cells; /* [E, candidate_stride, 2] (x, y) per env */
+    const int32_t* candidate_counts; /* [E] cells of each env's list in use */
+    int32_t* goal_cursors;           /* [E, A] goals taken so far (in/out) */
+    int32_t candidate_length;
+    int32_t candidate_stride;
 } jl_sim_t;
 
 /* Pack int32 [E, W, H] grids (nonzero = obstacle) into bitmaps.

@@ -247,15 +247,73 @@ static void write_state_row(uint16_t* row, int env, int agent, int px, int py, i
     row[7] = (uint16_t)reset;
 }
 
+/* Deterministic lifelong goals of one env after its move: the canonical
+ * agent order of assign_goals (rebuttal/online-il/tasks.py:51-65), the CPU
+ * twin of the candidate branch of 128_agents_map_step.cu:303-330 in
+ * rebuttal/online-rl/native/src/cuda_backend.  Goals held by agents off
+ * their goal are reserved; each agent on its goal, in id order, takes the
+ * first cell of the env's list, from candidates[cursor % K] on, that is not
+ * its own cell and not reserved, and reserves it.  Returns the number of
+ * agents that found no cell (the CPU twin raises for them; the device leaves
+ * their goal). */
+static int assign_candidate_goals(const jl_sim_t* s, int e, const int32_t* fin) {
+    const int A = s->n_agents, W = s->map_w, H = s->map_h;
+    const int K = s->candidate_length;
+    int count = s->candidate_counts[e];
+    if (count > s->candidate_stride) count = s->candidate_stride;
+    const uint16_t* cells = s->candidate_cells + (size_t)e * s->candidate_stride * 2;
+    uint8_t* reserved = (uint8_t*)calloc((size_t)W * H, 1);
+    uint8_t* reached = (uint8_t*)malloc((size_t)A);
+    for (int i = 0; i < A; ++i) {
+        const size_t g = (size_t)e * A + i;
+        reached[i] = fin[2 * i] == s->goal_x[g] && fin[2 * i + 1] == s->goal_y[g];
+        if (!reached[i]) reserved[s->goal_x[g] * H + s->goal_y[g]] = 1;
+    }
+    int failed = 0;
+    for (int i = 0; i < A && count > 0; ++i) {
+        if (!reached[i]) continue;
+        const size_t g = (size_t)e * A + i;
+        const int cursor = s->goal_cursors[g];
+        int ci = cursor % K;
+        if (ci < 0) ci += K;
+        int begin = s->goal_candidates[g * K + ci] % count;
+        if (begin < 0) begin += count;
+        int done = 0;
+        for (int off = 0; off < count && !done; ++off) {
+            const int k = (int)(((int64_t)begin + off) % count);
+            const int x = cells[2 * k], y = cells[2 * k + 1];
+            if (x < 0 || x >= W || y < 0 || y >= H) continue;
+            if (x == fin[2 * i] && y == fin[2 * i + 1]) continue;
+            if (reserved[x * H + y]) continue;
+            reserved[x * H + y] = 1;
+            s->goal_x[g] = (uint16_t)x;
+            s->goal_y[g] = (uint16_t)y;
+            s->goal_changed[g] = 1;
+            s->goal_cursors[g] = cursor + 1;
+            done = 1;
+        }
+        failed += !done;
+    }
+    free(reached);
+    free(reserved);
+    return failed;
+}
+
 /* Batched step, step_kernel 128_agents_map_step.cu:25-262 (positions are
  * cached as uint8 there, :39-43; supported maps are at most 256 wide so the
- * cache is exact).  The lifelong goal resampling (:265-343) draws from
- * cuRAND and is not restated: in lifelong mode this oracle leaves goals,
- * goal_changed (0) and reset flags (0) as a step without arrivals would. */
+ * cache is exact).  CostTracer steps (task mode 2, rebuttal/online-rl/native/
+ * src/cuda_backend/128_agents_map_step.cu:219-222) count the step and stop
+ * before the packed rows.  Lifelong steps with candidate lists take new goals
+ * in canonical order (assign_candidate_goals) and count the step; the
+ * generator-drawn resampling (:265-343) draws from cuRAND and is not
+ * restated: without candidate lists this oracle leaves goals, goal_changed
+ * (0) and reset flags (0) as a step without arrivals would. */
 void jlo_step(const jl_sim_t* s, int naive) {
     const int E = s->n_envs, A = s->n_agents, W = s->map_w, H = s->map_h;
     const int words = W * H / 32;
     const int standard = s->task_mode == JL_TASK_STANDARD_MAPF;
+    const int costtracer = s->task_mode == JL_TASK_COSTTRACER;
+    const int by_candidates = s->task_mode == JL_TASK_LIFELONG && s->goal_candidates != NULL;
     int32_t* cur = (int32_t*)malloc(sizeof(int32_t) * (size_t)A * 4);
     int32_t* fin = cur + 2 * A;
     uint8_t* cat = (uint8_t*)malloc((size_t)A);
@@ -289,6 +347,14 @@ void jlo_step(const jl_sim_t* s, int naive) {
             ocp[cell >> 5] |= 1u << (cell & 31); /* :202-210 */
             if (s->outcomes) s->outcomes[g] = cat[i];
         }
+        if (costtracer) {
+            s->step_counts[e] += 1;
+            continue;
+        }
+        if (by_candidates) {
+            assign_candidate_goals(s, e, fin);
+            s->step_counts[e] += 1;
+        }
         if (standard) {
             int all = 1;
             for (int i = 0; i < A; ++i) {
@@ -310,7 +376,7 @@ void jlo_step(const jl_sim_t* s, int naive) {
             const size_t g = (size_t)e * A + i;
             const int action = (standard && was_arrived[i]) ? 0 : s->actions[g]; /* :257-259 */
             write_state_row(s->state_packed + g * 8, e, i, fin[2 * i], fin[2 * i + 1], s->goal_x[g],
-                            s->goal_y[g], action, 0);
+                            s->goal_y[g], action, standard ? 0 : s->goal_changed[g]);
         }
     }
     free(was_arrived);

@@ -146,6 +146,20 @@ class OracleSim:
         cnt = np.ascontiguousarray(np.zeros(self.E) if step_counts is None else step_counts, dtype=np.int32)
         lib().jlo_load_state(ctypes.byref(self.desc), _p(pos), _p(gol), _p(arr), _p(cnt))
 
+    def set_goal_candidates(self, candidates, cells, counts) -> None:
+        """Candidate lists of the deterministic lifelong mode (host copies)."""
+        self.goal_candidates = np.ascontiguousarray(candidates, dtype=np.int32)
+        self.candidate_cells = np.ascontiguousarray(cells, dtype=np.int16).view(np.uint16)
+        self.candidate_counts = np.ascontiguousarray(counts, dtype=np.int32)
+        self.goal_cursors = np.zeros((self.E, self.A), np.int32)
+        d = self.desc
+        d.goal_candidates = _p(self.goal_candidates)
+        d.candidate_cells = _p(self.candidate_cells)
+        d.candidate_counts = _p(self.candidate_counts)
+        d.goal_cursors = _p(self.goal_cursors)
+        d.candidate_length = self.goal_candidates.shape[2]
+        d.candidate_stride = self.candidate_cells.shape[1]
+
     def step(self, actions=None, naive: bool = False) -> None:
         if actions is not None:
             self.actions[...] = actions
