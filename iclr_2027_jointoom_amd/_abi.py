@@ -158,6 +158,23 @@ SIGNATURES = {
     "jl_magat_occupancy": (c_int32, [ctypes.POINTER(MagatDesc), c_void_p]),
     "jl_magat_nodes": (c_int32, [ctypes.POINTER(MagatDesc), c_void_p]),
     "jl_magat_edges": (c_int32, [ctypes.POINTER(MagatDesc), c_void_p]),
+    "jl_mapfgpt_refresh_state": (
+        c_int32,
+        [ctypes.POINTER(MapfGPTDesc), c_void_p, c_void_p, c_void_p, c_void_p, c_void_p],
+    ),
+    "jl_costtracer_reward_goals": (
+        c_int32,
+        [ctypes.POINTER(SimDesc), ctypes.POINTER(MapfGPTDesc), c_void_p, c_void_p, c_int32, c_void_p,
+         c_void_p, c_void_p, c_void_p],
+    ),
+    "jl_costtracer_observe": (
+        c_int32, [ctypes.POINTER(SimDesc), ctypes.POINTER(MapfGPTDesc), c_void_p, c_void_p, c_void_p]
+    ),
+    "jl_costtracer_reset": (
+        c_int32,
+        [ctypes.POINTER(SimDesc), c_void_p, c_void_p, c_int32, c_void_p, c_void_p, c_void_p, c_int32,
+         c_void_p],
+    ),
     "jl_expand_records": (c_int32, [ctypes.POINTER(RecordsDesc), c_void_p]),
     "jl_decode_to_uint8": (c_int32, [c_void_p, c_void_p, c_int64, c_int32, c_void_p]),
     "jl_error_string": (ctypes.c_char_p, [c_int32]),

@@ -872,6 +872,26 @@ __global__ __launch_bounds__(256) void agent_at_cell_kernel(jl_mapfgpt_t b) {
         if (map[c] == 0x7FFFFFFF) map[c] = -1;
 }
 
+// Diagnostics of a refresh without tokens (refresh_distances): the BFS
+// overflow counts and bad goals pass 1 left in agent_info, summed the way the
+// token pass sums them (diagnostics[0] and [3]; the token pass's scatter
+// counts, [2] and the off-map part of [3], belong to token builds only).
+__global__ __launch_bounds__(256) void refresh_diag_kernel(jl_mapfgpt_t b, int n) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    const uint32_t info = i < n ? b.agent_info[i] : 0u;
+    int over = (int)(info >> kInfoOverflowShift);
+    int bad = (info & kInfoBadGoal) ? 1 : 0;
+#pragma unroll
+    for (int m = 1; m < kWave; m <<= 1) {
+        over += __shfl_xor(over, m, kWave);
+        bad += __shfl_xor(bad, m, kWave);
+    }
+    if ((threadIdx.x & (kWave - 1)) == 0) {
+        if (over) atomicAdd(b.diagnostics + 0, over);
+        if (bad) atomicAdd(b.diagnostics + 3, bad);
+    }
+}
+
 int check_builder(const jl_mapfgpt_t* b) {
     if (!b || b->n_envs <= 0 || b->n_agents <= 0) return JL_ERR_ARG;
     if (!profile_ok(b->map_w, b->map_h)) return JL_ERR_PROFILE;
@@ -997,6 +1017,29 @@ extern "C" int jl_mapfgpt_build_state(const jl_mapfgpt_t* b, const int16_t* cur_
                                       const int16_t* goal_y, jl_stream_t stream) {
     if (!cur_x || !cur_y || !goal_x || !goal_y) return JL_ERR_ARG;
     return build<false>(b, nullptr, cur_x, cur_y, goal_x, goal_y, (hipStream_t)stream);
+}
+
+extern "C" int jl_mapfgpt_refresh_state(const jl_mapfgpt_t* b, const int16_t* cur_x,
+                                        const int16_t* cur_y, const int16_t* goal_x,
+                                        const int16_t* goal_y, jl_stream_t stream) {
+    if (!cur_x || !cur_y || !goal_x || !goal_y) return JL_ERR_ARG;
+    int rc = check_builder(b);
+    if (rc) return rc;
+    const int W = b->map_w;
+    const int N = b->n_envs * b->n_agents;
+    hipStream_t st = (hipStream_t)stream;
+    JL_DISPATCH_H(b->map_h, {
+        if (W <= 64) {
+            rc = launch_pass1<H, 1, false>(b, nullptr, cur_x, cur_y, goal_x, goal_y, st);
+        } else if (W <= 128) {
+            rc = launch_pass1<H, 2, false>(b, nullptr, cur_x, cur_y, goal_x, goal_y, st);
+        } else {
+            rc = launch_pass1<H, 4, false>(b, nullptr, cur_x, cur_y, goal_x, goal_y, st);
+        }
+        if (rc) return rc;
+    });
+    hipLaunchKernelGGL(refresh_diag_kernel, dim3((N + 255) / 256), dim3(256), 0, st, *b, N);
+    return launch_status();
 }
 
 extern "C" int jl_mapfgpt_append_actions(const jl_mapfgpt_t* b, const uint8_t* actions,

@@ -342,6 +342,19 @@ class MapfGPTObservationBuilder(_Base):
             "MAPF-GPT resident token generation",
         )
 
+    def refresh_distances(self, cur_x, cur_y, goal_x, goal_y) -> None:
+        """Goal-cache refresh and BFS of changed goals, no tokens
+        (mapf_gpt_builder.cpp:200-212 of rebuttal/online-rl/native/src/cuda_backend)."""
+        for t, name in ((cur_x, "cur_x"), (cur_y, "cur_y"), (goal_x, "goal_x"), (goal_y, "goal_y")):
+            self._check_state(t, name)
+        check(
+            self._lib.jl_mapfgpt_refresh_state(
+                self._desc_ref, cur_x.data_ptr(), cur_y.data_ptr(), goal_x.data_ptr(), goal_y.data_ptr(),
+                _stream(self._device),
+            ),
+            "MAPF-GPT distance refresh",
+        )
+
     def append_actions(self, actions: torch.Tensor) -> None:
         """mapf_gpt_builder.cpp:170-192."""
         _require(actions.is_cuda, "actions must be on a CUDA device")
@@ -976,6 +989,88 @@ def parse_profile(text: str) -> tuple[int, int]:
     return w, h
 
 
+# ---------------------------------------------------------------------------
+# CostTracer (rebuttal/online-rl/native/src/cuda_backend/costtracer.cu:87-127,
+# bound as module functions in bind.cpp:96-98 of that tree)
+# ---------------------------------------------------------------------------
+def _ct_check(t, dtype, n, device) -> None:
+    _require(
+        isinstance(t, torch.Tensor) and t.is_cuda and t.is_contiguous() and t.dtype == dtype
+        and t.numel() == n and t.device == device,
+        "CostTracer tensor shape/dtype/device mismatch",
+    )
+
+
+def _ct_pair(sim, builder) -> None:
+    _require(
+        builder.n_envs == sim.n_envs and builder.n_agents == sim.n_agents
+        and builder._MAP_W == sim._MAP_W and builder._MAP_H == sim._MAP_H and builder._device == sim._device,
+        "CostTracer simulator and builder must share envs, agents, map size and device",
+    )
+
+
+def costtracer_reward_goals(sim, builder, best, targets, cursor, rewards, reached) -> None:
+    """Progress rewards, goal hits and the next goals of the streams
+    (costtracer.cu:87-103)."""
+    n = sim.n_envs * sim.n_agents
+    dev = sim._device
+    _ct_pair(sim, builder)
+    _ct_check(best, torch.int32, n, dev)
+    _ct_check(cursor, torch.int32, n, dev)
+    _ct_check(rewards, torch.float32, n, dev)
+    _ct_check(reached, torch.float32, n, dev)
+    _require(
+        targets.dim() == 4 and targets.size(0) == sim.n_envs and targets.size(1) == sim.n_agents
+        and targets.size(2) > sim.max_episode_steps and targets.size(3) == 2,
+        "goal stream must be [N,A,K>horizon,2]",
+    )
+    _ct_check(targets, torch.int16, targets.numel(), dev)
+    check(
+        sim._lib.jl_costtracer_reward_goals(
+            sim._sim_ref, builder._desc_ref, best.data_ptr(), targets.data_ptr(), int(targets.size(2)),
+            cursor.data_ptr(), rewards.data_ptr(), reached.data_ptr(), _stream(dev),
+        ),
+        "CostTracer reward",
+    )
+
+
+def costtracer_observe(sim, builder, best, output) -> None:
+    """2 x 11 x 11 observation per agent (costtracer.cu:105-113)."""
+    n = sim.n_envs * sim.n_agents
+    dev = sim._device
+    _ct_pair(sim, builder)
+    _ct_check(best, torch.int32, n, dev)
+    _ct_check(output, torch.float32, n * 242, dev)
+    check(
+        sim._lib.jl_costtracer_observe(sim._sim_ref, builder._desc_ref, best.data_ptr(), output.data_ptr(),
+                                       _stream(dev)),
+        "CostTracer observation",
+    )
+
+
+def costtracer_reset(sim, pos, goal, episodes, cursors, best, reserved, horizon) -> None:
+    """Envs at the horizon start the next episode of the bank
+    (costtracer.cu:115-127); ``reserved`` is unused, as there."""
+    n = sim.n_envs * sim.n_agents
+    dev = sim._device
+    _require(
+        pos.dim() == 4 and pos.size(1) == sim.n_envs and pos.size(2) == sim.n_agents and pos.size(3) == 2,
+        "reset bank must be [episodes,N,A,2]",
+    )
+    _ct_check(pos, torch.int16, pos.numel(), dev)
+    _ct_check(goal, torch.int16, pos.numel(), dev)
+    _ct_check(episodes, torch.int32, sim.n_envs, dev)
+    _ct_check(cursors, torch.int32, n, dev)
+    _ct_check(best, torch.int32, n, dev)
+    check(
+        sim._lib.jl_costtracer_reset(
+            sim._sim_ref, pos.data_ptr(), goal.data_ptr(), int(pos.size(0)), episodes.data_ptr(),
+            cursors.data_ptr(), best.data_ptr(), int(horizon), _stream(dev),
+        ),
+        "CostTracer reset",
+    )
+
+
 def profile(w: int, h: int) -> types.SimpleNamespace:
     """Module-like namespace with COMPILED_MAP_W/H and the three classes for a WxH map."""
     key = (int(w), int(h))
@@ -990,6 +1085,9 @@ def profile(w: int, h: int) -> types.SimpleNamespace:
             StatelessGridWorldSimulator=type(
                 "StatelessGridWorldSimulator", (StatelessGridWorldSimulator,), attrs
             ),
+            costtracer_reward_goals=costtracer_reward_goals,
+            costtracer_observe=costtracer_observe,
+            costtracer_reset=costtracer_reset,
         )
     return _PROFILES[key]
 

@@ -195,6 +195,15 @@ int jl_mapfgpt_build_state(const jl_mapfgpt_t* b, const int16_t* cur_x,
 
 /* append_actions(uint8 [E, A]).  Replaces mapf_gpt_append_actions_kernel,
  * mapf_gpt_cuda.cu:155-178. */
+/* Goal-cache refresh and BFS of changed goals from the resident split state,
+ * without tokens: state rows, labels, goal cache, cost_to_go (and its tiled
+ * copy), diagnostics [0] and [3].  Replaces
+ * MapfGPTObservationBuilder::refresh_distances, mapf_gpt_builder.cpp:200-212 of
+ * rebuttal/online-rl/native/src/cuda_backend. */
+int jl_mapfgpt_refresh_state(const jl_mapfgpt_t* b, const int16_t* cur_x,
+                             const int16_t* cur_y, const int16_t* goal_x,
+                             const int16_t* goal_y, jl_stream_t stream);
+
 int jl_mapfgpt_append_actions(const jl_mapfgpt_t* b, const uint8_t* actions,
                               jl_stream_t stream);
 
@@ -270,6 +279,40 @@ int jl_magat_nodes(const jl_magat_t* m, jl_stream_t stream);
  * grid_world_cuda.cu:17-110, and generate_pyg_edges_kernel,
  * 128_agents_map_stateless_step.cu:854-935. */
 int jl_magat_edges(const jl_magat_t* m, jl_stream_t stream);
+
+/* ------------------------------------------------------------------------ */
+/* CostTracer (rebuttal/online-rl/native/src/cuda_backend/costtracer.{h,cu})  */
+/* The simulator runs in JL_TASK_COSTTRACER mode; distances come from the     */
+/* builder's fields after jl_mapfgpt_refresh_state (read from its tiled copy). */
+/* best, cursor: int32 [E*A]; rewards, reached: float [E*A].                  */
+/* ------------------------------------------------------------------------ */
+
+/* Progress reward (0.1 when the distance to the goal fell below best), the
+ * goal hit flag, and on a hit the next goal of the agent's stream
+ * targets int16 [E, A, target_length, 2] (best becomes -1).  Replaces
+ * costtracer_reward_goals / progress_goals, costtracer.cu:5-23, 87-103. */
+int jl_costtracer_reward_goals(const jl_sim_t* sim, const jl_mapfgpt_t* b, int32_t* best,
+                               const int16_t* targets, int32_t target_length,
+                               int32_t* cursor, float* rewards, float* reached,
+                               jl_stream_t stream);
+
+/* Observation float [E*A, 2, 11, 11]: occupancy of the window around each
+ * agent, and its distances normalised (cells without a distance placed 4
+ * past the largest, shifted to 0, inverted and divided by the range), with
+ * the progress feature -min(1, (d - best + 1) / 64) at the centre; best is
+ * set to the agent's distance when negative or when its goal was refreshed.
+ * Replaces costtracer_observe / observe, costtracer.cu:25-64, 105-113. */
+int jl_costtracer_observe(const jl_sim_t* sim, const jl_mapfgpt_t* b, int32_t* best,
+                          float* output, jl_stream_t stream);
+
+/* Envs whose step count reached `horizon` start the next episode of the bank
+ * (bank_positions/bank_goals int16 [bank_episodes, E, A, 2], episode =
+ * ++episodes[e] % bank_episodes): positions, goals, occupancy, cursors 0,
+ * best -1, step count 0.  Replaces costtracer_reset / reset_selected,
+ * costtracer.cu:66-85, 115-127. */
+int jl_costtracer_reset(const jl_sim_t* sim, const int16_t* bank_positions,
+                        const int16_t* bank_goals, int32_t bank_episodes, int32_t* episodes,
+                        int32_t* cursors, int32_t* best, int32_t horizon, jl_stream_t stream);
 
 /* ------------------------------------------------------------------------ */
 /* Compact expert records (one stage = one joint step of every env)          */

@@ -1,0 +1,136 @@
+"""CPU restatement of the CostTracer kernels (rebuttal/online-rl/native/src/
+cuda_backend/costtracer.cu) and of the distance refresh they read
+(MapfGPTObservationBuilder::refresh_distances, mapf_gpt_builder.cpp:200-212
+of the same tree), driven beside the C step oracle.
+
+TEST INFRASTRUCTURE ONLY: imported by tests/ and bench.py's cpu_baseline leg
+as the checker; the product path (iclr_2027_jointoom_amd) never imports it.
+
+* reward_goals follows progress_goals, costtracer.cu:5-23;
+* observe follows observe, costtracer.cu:25-64, cell by cell (the window
+  reductions as plain max/min over the 121 cells);
+* reset follows reset_selected, costtracer.cu:66-85.
+Pinned by a closed form on empty maps and by the reference's own vectorised
+statement of the observation (encode_numpy, rebuttal/online-rl/
+implementation/environments.py:30-47), restated in tests/test_oracle_costtracer.py.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+from oracle import oracle as _o
+
+UNREACHABLE = 0xFFFF
+
+
+class OracleCostTracer:
+    """Simulator in CostTracer mode + per-agent distance fields + the
+    reward/observation/reset state of one CudaEnvironment
+    (rebuttal/online-rl/implementation/environments.py:176-219)."""
+
+    def __init__(self, grids, n_agents: int, horizon: int):
+        self.grids = np.asarray(grids)
+        E, W, H = self.grids.shape
+        self.E, self.A, self.W, self.H = E, int(n_agents), W, H
+        self.sim = _o.OracleSim(self.grids, n_agents, task_mode=2, max_episode_steps=horizon)
+        self.fields = np.full((E, n_agents, W, H), UNREACHABLE, np.uint16)
+        self.goal_cache = np.full((E, n_agents, 2), -1, np.int64)
+        self.reset_flags = np.zeros((E, n_agents), np.uint8)
+        self.best = np.full((E, n_agents), -1, np.int64)
+        self.cursor = np.zeros((E, n_agents), np.int64)
+        self.rewards = np.zeros((E, n_agents), np.float32)
+        self.reached = np.zeros((E, n_agents), np.float32)
+
+    def goals(self) -> np.ndarray:
+        return np.stack([self.sim.goal_x, self.sim.goal_y], -1).astype(np.int64)
+
+    def refresh_distances(self) -> None:
+        """Goal-cache compare and BFS of changed goals (mapf_gpt_cuda.cu:121-152,
+        181-325 of the main tree)."""
+        goals = self.goals()
+        for e in range(self.E):
+            for a in range(self.A):
+                changed = not np.array_equal(goals[e, a], self.goal_cache[e, a])
+                self.reset_flags[e, a] = 1 if changed else 0
+                if changed:
+                    self.goal_cache[e, a] = goals[e, a]
+                    self.fields[e, a] = _o.bfs_u16(self.grids[e], goals[e, a])[0]
+
+    def observe(self) -> np.ndarray:
+        """float32 [E, A, 2, 11, 11]; updates best."""
+        E, A, W, H = self.E, self.A, self.W, self.H
+        out = np.zeros((E, A, 2, 11, 11), np.float32)
+        cur = self.sim.positions().astype(np.int64)
+        # occupancy from the simulator's bitmap after the step (grid_ocp)
+        bits = self.sim.grid_ocp.reshape(E, -1)
+        cells = np.arange(W * H)
+        occupied = ((bits[:, cells >> 5] >> (cells & 31).astype(np.uint32)) & 1).astype(bool).reshape(E, W, H)
+        for e in range(E):
+            for a in range(A):
+                cx, cy = int(cur[e, a, 0]), int(cur[e, a, 1])
+                f = self.fields[e, a]
+                d = np.full(121, -1, np.int64)
+                inside = np.zeros(121, bool)
+                for t in range(121):
+                    x, y = cx + t // 11 - 5, cy + t % 11 - 5
+                    if 0 <= x < W and 0 <= y < H:
+                        inside[t] = True
+                        raw = int(f[x, y])
+                        d[t] = -1 if raw == UNREACHABLE else raw
+                m_reach = max(0, int(np.max(np.maximum(d, 0))))
+                v = np.where(d < 0, d + 5 + m_reach, d)
+                v = v - int(v.min())
+                V = int(v.max())
+                current = int(f[cx, cy])
+                if self.best[e, a] < 0 or self.reset_flags[e, a]:
+                    self.best[e, a] = current
+                for t in range(121):
+                    x, y = cx + t // 11 - 5, cy + t % 11 - 5
+                    out[e, a, 0, t // 11, t % 11] = 1.0 if inside[t] and occupied[e, x, y] else 0.0
+                    if V > 0:
+                        out[e, a, 1, t // 11, t % 11] = np.float32(V - int(v[t])) / np.float32(V)
+                out[e, a, 1, 5, 5] = -np.minimum(np.float32(1.0),
+                                                 np.float32(current - int(self.best[e, a]) + 1) / np.float32(64.0))
+        return out
+
+    def step(self, actions, targets) -> None:
+        """update_actions + step (CostTracer mode) + reward_goals."""
+        self.sim.step(actions)
+        cur = self.sim.positions().astype(np.int64)
+        goals = self.goals()
+        K = targets.shape[2]
+        for e in range(self.E):
+            for a in range(self.A):
+                d = int(self.fields[e, a, cur[e, a, 0], cur[e, a, 1]])
+                self.rewards[e, a] = np.float32(0.1) if d < self.best[e, a] else np.float32(0.0)
+                self.best[e, a] = min(int(self.best[e, a]), d)
+                hit = bool(np.array_equal(cur[e, a], goals[e, a]))
+                self.reached[e, a] = 1.0 if hit else 0.0
+                if hit:
+                    k = int(self.cursor[e, a])
+                    self.cursor[e, a] = k + 1
+                    if k < K:
+                        self.sim.goal_x[e, a] = int(targets[e, a, k, 0])
+                        self.sim.goal_y[e, a] = int(targets[e, a, k, 1])
+                    self.best[e, a] = -1
+
+    def reset_due(self, bank_pos, bank_goal, episodes, horizon: int) -> None:
+        """reset_selected: envs at the horizon take the next bank episode."""
+        bank = bank_pos.shape[0]
+        for e in range(self.E):
+            if self.sim.step_counts[e] < horizon:
+                continue
+            episodes[e] += 1
+            ep = int(episodes[e]) % bank
+            self.sim.step_counts[e] = 0
+            self.sim.cur_x[e] = bank_pos[ep, e, :, 0]
+            self.sim.cur_y[e] = bank_pos[ep, e, :, 1]
+            self.sim.goal_x[e] = bank_goal[ep, e, :, 0]
+            self.sim.goal_y[e] = bank_goal[ep, e, :, 1]
+            self.cursor[e] = 0
+            self.best[e] = -1
+            ocp = self.sim.grid_ocp[e]
+            ocp[:] = 0
+            for x, y in bank_pos[ep, e]:
+                cell = int(x) * self.H + int(y)
+                ocp[cell >> 5] |= np.uint32(1 << (cell & 31))
