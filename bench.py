@@ -30,6 +30,11 @@ kernel's roofline and the C restatement of the same step as CPU baseline.
 ring and the HBM ring into build_tokens, once in the compact format (5 bytes
 per agent-step over the host link, rows rebuilt on the device) and once in the
 reference's 13-column row format, with the expansion kernel's roofline.
+
+`--workload costtracer` measures the CostTracer RL environment step of the
+online-RL tree (update_actions, a CostTracer-mode step, rewards and goal
+streams, the distance refresh of changed goals, the 2x11x11 observation, the
+horizon reset) at the C2 shape, with the observation kernel's roofline.
 """
 from __future__ import annotations
 
@@ -168,13 +173,26 @@ def run_gpu(args) -> dict:
     ext = profile(W, W)
     g = torch.from_numpy(grids.astype(np.int32)).to(dev)
     horizon = 1 << 30  # no env reaches its horizon inside the run: every step does full work
-    sim = ext.GridWorldSimulator(g, A, 0, E * W * W, 20260728, "standard_mapf", horizon)
+    sim = ext.GridWorldSimulator(g, A, 0, E * W * W, 20260728, args.task_mode, horizon)
     sim.load_state(
         torch.from_numpy(starts).to(dev),
         torch.from_numpy(goals).to(dev),
         torch.zeros((E, A), dtype=torch.uint8, device=dev),
         torch.zeros(E, dtype=torch.int32, device=dev),
     )
+    if args.task_mode == "lifelong":
+        # deterministic lifelong goals: per-env lists of the free cells and
+        # per-agent candidate start indices (the online-IL tasks' layout)
+        rng = np.random.default_rng(args.seed)
+        cells_l = [np.argwhere(gr == 0).astype(np.int16) for gr in grids]
+        stride = max(len(c) for c in cells_l)
+        cells = np.zeros((E, stride, 2), np.int16)
+        for e, c in enumerate(cells_l):
+            cells[e, :len(c)] = rng.permutation(c)
+        counts = np.array([len(c) for c in cells_l], np.int32)
+        cand = rng.integers(0, counts.min(), size=(E, A, 8)).astype(np.int32)
+        sim.set_goal_candidates(torch.from_numpy(cand).to(dev), torch.from_numpy(cells).to(dev),
+                                torch.from_numpy(counts).to(dev))
     builder = ext.MapfGPTObservationBuilder(g, A)
     builder.reset_histories()
     total_steps = args.warmup + args.steps
@@ -260,6 +278,7 @@ def run_gpu(args) -> dict:
             "bytes_per_launch": tok_bytes,
             "avg_launch_us": tok_avg_s * 1e6,
         },
+        "goals_reassigned": int(sim.goal_cursors.sum().item()) if args.task_mode == "lifelong" else None,
         "step_effective_GBps": value * B_STEP_NORTH_STAR / 1e9,
         "step_frac_of_peak": value * B_STEP_NORTH_STAR / PEAK_HBM_BPS,
         "device": torch.cuda.get_device_name(0),
@@ -617,6 +636,180 @@ def main_ring(args) -> int:
     return 0
 
 
+# CostTracer observation per agent: 11x11 uint16 window 242, 242 floats out 968,
+# the window's occupancy bits 16, position 4, refresh flag 2, best read+write 8
+B_CT_OBSERVE = 242 + 968 + 16 + 4 + 2 + 8
+
+
+def cpu_baseline_costtracer(args) -> dict:
+    """The CostTracer environment loop on the host cores (oracle/costtracer.py:
+    C step oracle + numpy observation + C BFS of changed goals), one block of
+    envs per worker process, as the reference's CpuPool runs its envs."""
+    from iclr_2027_jointoom_amd.synthetic import make_batch
+    from oracle.costtracer import run_costtracer_worker
+
+    cores = len(os.sched_getaffinity(0))
+    workers = max(1, min(cores, 16))
+    jobs = []
+    for w in range(workers):
+        grids, starts, goals = make_batch(7000 + w, args.cpu_envs, args.map, args.map, args.agents)
+        streams = np.stack([np.roll(goals, k + 1, axis=1) for k in range(16)], axis=2).astype(np.int16)
+        acts = np.random.default_rng(w).integers(0, 5, (args.cpu_steps, args.cpu_envs, args.agents)).astype(np.uint8)
+        jobs.append((grids, starts, goals, streams, acts, args.cpu_steps))
+    ctx = mp.get_context("fork")  # before any HIP call in this process
+    t1 = run_costtracer_worker(jobs[0])
+    with ctx.Pool(workers) as pool:
+        results = pool.map(run_costtracer_worker, jobs)
+    total = sum(n for _, n in results)
+    timed = max(t for t, _ in results)
+    return {
+        "value": total / timed,
+        "unit": "agent-steps/s",
+        "cores": workers,
+        "kind": "port",
+        "value_1core": t1[1] / t1[0],
+        "sample": (f"{workers} workers x {args.cpu_envs} envs x {args.agents} agents on {args.map}x{args.map} "
+                   f"p=0.2, {args.cpu_steps} CostTracer steps each (step, reward and goal stream, BFS of "
+                   f"changed goals, observation)"),
+    }
+
+
+def run_gpu_costtracer(args) -> dict:
+    """The CostTracer environment step of rebuttal/online-rl/implementation/
+    environments.py:206-217 (update_actions, step in CostTracer mode, reward
+    and goal streams, refresh_distances, observation) plus reset_due."""
+    import torch
+
+    from iclr_2027_jointoom_amd import profile
+    from iclr_2027_jointoom_amd.synthetic import make_batch
+
+    E, W, A = args.envs, args.map, args.agents
+    horizon = args.ct_horizon
+    print(f"[bench] costtracer: {E} maps {W}x{W}, {A} agents, horizon {horizon}", file=sys.stderr, flush=True)
+    grids, starts, goals = make_batch(args.seed, E, W, W, A, kind=args.map_kind)
+    rng = np.random.default_rng(args.seed)
+    bank = 2
+    bank_pos = np.stack([starts] + [np.stack([s[rng.permutation(A)] for s in starts]) for _ in range(bank - 1)])
+    bank_goal = np.stack([goals] + [np.stack([g[rng.permutation(A)] for g in goals]) for _ in range(bank - 1)])
+    dev = torch.device("cuda:0")
+    K = horizon + 1
+    # goal streams: each agent cycles through rolled copies of its env's goal set (free, distinct cells)
+    streams = torch.stack([torch.from_numpy(np.stack([np.roll(bank_goal[ep], k + 1, axis=1) for k in range(K)],
+                                                     axis=2).astype(np.int16)) for ep in range(bank)]).to(dev)
+    ext = profile(W, W)
+    g = torch.from_numpy(grids.astype(np.int32)).to(dev)
+    sim = ext.GridWorldSimulator(g, A, 0, E * W * W, 3, "costtracer", horizon)
+    builder = ext.MapfGPTObservationBuilder(g, A)
+    bp = torch.from_numpy(bank_pos.astype(np.int16)).to(dev)
+    bg = torch.from_numpy(bank_goal.astype(np.int16)).to(dev)
+    episodes = torch.zeros(E, dtype=torch.int32, device=dev)
+    stream = streams[0].contiguous()
+    cursor = torch.zeros((E, A), dtype=torch.int32, device=dev)
+    best = torch.full_like(cursor, -1)
+    reward = torch.empty((E, A), device=dev)
+    reached = torch.empty_like(reward)
+    obs = torch.empty((E, A, 2, 11, 11), device=dev)
+    sim.load_state(bp[0], bg[0], torch.zeros((E, A), dtype=torch.uint8, device=dev),
+                   torch.zeros(E, dtype=torch.int32, device=dev))
+    total = args.warmup + args.steps
+    gen = torch.Generator(device=dev).manual_seed(args.seed)
+    actions = torch.randint(0, 5, (total, E, A), dtype=torch.uint8, device=dev, generator=gen)
+
+    def observe(ev=None):
+        builder.refresh_distances(sim.cur_x, sim.cur_y, sim.goal_x, sim.goal_y)
+        if ev is not None:
+            ev[0].record()
+        ext.costtracer_observe(sim, builder, best, obs)
+        if ev is not None:
+            ev[1].record()
+
+    def one_step(s, ev=None):
+        sim.update_actions(actions[s])
+        sim.step_sim_only()
+        ext.costtracer_reward_goals(sim, builder, best, stream, cursor, reward, reached)
+        observe(ev)
+        # envs at the horizon restart from the bank (a no-op launch otherwise);
+        # the stream of a restarted env stays the one it had, as the bench
+        # keeps every env on its bank's first streams
+        ext.costtracer_reset(sim, bp, bg, episodes, cursor, best, episodes, horizon)
+
+    print("[bench] warmup (the first refresh computes every BFS field)", file=sys.stderr, flush=True)
+    observe()
+    for s in range(args.warmup):
+        one_step(s)
+    torch.cuda.synchronize()
+    if any(builder.diagnostics.cpu().tolist()):
+        raise RuntimeError(f"builder diagnostics non-zero: {builder.diagnostics.cpu().tolist()}")
+    obs_events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+                  for _ in range(args.steps)]
+    hits0 = int(cursor.sum().item())
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        one_step(args.warmup + i, obs_events[i])
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    obs_s = float(np.mean([a.elapsed_time(b) for a, b in obs_events])) / 1000.0
+    N = E * A
+    nbytes = B_CT_OBSERVE * N
+    return {
+        "value": N * args.steps / wall,
+        "ms_per_step": wall * 1000.0 / args.steps,
+        "roofline": {
+            "bound": "hbm",
+            "kernel": f"observe_kernel<{W}>",
+            "achieved": nbytes / obs_s / 1e9,
+            "peak": PEAK_HBM_BPS / 1e9,
+            "unit": "GB/s",
+            "frac": nbytes / obs_s / PEAK_HBM_BPS,
+            "traffic": None,
+            "bytes_per_launch": nbytes,
+            "avg_launch_us": obs_s * 1e6,
+        },
+        "goal_hits_in_timed_steps": int(cursor.sum().item()) - hits0,
+        "resets": int(episodes.sum().item()),
+        "device": torch.cuda.get_device_name(0),
+    }
+
+
+def main_costtracer(args) -> int:
+    base = None
+    if not args.no_cpu_baseline:
+        print("[bench] cpu baseline", file=sys.stderr, flush=True)
+        base = cpu_baseline_costtracer(args)
+    res = run_gpu_costtracer(args)
+    line = {
+        "metric": "agent-steps/sec incl. obs/token build on 1 GPU; % of HBM roofline",
+        "value": res["value"],
+        "unit": "agent-steps/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": res["ms_per_step"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int16/int32 (integer) + float32 observations",
+        "data": "synthetic (seeded i.i.d. maps p=0.2, largest component; distinct starts/goals; goal streams "
+                "of free cells; uniform random actions)",
+        "config": {
+            "workload": "CostTracer environment step: step + reward/goal streams + distance refresh + "
+                        "2x11x11 observation + reset",
+            "envs": args.envs,
+            "agents": args.agents,
+            "map": f"{args.map}x{args.map}",
+            "task_mode": "costtracer",
+            "horizon": args.ct_horizon,
+        },
+        "roofline": res["roofline"],
+        "cpu_baseline": base,
+        "goal_hits_in_timed_steps": res["goal_hits_in_timed_steps"],
+        "device": res["device"],
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
 def main() -> int:
     p = argparse.ArgumentParser(description=__doc__.split("\n", 1)[0])
     p.add_argument("--gpus", type=int, default=1)
@@ -633,15 +826,19 @@ def main() -> int:
                    help="only run 3 device copies of 256 MiB (PMC byte-counter calibration)")
     p.add_argument("--graph", action="store_true",
                    help="replay each step from a captured HIP graph (iclr_2027_jointoom_amd/graphs.py)")
-    p.add_argument("--workload", choices=("resident", "magat", "c5", "ring"), default="resident",
+    p.add_argument("--workload", choices=("resident", "magat", "c5", "ring", "costtracer"), default="resident",
                    help="resident: the north-star MAPF-GPT loop (C2+C3); magat: the C4 MAGAT stateful "
                         "step; c5: the resident loop at C5 (256 envs x 1024 agents, 256x256 warehouses); "
-                        "ring: C5 frozen records streamed through the HBM ring into build_tokens")
+                        "ring: C5 frozen records streamed through the HBM ring into build_tokens; "
+                        "costtracer: the CostTracer RL environment step at the C2 shape")
     p.add_argument("--map-kind", choices=("iid", "maze", "warehouse"), default="iid")
     p.add_argument("--ring-workers", type=int, default=8, help="record producer processes (ring workload)")
     p.add_argument("--ring-slots", type=int, default=4, help="stage slots of the ring (ring workload)")
     p.add_argument("--ring-compact-only", action="store_true",
                    help="skip the row-format comparison run (ring workload)")
+    p.add_argument("--ct-horizon", type=int, default=512, help="episode horizon (costtracer workload)")
+    p.add_argument("--task-mode", choices=("standard_mapf", "lifelong"), default="standard_mapf",
+                   help="resident workload: standard MAPF, or lifelong with deterministic candidate goals")
     args = p.parse_args()
     if args.workload == "ring":
         for flag, name, value in (("--envs", "envs", 256), ("--agents", "agents", 1024),
@@ -683,6 +880,12 @@ def main() -> int:
         return main_magat(args)
     if args.workload == "ring":
         return main_ring(args)
+    if args.workload == "costtracer":
+        if "--steps" not in sys.argv:
+            args.steps = 100
+        if "--cpu-steps" not in sys.argv:
+            args.cpu_steps = 40
+        return main_costtracer(args)
     base = None
     if not args.no_cpu_baseline:
         print("[bench] cpu baseline", file=sys.stderr, flush=True)
@@ -715,13 +918,14 @@ def main() -> int:
             "envs": args.envs,
             "agents": args.agents,
             "map": f"{args.map}x{args.map}",
-            "task_mode": "standard_mapf",
+            "task_mode": args.task_mode,
         },
         "roofline": res["roofline"],
         "cpu_baseline": base,
         "gpu_ms_per_step": res["gpu_ms_per_step"],
         "step_effective_GBps": res["step_effective_GBps"],
         "step_frac_of_peak": res["step_frac_of_peak"],
+        "goals_reassigned": res["goals_reassigned"],
         "device": res["device"],
     }
     print(json.dumps(line), flush=True)

@@ -4,7 +4,8 @@
 // (r < R, so W <= 64*R); a row is held as HW 64-bit masks over its H
 // columns.  A level expands the frontier with shifts inside the row
 // (y +- 1, carrying across words) and with the frontier rows of the lanes
-// above/below (x +- 1, via ds_bpermute), masks with free & ~visited, and
+// above/below (x +- 1, via DPP whole-wavefront shifts by one lane, and
+// readlane across the 64-row groups), masks with free & ~visited, and
 // stops when no lane found a new cell.  Newly reached cells get their level
 // written into an LDS distance array; every other access is a register op,
 // so a level costs O(R*HW) VALU work instead of one thread per frontier
@@ -16,6 +17,28 @@
 #include "jl_common.h"
 
 namespace jl {
+
+// Value of lane - 1 (lane 0 reads 0) and of lane + 1 (lane 63 reads 0): DPP
+// wave_shr:1 / wave_shl:1 on both halves, no LDS round trip.  Every lane of
+// the wavefront must be active.
+__device__ __forceinline__ uint64_t from_lane_below(uint64_t v) {
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)v, 0x138, 0xF, 0xF, false);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(v >> 32), 0x138, 0xF, 0xF, false);
+    return ((uint64_t)hi << 32) | lo;
+}
+
+__device__ __forceinline__ uint64_t from_lane_above(uint64_t v) {
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)v, 0x130, 0xF, 0xF, false);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(v >> 32), 0x130, 0xF, 0xF, false);
+    return ((uint64_t)hi << 32) | lo;
+}
+
+// Value of a fixed lane, wavefront-uniform.
+__device__ __forceinline__ uint64_t lane_value(uint64_t v, int lane) {
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, lane);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), lane);
+    return ((uint64_t)hi << 32) | lo;
+}
 
 template <int H>
 struct RowWords {
@@ -95,20 +118,15 @@ __device__ int wave_bfs(const uint64_t (&fr)[R][RowWords<H>::HW], int gx, int gy
 #pragma unroll
             for (int k = 0; k < HW; ++k) {
                 // vertical neighbours: row x-1 and x+1 of the same column word
-                const uint64_t from_prev_lane = shfl64(front[r][k], lane - 1);
-                const uint64_t from_next_lane = shfl64(front[r][k], lane + 1);
-                uint64_t up = from_prev_lane, down = from_next_lane;
+                uint64_t up = from_lane_below(front[r][k]);
+                uint64_t down = from_lane_above(front[r][k]);
                 if (r > 0) {
-                    const uint64_t wrap = shfl64(front[r - 1][k], kWave - 1);
+                    const uint64_t wrap = lane_value(front[r - 1][k], kWave - 1);
                     if (lane == 0) up = wrap;
-                } else if (lane == 0) {
-                    up = 0;
                 }
                 if (r + 1 < R) {
-                    const uint64_t wrap = shfl64(front[r + 1][k], 0);
+                    const uint64_t wrap = lane_value(front[r + 1][k], 0);
                     if (lane == kWave - 1) down = wrap;
-                } else if (lane == kWave - 1) {
-                    down = 0;
                 }
                 // horizontal neighbours inside the row (y+1: <<1, y-1: >>1)
                 uint64_t left = front[r][k] << 1;
@@ -138,7 +156,9 @@ __device__ int wave_bfs(const uint64_t (&fr)[R][RowWords<H>::HW], int gx, int gy
                 }
             }
         }
-        if (kCountOverflow) {
+        // a level of more than kMaxFrontier = 64 * 64 cells has a lane with
+        // more than 64 of them, so the sum is only needed then
+        if (kCountOverflow && __any(local > kMaxFrontier / kWave)) {
 #pragma unroll
             for (int off = 32; off > 0; off >>= 1) local += __shfl_xor(local, off, kWave);
             if (local > kMaxFrontier) overflow += local - kMaxFrontier;

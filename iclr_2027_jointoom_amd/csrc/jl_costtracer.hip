@@ -10,15 +10,18 @@
 // Distances are read from the builder's tiled fields (8 x 8 tiles of uint16,
 // one 128-byte line each), which hold exactly what the builder last wrote into
 // cost_to_go: an 11 x 11 window touches 4 to 9 lines instead of 11 to 22
-// row-major ones.  The observation runs one wavefront per agent (two window
-// cells per lane, the three window reductions as 64-lane butterflies) and
-// writes the agent's 242 floats as contiguous dword stores.
+// row-major ones.  The observation runs four agents per wavefront (two
+// window cells per lane and agent, all loads of the four in flight together,
+// the window reductions as DPP steps); the 16 agents of a workgroup assemble
+// their floats in LDS, which leave as one contiguous run of 16-byte stores.
 #include "jl_common.h"
 
 namespace jl {
 namespace {
 
-constexpr int kObsWaves = 4;  // agents per workgroup of the observation
+constexpr int kObsWaves = 4;  // wavefronts per workgroup of the observation
+constexpr int kObsPer = 4;    // agents per wavefront
+constexpr int kObsAgents = kObsWaves * kObsPer;
 constexpr int kObsCells = kCostTokens;       // 121
 constexpr int kObsFloats = 2 * kObsCells;    // 242
 constexpr int kObsCentre = kRadius * kDiam + kRadius;  // 60
@@ -31,17 +34,25 @@ __device__ __forceinline__ uint32_t tile_at(int x, int y) {
            (uint32_t)((x & 7) * 8 + (y & 7));
 }
 
-__device__ __forceinline__ int wave_max(int v) {
-#pragma unroll
-    for (int m = 1; m < kWave; m <<= 1) v = max(v, __shfl_xor(v, m, kWave));
-    return v;
+// Wavefront max / min, wavefront-uniform result: DPP steps within quads,
+// half-rows and rows, then row 0 into row 1 and row 2 into row 3 (bcast15,
+// rows 1 and 3 written) and rows 0-1 into rows 2-3 (bcast31, rows 2 and 3
+// written), which leaves the result in lane 63.  Lanes a step does not
+// write keep their own value (old = v), the identity of max and min.
+template <bool kMax>
+__device__ __forceinline__ int wave_reduce(int v) {
+    auto op = [](int a, int b) { return kMax ? max(a, b) : min(a, b); };
+    v = op(v, __builtin_amdgcn_update_dpp(v, v, 0xB1, 0xF, 0xF, false));  // quad_perm [1,0,3,2]
+    v = op(v, __builtin_amdgcn_update_dpp(v, v, 0x4E, 0xF, 0xF, false));  // quad_perm [2,3,0,1]
+    v = op(v, __builtin_amdgcn_update_dpp(v, v, 0x141, 0xF, 0xF, false)); // row_half_mirror
+    v = op(v, __builtin_amdgcn_update_dpp(v, v, 0x140, 0xF, 0xF, false)); // row_mirror
+    v = op(v, __builtin_amdgcn_update_dpp(v, v, 0x142, 0xA, 0xF, false)); // row_bcast15
+    v = op(v, __builtin_amdgcn_update_dpp(v, v, 0x143, 0xC, 0xF, false)); // row_bcast31
+    return __builtin_amdgcn_readlane(v, kWave - 1);
 }
 
-__device__ __forceinline__ int wave_min(int v) {
-#pragma unroll
-    for (int m = 1; m < kWave; m <<= 1) v = min(v, __shfl_xor(v, m, kWave));
-    return v;
-}
+__device__ __forceinline__ int wave_max(int v) { return wave_reduce<true>(v); }
+__device__ __forceinline__ int wave_min(int v) { return wave_reduce<false>(v); }
 
 // progress_goals, costtracer.cu:5-23: reward 0.1 when the distance to the goal
 // fell below the best so far, the goal hit flag, and on a hit the next goal of
@@ -80,66 +91,111 @@ __global__ __launch_bounds__(256) void reward_goals_kernel(jl_sim_t s, const uin
     if (bn != b0) best[i] = bn;
 }
 
-// observe, costtracer.cu:25-64 (one 128-thread block per agent there).
+// The observations of kObsPer consecutive agents i0.. (nvalid of them real)
+// into o[k * 242 ..] (LDS), by one wavefront: every load of the group is in
+// flight at once (their positions in one round trip, then the windows and
+// the occupancy words of all of them in a second), and the per-agent
+// reductions interleave.
 template <int H>
-__global__ __launch_bounds__(kWave * kObsWaves) void observe_kernel(jl_sim_t s, jl_mapfgpt_t b,
-                                                                    int32_t* __restrict__ best,
-                                                                    float* __restrict__ out, int n) {
-    const int lane = threadIdx.x & (kWave - 1);
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
-    const int i = blockIdx.x * kObsWaves + wave;
-    if (i >= n) return;  // whole wavefront
+__device__ __forceinline__ void observe_agents(const jl_sim_t& s, const jl_mapfgpt_t& b,
+                                               int32_t* __restrict__ best, float* o, int i0,
+                                               int nvalid, int lane) {
     const int W = s.map_w, A = s.n_agents;
-    const int env = i / A;
-    const int cx = s.cur_x[i], cy = s.cur_y[i];
-    const uint16_t* f = b.cost_tiles + (size_t)i * tiled_field_cells(W, H);
-    const uint32_t* ocp = s.grid_ocp + (size_t)env * (W * H / 32);
+    const size_t tcells = tiled_field_cells(W, H);
+    const int words = W * H / 32;
+    // lane k < nvalid fetches agent i0 + k's position, best and refresh flag
+    const int il = i0 + (lane < nvalid ? lane : 0);
+    const int pxl = s.cur_x[il], pyl = s.cur_y[il];
+    const int32_t bestl = best[il];
+    const int resetl = b.state_packed[(size_t)il * 8 + 7];
     // window cells t0 = lane, t1 = lane + 64 (a cell when < 121); t = r*11 + c
     // is (cx + r - 5, cy + c - 5)
     const int t0 = lane, t1 = lane + kWave;
     const bool has1 = t1 < kObsCells;
-    const int x0 = cx + t0 / kDiam - kRadius, y0 = cy + t0 % kDiam - kRadius;
-    const int x1 = cx + t1 / kDiam - kRadius, y1 = cy + t1 % kDiam - kRadius;
-    const bool in0 = x0 >= 0 && x0 < W && y0 >= 0 && y0 < H;
-    const bool in1 = has1 && x1 >= 0 && x1 < W && y1 >= 0 && y1 < H;
-    // reads at clamped cells, unconditionally (one round trip)
-    const int xa = in0 ? x0 : 0, ya = in0 ? y0 : 0, xb = in1 ? x1 : 0, yb = in1 ? y1 : 0;
-    const uint32_t raw0 = f[tile_at<H>(xa, ya)];
-    const uint32_t raw1 = f[tile_at<H>(xb, yb)];
-    const uint32_t w0 = ocp[(uint32_t)(xa * H + ya) >> 5];
-    const uint32_t w1 = ocp[(uint32_t)(xb * H + yb) >> 5];
-    const int32_t best_in = lane == 0 ? best[i] : 0;
-    const uint32_t reset = lane == 0 ? b.state_packed[(size_t)i * 8 + 7] : 0;
-    const int d0 = (in0 && raw0 != kUnreachable) ? (int)raw0 : -1;
-    const int d1 = (in1 && raw1 != kUnreachable) ? (int)raw1 : -1;
-    // largest reachable distance in the window (0 if none)
-    const int M = wave_max(max(max(0, d0), has1 ? max(0, d1) : 0));
-    // cells without a distance sit 4 past the largest one
-    int v0 = d0 < 0 ? d0 + 5 + M : d0;
-    int v1 = d1 < 0 ? d1 + 5 + M : d1;
-    const int m = wave_min(has1 ? min(v0, v1) : v0);
-    v0 -= m;
-    v1 -= m;
-    const int V = wave_max(has1 ? max(v0, v1) : v0);
-    // the distance at the agent's cell is the window centre (t = 60, lane 60)
-    const int current = __shfl((int)raw0, kObsCentre, kWave);
-    int bi = __shfl(best_in, 0, kWave);
-    const uint32_t rf = (uint32_t)__shfl((int)reset, 0, kWave);
-    if (bi < 0 || rf != 0) {
-        bi = current;
-        if (lane == 0) best[i] = bi;
+    const int r0 = t0 / kDiam - kRadius, q0 = t0 % kDiam - kRadius;
+    const int r1 = t1 / kDiam - kRadius, q1 = t1 % kDiam - kRadius;
+    int cxk[kObsPer], cyk[kObsPer];
+    bool in0[kObsPer], in1[kObsPer];
+    uint32_t raw0[kObsPer], raw1[kObsPer], w0[kObsPer], w1[kObsPer], c0[kObsPer], c1[kObsPer];
+#pragma unroll
+    for (int k = 0; k < kObsPer; ++k) {
+        const int i = i0 + (k < nvalid ? k : 0);
+        cxk[k] = __builtin_amdgcn_readlane(pxl, k);
+        cyk[k] = __builtin_amdgcn_readlane(pyl, k);
+        const int x0 = cxk[k] + r0, y0 = cyk[k] + q0, x1 = cxk[k] + r1, y1 = cyk[k] + q1;
+        in0[k] = x0 >= 0 && x0 < W && y0 >= 0 && y0 < H;
+        in1[k] = has1 && x1 >= 0 && x1 < W && y1 >= 0 && y1 < H;
+        // reads at clamped cells, unconditionally
+        const int xa = in0[k] ? x0 : 0, ya = in0[k] ? y0 : 0;
+        const int xb = in1[k] ? x1 : 0, yb = in1[k] ? y1 : 0;
+        const uint16_t* f = b.cost_tiles + (size_t)i * tcells;
+        const uint32_t* ocp = s.grid_ocp + (size_t)(i / A) * words;
+        c0[k] = (uint32_t)(xa * H + ya);
+        c1[k] = (uint32_t)(xb * H + yb);
+        raw0[k] = f[tile_at<H>(xa, ya)];
+        raw1[k] = f[tile_at<H>(xb, yb)];
+        w0[k] = ocp[c0[k] >> 5];
+        w1[k] = ocp[c1[k] >> 5];
     }
-    float* o = out + (size_t)i * kObsFloats;
-    const uint32_t c0 = (uint32_t)(xa * H + ya), c1 = (uint32_t)(xb * H + yb);
-    o[t0] = (in0 && ((w0 >> (c0 & 31)) & 1u)) ? 1.0f : 0.0f;
-    const float fv = (float)V;
-    float n0 = V > 0 ? (float)(V - v0) / fv : 0.0f;
-    if (t0 == kObsCentre) n0 = -fminf(1.0f, (float)(current - bi + 1) / 64.0f);
-    o[kObsCells + t0] = n0;
-    if (has1) {
-        o[t1] = (in1 && ((w1 >> (c1 & 31)) & 1u)) ? 1.0f : 0.0f;
-        o[kObsCells + t1] = V > 0 ? (float)(V - v1) / fv : 0.0f;
+#pragma unroll
+    for (int k = 0; k < kObsPer; ++k) {
+        if (k >= nvalid) break;  // wavefront-uniform
+        const int d0 = (in0[k] && raw0[k] != kUnreachable) ? (int)raw0[k] : -1;
+        const int d1 = (in1[k] && raw1[k] != kUnreachable) ? (int)raw1[k] : -1;
+        // largest reachable distance in the window (0 if none)
+        const int M = wave_max(max(max(0, d0), has1 ? max(0, d1) : 0));
+        // cells without a distance sit 4 past the largest one
+        int v0 = d0 < 0 ? d0 + 5 + M : d0;
+        int v1 = d1 < 0 ? d1 + 5 + M : d1;
+        const int m = wave_min(has1 ? min(v0, v1) : v0);
+        v0 -= m;
+        v1 -= m;
+        const int V = wave_max(has1 ? max(v0, v1) : v0);
+        // the distance at the agent's cell is the window centre (t = 60, lane 60)
+        const int current = __builtin_amdgcn_readlane((int)raw0[k], kObsCentre);
+        int bi = __builtin_amdgcn_readlane(bestl, k);
+        if (bi < 0 || __builtin_amdgcn_readlane(resetl, k) != 0) {
+            bi = current;
+            if (lane == 0) best[i0 + k] = bi;
+        }
+        float* ok = o + k * kObsFloats;
+        ok[t0] = (in0[k] && ((w0[k] >> (c0[k] & 31)) & 1u)) ? 1.0f : 0.0f;
+        const float fv = (float)V;
+        float n0 = V > 0 ? (float)(V - v0) / fv : 0.0f;
+        if (t0 == kObsCentre) n0 = -fminf(1.0f, (float)(current - bi + 1) / 64.0f);
+        ok[kObsCells + t0] = n0;
+        if (has1) {
+            ok[t1] = (in1[k] && ((w1[k] >> (c1[k] & 31)) & 1u)) ? 1.0f : 0.0f;
+            ok[kObsCells + t1] = V > 0 ? (float)(V - v1) / fv : 0.0f;
+        }
     }
+}
+
+// observe, costtracer.cu:25-64 (one 128-thread block per agent there).
+template <int H>
+__global__ __launch_bounds__(kWave * kObsWaves) void observe_kernel(jl_sim_t s, jl_mapfgpt_t b,
+                                                                    int32_t* __restrict__ best,
+                                                                    float* __restrict__ out, int n,
+                                                                    int vec_store) {
+    __shared__ __align__(16) float s_out[kObsAgents * kObsFloats];
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    const int first = blockIdx.x * kObsAgents;
+    const int i0 = first + wave * kObsPer;
+    const int nvalid = min(kObsPer, n - i0);
+    if (nvalid > 0) observe_agents<H>(s, b, best, s_out + wave * kObsPer * kObsFloats, i0, nvalid, lane);
+    __syncthreads();
+    // the workgroup's agents are one contiguous run of floats
+    float* o = out + (size_t)first * kObsFloats;
+    const int count = min(kObsAgents, n - first) * kObsFloats;
+    int k0 = 0;
+    if (vec_store) {
+        const float4* src = reinterpret_cast<const float4*>(s_out);
+        float4* dst = reinterpret_cast<float4*>(o);
+        for (int k = threadIdx.x; k < count / 4; k += kWave * kObsWaves) dst[k] = src[k];
+        k0 = count / 4 * 4;
+    }
+    for (int k = k0 + threadIdx.x; k < count; k += kWave * kObsWaves) o[k] = s_out[k];
 }
 
 // reset_selected, costtracer.cu:66-85: envs at the horizon start the next
@@ -228,8 +284,9 @@ extern "C" int jl_costtracer_observe(const jl_sim_t* s, const jl_mapfgpt_t* b, i
     if (!best || !output) return JL_ERR_ARG;
     const int n = s->n_envs * s->n_agents;
     JL_DISPATCH_H(s->map_h, {
-        hipLaunchKernelGGL((observe_kernel<H>), dim3((n + kObsWaves - 1) / kObsWaves),
-                           dim3(kWave * kObsWaves), 0, (hipStream_t)stream, *s, *b, best, output, n);
+        hipLaunchKernelGGL((observe_kernel<H>), dim3((n + kObsAgents - 1) / kObsAgents),
+                           dim3(kWave * kObsWaves), 0, (hipStream_t)stream, *s, *b, best, output, n,
+                           ((uintptr_t)output & 15) == 0 ? 1 : 0);
     });
     return launch_status();
 }

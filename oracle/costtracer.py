@@ -134,3 +134,81 @@ class OracleCostTracer:
             for x, y in bank_pos[ep, e]:
                 cell = int(x) * self.H + int(y)
                 ocp[cell >> 5] |= np.uint32(1 << (cell & 31))
+
+
+def observe_vectorized(positions, fields, best, reset_flags, occupied):
+    """The same observation for one env at numpy speed (the form of the
+    reference's CPU environment, encode_numpy, environments.py:30-47):
+    positions [A, 2], fields uint16 [A, W, H], best int [A] (updated in place
+    as observe does), reset_flags [A], occupied bool [W, H].  Used by the CPU
+    baseline; checked against OracleCostTracer.observe in the tests."""
+    n = len(positions)
+    w, h = fields.shape[1:]
+    rr = positions[:, 0, None, None] + np.arange(-5, 6)[None, :, None]
+    cc = positions[:, 1, None, None] + np.arange(-5, 6)[None, None, :]
+    valid = (rr >= 0) & (rr < w) & (cc >= 0) & (cc < h)
+    raw = fields[np.arange(n)[:, None, None], rr.clip(0, w - 1), cc.clip(0, h - 1)].astype(np.int64)
+    d = np.where(valid & (raw != UNREACHABLE), raw, -1)
+    mx = np.maximum(0, d.max((1, 2)))
+    v = np.where(d < 0, d + 5 + mx[:, None, None], d)
+    v -= v.min((1, 2))[:, None, None]
+    V = v.max((1, 2))
+    current = fields[np.arange(n), positions[:, 0], positions[:, 1]].astype(np.int64)
+    upd = (best < 0) | (reset_flags != 0)
+    best[upd] = current[upd]
+    norm = np.where(V[:, None, None] > 0,
+                    (V[:, None, None] - v).astype(np.float32) / np.maximum(V, 1)[:, None, None].astype(np.float32),
+                    np.float32(0.0)).astype(np.float32)
+    norm[:, 5, 5] = -np.minimum(np.float32(1.0), (current - best + 1).astype(np.float32) / np.float32(64.0))
+    local = np.where(valid, occupied[rr.clip(0, w - 1), cc.clip(0, h - 1)], False).astype(np.float32)
+    return np.stack((local, norm), axis=1)
+
+
+def run_costtracer_worker(job) -> tuple[float, int]:
+    """CPU baseline: one process runs the CostTracer environment loop on its
+    envs (the reference's CpuEnvironment, environments.py:50-118, with the C
+    step oracle in place of POGEMA's move and the C BFS in place of scipy's
+    shortest_path).  Returns (seconds of the timed steps, agent-steps)."""
+    import time
+
+    grids, starts, goals, streams, actions, steps = job
+    E, A = starts.shape[:2]
+    sim = _o.OracleSim(grids, A, task_mode=2, max_episode_steps=1 << 30)
+    sim.load_state(starts, goals)
+    W, H = grids.shape[1:]
+    fields = np.zeros((E, A, W, H), np.uint16)
+    cache = np.full((E, A, 2), -1, np.int64)
+    best = np.full((E, A), -1, np.int64)
+    cursor = np.zeros((E, A), np.int64)
+
+    def refresh_and_observe():
+        g = np.stack([sim.goal_x, sim.goal_y], -1).astype(np.int64)
+        pos = sim.positions().astype(np.int64)
+        for e in range(E):
+            changed = np.flatnonzero(np.any(g[e] != cache[e], axis=1))
+            for a in changed:
+                fields[e, a] = _o.bfs_u16(grids[e], g[e, a])[0]
+            cache[e] = g[e]
+            flags = np.zeros(A, np.uint8)
+            flags[changed] = 1
+            occ = np.zeros((W, H), bool)
+            occ[pos[e, :, 0], pos[e, :, 1]] = True
+            observe_vectorized(pos[e], fields[e], best[e], flags, occ)
+
+    refresh_and_observe()
+    t0 = time.perf_counter()
+    for s in range(steps):
+        sim.step(actions[s])
+        pos = sim.positions().astype(np.int64)
+        g = np.stack([sim.goal_x, sim.goal_y], -1).astype(np.int64)
+        for e in range(E):
+            d = fields[e, np.arange(A), pos[e, :, 0], pos[e, :, 1]].astype(np.int64)
+            best[e] = np.minimum(best[e], d)
+            hit = np.flatnonzero(np.all(pos[e] == g[e], axis=1))
+            for a in hit:
+                k = int(cursor[e, a])
+                cursor[e, a] = k + 1
+                sim.goal_x[e, a], sim.goal_y[e, a] = (int(v) for v in streams[e, a, k % streams.shape[2]])
+                best[e, a] = -1
+        refresh_and_observe()
+    return time.perf_counter() - t0, E * A * steps

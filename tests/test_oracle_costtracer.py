@@ -77,6 +77,7 @@ def test_observation_matches_encode_numpy_on_seeded_maps(oracle):
     streams = np.stack([np.roll(goals, k + 1, axis=1) for k in range(70)], axis=2).astype(np.int16)
     for t in range(12):
         ct.refresh_distances()
+        best_before = ct.best.copy()
         obs = ct.observe()
         pos = ct.sim.positions().astype(np.int64)
         for e in range(E):
@@ -84,6 +85,14 @@ def test_observation_matches_encode_numpy_on_seeded_maps(oracle):
             dist[dist == 0xFFFF] = -1
             want = encode_numpy_restated(pos[e], dist, ct.best[e])
             assert np.array_equal(obs[e], want), (t, e)
+            # the CPU baseline's vectorised form gives the same floats and best
+            from oracle.costtracer import observe_vectorized
+
+            occ = np.zeros((W, W), bool)
+            occ[pos[e, :, 0], pos[e, :, 1]] = True
+            b = best_before[e].copy()
+            assert np.array_equal(observe_vectorized(pos[e], ct.fields[e], b, ct.reset_flags[e], occ), obs[e])
+            assert np.array_equal(b, ct.best[e])
         ct.step(rng.integers(0, 5, size=(E, A)).astype(np.uint8), streams)
 
 
