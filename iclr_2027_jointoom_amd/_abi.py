@@ -124,6 +124,22 @@ class RecordsDesc(ctypes.Structure):
     ]
 
 
+class StageUploadDesc(ctypes.Structure):
+    """``jl_stage_upload_t``: one compact stage for the DMA thread's native step."""
+
+    _fields_ = [
+        ("host_slot", c_void_p),
+        ("staging", c_void_p),
+        ("device_slot", c_void_p),
+        ("slot_bytes", c_int64),
+        ("staging_free", c_void_p),
+        ("rows_free", c_void_p),
+        ("done", c_void_p),
+        ("bytes_uploaded", c_int64),
+        ("records", RecordsDesc),
+    ]
+
+
 # name -> (restype, argtypes); the exact set of symbols include/jointloom.h declares
 SIGNATURES = {
     "jl_encode_map": (c_int32, [c_void_p, c_void_p, c_int32, c_int32, c_int32, c_void_p]),
@@ -176,6 +192,7 @@ SIGNATURES = {
          c_void_p],
     ),
     "jl_expand_records": (c_int32, [ctypes.POINTER(RecordsDesc), c_void_p]),
+    "jl_ring_upload_compact": (c_int32, [ctypes.POINTER(StageUploadDesc), c_void_p]),
     "jl_decode_to_uint8": (c_int32, [c_void_p, c_void_p, c_int64, c_int32, c_void_p]),
     "jl_error_string": (ctypes.c_char_p, [c_int32]),
     "jl_version": (ctypes.c_char_p, []),

@@ -149,10 +149,15 @@ __device__ int wave_bfs(const uint64_t (&fr)[R][RowWords<H>::HW], int gx, int gy
                 front[r][k] = nf[r][k];
                 uint64_t m = nf[r][k];
                 if (kCountOverflow) local += __popcll(m);
+                // two new cells per pass, the lowest and the highest (the same
+                // cell twice when one is left)
+                T* row_dist = dist + x * H + k * 64;
                 while (m) {
-                    const int b = __ffsll((unsigned long long)m) - 1;
-                    dist[x * H + k * 64 + b] = (T)level;
-                    m &= m - 1;
+                    const int lo = __ffsll((unsigned long long)m) - 1;
+                    const int hi = 63 - __clzll((long long)m);
+                    row_dist[lo] = (T)level;
+                    row_dist[hi] = (T)level;
+                    m &= ~((1ull << lo) | (1ull << hi));
                 }
             }
         }

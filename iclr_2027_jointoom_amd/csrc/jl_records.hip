@@ -16,6 +16,8 @@
 // on the device, keeping the running goals and histories in HBM between
 // stages: one thread per agent, rows assembled in LDS and written out as one
 // contiguous, 16-byte-vectorised range per workgroup.
+#include <cstring>
+
 #include "jl_common.h"
 
 namespace jl {
@@ -89,7 +91,7 @@ __global__ __launch_bounds__(kRecThreads) void expand_records_kernel(
 }  // namespace
 }  // namespace jl
 
-extern "C" int jl_expand_records(const jl_records_t* r, jl_stream_t stream) {
+static int check_records(const jl_records_t* r) {
     using namespace jl;
     if (!r || r->n_envs <= 0 || r->n_agents <= 0) return JL_ERR_ARG;
     if (r->features != 8 && r->features != 13) return JL_ERR_ARG;
@@ -104,10 +106,14 @@ extern "C" int jl_expand_records(const jl_records_t* r, jl_stream_t stream) {
     if (((uintptr_t)r->positions & 3) || ((uintptr_t)r->new_goals & 3) ||
         ((uintptr_t)r->goals & 3) || ((uintptr_t)r->history & 7) || ((uintptr_t)r->rows & 1))
         return JL_ERR_ARG;
-    const int n = (int)n64;
+    return JL_OK;
+}
+
+static int launch_expand(const jl_records_t* r, hipStream_t s) {
+    using namespace jl;
+    const int n = r->n_envs * r->n_agents;
     const int grid = (n + kRecThreads - 1) / kRecThreads;
     const int vec = ((uintptr_t)r->rows & 15) == 0 ? 1 : 0;
-    hipStream_t s = (hipStream_t)stream;
     const uint32_t* pos = reinterpret_cast<const uint32_t*>(r->positions);
     const uint32_t* ng = reinterpret_cast<const uint32_t*>(r->new_goals);
     uint32_t* g = reinterpret_cast<uint32_t*>(r->goals);
@@ -121,4 +127,73 @@ extern "C" int jl_expand_records(const jl_records_t* r, jl_stream_t stream) {
                            r->actions, r->episode_start, ng, g, h, rows, n, r->n_agents, vec);
     }
     return launch_status();
+}
+
+extern "C" int jl_expand_records(const jl_records_t* r, jl_stream_t stream) {
+    const int rc = check_records(r);
+    if (rc) return rc;
+    return launch_expand(r, (hipStream_t)stream);
+}
+
+// Byte layout of a compact stage slot (N agents, E envs): positions [0, 4N),
+// actions [4N, 5N), episode-start flags [5N, 5N + E), goals from the next
+// 16-byte boundary, 4N bytes.
+static int64_t slot_goals_offset(int64_t n, int64_t e) { return (5 * n + e + 15) / 16 * 16; }
+
+extern "C" int jl_ring_upload_compact(jl_stage_upload_t* u, jl_stream_t stream) {
+    using namespace jl;
+    if (!u || !u->host_slot || !u->staging || !u->device_slot || !u->staging_free) return JL_ERR_ARG;
+    jl_records_t r = u->records;
+    r.positions = nullptr;  // set below from the device slot
+    const int64_t n = (int64_t)r.n_envs * r.n_agents, e = r.n_envs;
+    if (r.n_envs <= 0 || r.n_agents <= 0) return JL_ERR_ARG;
+    const int64_t head = 5 * n + e, goff = slot_goals_offset(n, e);
+    if (u->slot_bytes < goff + 4 * n) return JL_ERR_ARG;
+    hipStream_t s = (hipStream_t)stream;
+    // the staging buffer's previous upload must have left it
+    int rc = status(hipEventSynchronize((hipEvent_t)u->staging_free));
+    if (rc) return rc;
+    std::memcpy(u->staging, u->host_slot, (size_t)head);
+    // goals of the envs that start an episode: one range from the first to the last
+    const uint8_t* starts = u->host_slot + 5 * n;
+    int64_t lo = -1, hi = -1;
+    for (int64_t k = 0; k < e; ++k) {
+        if (starts[k]) {
+            if (lo < 0) lo = k;
+            hi = k + 1;
+        }
+    }
+    int64_t g0 = 0, g1 = 0;
+    if (lo >= 0) {
+        g0 = goff + lo * 4 * r.n_agents;
+        g1 = goff + hi * 4 * r.n_agents;
+        std::memcpy(u->staging + g0, u->host_slot + g0, (size_t)(g1 - g0));
+    }
+    rc = status(hipMemcpyAsync(u->device_slot, u->staging, (size_t)head, hipMemcpyHostToDevice, s));
+    if (rc) return rc;
+    if (g1 > g0) {
+        rc = status(hipMemcpyAsync(u->device_slot + g0, u->staging + g0, (size_t)(g1 - g0),
+                                   hipMemcpyHostToDevice, s));
+        if (rc) return rc;
+    }
+    rc = status(hipEventRecord((hipEvent_t)u->staging_free, s));
+    if (rc) return rc;
+    if (u->rows_free) {
+        rc = status(hipStreamWaitEvent(s, (hipEvent_t)u->rows_free, 0));
+        if (rc) return rc;
+    }
+    r.positions = reinterpret_cast<const uint16_t*>(u->device_slot);
+    r.actions = u->device_slot + 4 * n;
+    r.episode_start = u->device_slot + 5 * n;
+    r.new_goals = reinterpret_cast<const uint16_t*>(u->device_slot + goff);
+    rc = check_records(&r);
+    if (rc) return rc;
+    rc = launch_expand(&r, s);
+    if (rc) return rc;
+    if (u->done) {
+        rc = status(hipEventRecord((hipEvent_t)u->done, s));
+        if (rc) return rc;
+    }
+    u->bytes_uploaded = head + (g1 - g0);
+    return JL_OK;
 }

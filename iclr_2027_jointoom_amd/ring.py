@@ -40,6 +40,7 @@ Device side (this module's own design):
 """
 from __future__ import annotations
 
+import ctypes
 import hashlib
 import json
 import multiprocessing as mp
@@ -55,6 +56,10 @@ MAPFGPT_FEATURE_DIM = 13
 NUM_ACTIONS = 5
 RESET_FLAG_COL = 7
 _POLL_S = 0.0005
+# the DMA thread's poll when the next stage is not complete yet: a stage of a
+# large ring takes a few hundred microseconds end to end, so a 0.5 ms sleep
+# would leave the device idle
+_DMA_POLL_S = 0.00005
 
 
 # ============================================================
@@ -370,7 +375,7 @@ class DMAWorker:
     def _loop(self):
         while self._running:
             if self.run_once() is None:
-                time.sleep(_POLL_S)
+                time.sleep(_DMA_POLL_S)
 
 
 # ============================================================
@@ -487,14 +492,17 @@ class CompactDMAWorker(DMAWorker):
     """Moves ready compact stages to the device and expands them there into
     ``gpu_buffer`` rows (the same rows a row ring would deliver).
 
-    Per stage: the slot's head (positions, actions, start flags: 5N + E bytes)
-    and the goal range of the envs that start an episode are copied
-    shm -> pinned slot on the host, then host -> HBM on ``copy_stream``, where
-    ``jl_expand_records`` writes the stage's rows into ``gpu_buffer`` and
-    advances the running goals and histories; ``dma_event`` follows."""
+    Per stage one native call (``jl_ring_upload_compact``, run without the
+    interpreter lock) copies the slot's head (positions, actions, start
+    flags: 5N + E bytes) and the goal range of the envs that start an
+    episode from the shared host ring into a pinned staging buffer, uploads
+    them on ``copy_stream``, waits on the device for the consumer's copy out
+    of the ring slot's rows, expands the stage into ``gpu_buffer`` (advancing
+    the running goals and histories) and records ``dma_event``."""
 
     def __init__(self, ring_buffer: CompactRingBuffer, gpu_buffer: torch.Tensor, batch_threshold=4096,
                  device="cuda:0", *, staging_slots: int = 2):
+        from ._abi import StageUploadDesc, load_library
         from .records import RecordExpander
 
         if not isinstance(ring_buffer, CompactRingBuffer):
@@ -503,79 +511,69 @@ class CompactDMAWorker(DMAWorker):
         self.gpu_buffer = gpu_buffer
         self.batch_threshold = batch_threshold
         self.device = torch.device(device)
+        self._lib = load_library()
         self.copy_stream = torch.cuda.Stream(device=self.device)
-        self.dma_event = torch.cuda.Event(enable_timing=False)
-        self.dma_read_ptr = 0
-        self._running = False
         k = max(1, int(staging_slots))
         L = ring_buffer.slot_bytes
         self.staging = [torch.empty(L, dtype=torch.uint8).pin_memory() for _ in range(k)]
         self.device_slots = torch.empty((k, L), dtype=torch.uint8, device=self.device)
-        self.staging_events = [None] * k
+        self.dma_read_ptr = 0
+        self._running = False
         self._slot = 0
         self.expander = RecordExpander(ring_buffer.num_envs, ring_buffer.agents_per_env,
                                        ring_buffer.feature_dim, self.device)
+        # events the native step records and waits on: created here (a first
+        # record), re-recorded by the library
+        self.dma_event = torch.cuda.Event(enable_timing=False)
+        self.staging_events = [torch.cuda.Event(enable_timing=False) for _ in range(k)]
+        # per ring slot: recorded after the consumer's copy out of the slot's rows
+        self._consumed = [torch.cuda.Event(enable_timing=False) for _ in range(ring_buffer.num_stage_slots)]
+        self._consumed_used = [False] * ring_buffer.num_stage_slots
+        for ev in [self.dma_event, *self.staging_events, *self._consumed]:
+            ev.record(self.copy_stream)
         self.bytes_uploaded = 0
-        self.host_seconds = 0.0  # host time moving stages (staging copy + enqueue), waits excluded
-        # per ring slot: an event after the consumer's copy out of the slot's rows
-        self._consumed = [None] * ring_buffer.num_stage_slots
-        # set to a list to collect (bytes, upload events, expansion end event) per stage
+        self.host_seconds = 0.0  # host time of the native step (staging copy + enqueue), waits included
+        # set to a list to collect (bytes, start event, end event) of upload + expansion per stage
         self.timing = None
+        u = StageUploadDesc()
+        u.slot_bytes = L
+        u.records = self.expander._desc  # sizes, running goals and histories (a copy of the struct)
+        u.done = self.dma_event.cuda_event
+        self._upload = u
+        self._host_ptrs = [ring_buffer.cpu_buffer[j].data_ptr() for j in range(ring_buffer.num_stage_slots)]
+        self._rows_ptrs = [gpu_buffer[ring_buffer._stage_row_bounds(j)[0]].data_ptr()
+                           for j in range(ring_buffer.num_stage_slots)]
 
     def mark_slot_consumed(self, stage_seq: int, stream) -> None:
         """Record on the consumer's stream that the stage's rows have been
         copied out of ``gpu_buffer``: the slot's next expansion waits for it."""
-        ev = torch.cuda.Event(enable_timing=False)
-        ev.record(stream)
-        self._consumed[int(stage_seq) % len(self._consumed)] = ev
+        j = int(stage_seq) % len(self._consumed)
+        self._consumed[j].record(stream)
+        self._consumed_used[j] = True
 
     def _copy_stage(self, stage_seq: int) -> tuple[int, int]:
+        from ._abi import check
+
+        t_host = time.perf_counter()
         ring = self.ring_buffer
         slot = self._slot
         self._slot = (slot + 1) % len(self.staging)
-        pending = self.staging_events[slot]
-        if pending is not None:
-            pending.synchronize()  # the slot's previous upload has left host memory
-        t_host = time.perf_counter()
-        src_t = ring.cpu_buffer[int(stage_seq) % ring.num_stage_slots]
-        src = src_t.numpy()
-        staged = self.staging[slot]
-        head = ring.head_bytes
-        # torch's host copy runs without the interpreter lock (and in parallel
-        # for large spans), so the consumer thread keeps running meanwhile
-        staged[:head].copy_(src_t[:head])
-        starting = np.flatnonzero(src[ring.off_starts:ring.off_starts + ring.num_envs])
-        g0 = g1 = 0
-        if starting.size:
-            A4 = 4 * ring.agents_per_env
-            g0 = ring.off_goals + int(starting[0]) * A4
-            g1 = ring.off_goals + (int(starting[-1]) + 1) * A4
-            staged[g0:g1].copy_(src_t[g0:g1])
-        row_start, row_end = ring._stage_row_bounds(stage_seq)
-        dev = self.device_slots[slot]
-        base = dev.data_ptr()
-        timed = self.timing is not None
-        consumed = self._consumed[int(stage_seq) % len(self._consumed)]
-        with torch.cuda.stream(self.copy_stream):
-            if consumed is not None:
-                self.copy_stream.wait_event(consumed)
-            t0 = self._timing_event(self.copy_stream) if timed else None
-            dev[:head].copy_(staged[:head], non_blocking=True)
-            if g1 > g0:
-                dev[g0:g1].copy_(staged[g0:g1], non_blocking=True)
-            t1 = self._timing_event(self.copy_stream) if timed else None
-            rows = self.gpu_buffer[row_start:row_end]
-            self.expander.expand_ptrs(base, base + ring.off_actions, base + ring.off_starts,
-                                      base + ring.off_goals, rows.data_ptr(), self.copy_stream.cuda_stream)
-            if timed:
-                self.timing.append((head + (g1 - g0), t0, t1, self._timing_event(self.copy_stream)))
-            done = torch.cuda.Event(enable_timing=False)
-            done.record(self.copy_stream)
-            self.dma_event.record(self.copy_stream)
-        self.staging_events[slot] = done
-        self.bytes_uploaded += head + (g1 - g0)
+        j = int(stage_seq) % ring.num_stage_slots
+        u = self._upload
+        u.host_slot = self._host_ptrs[j]
+        u.staging = self.staging[slot].data_ptr()
+        u.device_slot = self.device_slots[slot].data_ptr()
+        u.staging_free = self.staging_events[slot].cuda_event
+        u.rows_free = self._consumed[j].cuda_event if self._consumed_used[j] else None
+        u.records.rows = self._rows_ptrs[j]
+        t0 = self._timing_event(self.copy_stream) if self.timing is not None else None
+        check(self._lib.jl_ring_upload_compact(ctypes.byref(u), self.copy_stream.cuda_stream),
+              "compact stage upload")
+        if t0 is not None:
+            self.timing.append((u.bytes_uploaded, t0, self._timing_event(self.copy_stream)))
+        self.bytes_uploaded += u.bytes_uploaded
         self.host_seconds += time.perf_counter() - t_host
-        return row_start, row_end
+        return ring._stage_row_bounds(stage_seq)
 
     def run_once(self):
         ring = self.ring_buffer

@@ -347,6 +347,35 @@ typedef struct jl_records {
  * 83-156; the rows equal the stages.npy rows save_records writes, :23-42). */
 int jl_expand_records(const jl_records_t* r, jl_stream_t stream);
 
+/* One step of the compact ring's DMA thread, on the host and `stream`
+ * (CompactDMAWorker in the package): waits on the host for `staging_free`
+ * (the staging buffer's previous upload), copies the stage's head (positions,
+ * actions, start flags: 5N + E bytes) and the goal range of the envs that
+ * start an episode from `host_slot` into the pinned `staging` buffer, uploads
+ * them into `device_slot`, re-records `staging_free`, makes the stream wait
+ * for `rows_free` (the consumer's copy out of the rows), expands the stage
+ * into `records.rows` and records `done`.  Slot layout: positions [0, 4N),
+ * actions [4N, 5N), start flags [5N, 5N + E), goals at the next multiple of
+ * 16, 4N bytes.  `records` carries the sizes, running goals/histories and
+ * rows; its stage pointers are set from `device_slot`.  Unlike the other
+ * entry points it blocks the calling thread on `staging_free` (host memory
+ * reuse) - the device stream is never synchronised.  No reference
+ * counterpart: the reference's DMA thread is Python (expert_running.py:
+ * 463-531) and streams full rows. */
+typedef struct jl_stage_upload {
+    const uint8_t* host_slot;
+    uint8_t* staging;
+    uint8_t* device_slot;
+    int64_t slot_bytes;
+    void* staging_free;   /* hipEvent_t, required */
+    void* rows_free;      /* hipEvent_t or NULL */
+    void* done;           /* hipEvent_t or NULL */
+    int64_t bytes_uploaded;  /* out: bytes copied to the device */
+    jl_records_t records;
+} jl_stage_upload_t;
+
+int jl_ring_upload_compact(jl_stage_upload_t* upload, jl_stream_t stream);
+
 /* ------------------------------------------------------------------------ */
 /* Misc                                                                      */
 /* ------------------------------------------------------------------------ */

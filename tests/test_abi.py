@@ -72,13 +72,20 @@ def test_host_side_argument_checks_return_before_device_work(lib):
     assert lib.jl_expand_records(ctypes.byref(r), None) == -1
     r.features, r.positions = 8, 18  # positions are read as 32-bit words
     assert lib.jl_expand_records(ctypes.byref(r), None) == -1
+    from iclr_2027_jointoom_amd._abi import StageUploadDesc
+
+    u = StageUploadDesc(host_slot=16, staging=16, device_slot=16, slot_bytes=8)
+    assert lib.jl_ring_upload_compact(ctypes.byref(u), None) == -1  # no staging event
+    u.staging_free = 16
+    u.records = RecordsDesc(n_envs=2, n_agents=4, features=13)
+    assert lib.jl_ring_upload_compact(ctypes.byref(u), None) == -1  # slot smaller than its layout
 
 
 def test_ctypes_structs_match_the_c_layout(tmp_path):
-    from iclr_2027_jointoom_amd._abi import MagatDesc, MapfGPTDesc, RecordsDesc, SimDesc
+    from iclr_2027_jointoom_amd._abi import MagatDesc, MapfGPTDesc, RecordsDesc, SimDesc, StageUploadDesc
 
     structs = {"jl_sim_t": SimDesc, "jl_mapfgpt_t": MapfGPTDesc, "jl_magat_t": MagatDesc,
-               "jl_records_t": RecordsDesc}
+               "jl_records_t": RecordsDesc, "jl_stage_upload_t": StageUploadDesc}
     lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{HEADER}"', "int main(void) {"]
     for cname, py in structs.items():
         lines.append(f'printf("{cname} size %zu\\n", sizeof({cname}));')
