@@ -160,6 +160,24 @@ def copy_calibration() -> None:
     print(f"copied 3 x {n} bytes", flush=True)
 
 
+def TokenMLP():
+    """Random-init token policy in bf16: the 256 token values of a context ->
+    Linear(256, 64) -> ReLU -> Linear(64, 5).  (An embedding-bag front end
+    took 9.5 ms per C5 step in torch, 50x the rest of the step.)"""
+    import torch
+
+    class _TokenMLP(torch.nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.fc1 = torch.nn.Linear(256, 64)
+            self.fc2 = torch.nn.Linear(64, 5)
+
+        def forward(self, tokens):
+            return self.fc2(torch.relu(self.fc1(tokens.to(torch.bfloat16))))
+
+    return _TokenMLP()
+
+
 def run_gpu(args) -> dict:
     import torch
 
@@ -200,9 +218,20 @@ def run_gpu(args) -> dict:
     actions = torch.randint(0, 5, (total_steps, E, A), dtype=torch.uint8, device=dev, generator=gen)
     hip = HipEvents()
 
+    policy = None
+    if args.policy == "mlp":
+        # token contexts feed a random-init small MLP
+        # in PyTorch (bf16, 256 -> 64 -> 5 logits), whose argmax is the next action
+        torch.manual_seed(args.seed)
+        policy = TokenMLP().to(device=dev, dtype=torch.bfloat16).eval()
+
     def eager_step(s):
         builder.build_tokens_from_state(sim.cur_x, sim.cur_y, sim.goal_x, sim.goal_y)
-        a = actions[s]
+        if policy is None:
+            a = actions[s]
+        else:
+            with torch.inference_mode():
+                a = policy(builder.tokens).argmax(-1).to(torch.uint8).view(E, A)
         builder.append_actions(a)
         sim.update_actions(a)
         sim.step_sim_only()
@@ -214,6 +243,8 @@ def run_gpu(args) -> dict:
     for s in range(args.warmup):
         one_step(s)
     torch.cuda.synchronize()
+    if args.graph and policy is not None:
+        raise SystemExit("--graph replays the loop with actions written into the graph's buffer: use --policy random")
     if args.graph:
         from iclr_2027_jointoom_amd.graphs import MapfGPTResidentGraph
 
@@ -602,14 +633,21 @@ def time_expansion(rec, E: int, A: int, dev, reps: int = 50) -> float:
     goals = torch.from_numpy(np.ascontiguousarray(rec.goals).reshape(N, 2).view(np.int16)).to(dev)
     rows = torch.empty((N, 13), dtype=torch.int16, device=dev)
     exp.expand(pos, act, first, goals, rows)
-    # one event pair around back-to-back launches through the raw entry point:
-    # a pair per launch of a few-microsecond kernel measures mostly the events
-    stream = torch.cuda.current_stream(dev).cuda_stream
+    # the launches are captured into a HIP graph and replayed between one
+    # event pair: separate launches from the host leave gaps longer than this
+    # few-microsecond kernel
     ptrs = (pos.data_ptr(), act.data_ptr(), cont.data_ptr(), goals.data_ptr(), rows.data_ptr())
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream(device=dev)
+    side.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.graph(graph, stream=side):
+        for _ in range(reps):
+            exp.expand_ptrs(*ptrs, side.cuda_stream)
+    torch.cuda.current_stream(dev).wait_stream(side)
+    graph.replay()
     a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     a.record()
-    for _ in range(reps):
-        exp.expand_ptrs(*ptrs, stream)
+    graph.replay()
     b.record()
     torch.cuda.synchronize()
     return a.elapsed_time(b) * 1e3 / reps
@@ -878,6 +916,9 @@ def main() -> int:
     p.add_argument("--ring-compact-only", action="store_true",
                    help="skip the row-format comparison run (ring workload)")
     p.add_argument("--ct-horizon", type=int, default=512, help="episode horizon (costtracer workload)")
+    p.add_argument("--policy", choices=("random", "mlp"), default=None,
+                   help="resident/c5: pre-staged uniform random actions (the C2 spec) or a random-init token "
+                        "MLP in PyTorch choosing them (the C5 spec, its default)")
     p.add_argument("--task-mode", choices=("standard_mapf", "lifelong"), default="standard_mapf",
                    help="resident workload: standard MAPF, or lifelong with deterministic candidate goals")
     args = p.parse_args()
@@ -887,6 +928,8 @@ def main() -> int:
                                   ("--steps", "steps", 40), ("--warmup", "warmup", 4)):
             if flag not in sys.argv:
                 setattr(args, name, value)
+    if args.policy is None:
+        args.policy = "mlp" if args.workload == "c5" else "random"
     if args.workload == "c5":
         for flag, name, value in (("--envs", "envs", 256), ("--agents", "agents", 1024),
                                   ("--map", "map", 256), ("--map-kind", "map_kind", "warehouse"),
@@ -948,7 +991,8 @@ def main() -> int:
             "synthetic (seeded "
             + {"iid": "i.i.d. maps p=0.2", "maze": "recursive-backtracker mazes",
                "warehouse": "warehouse maps (2x8 shelves, 2-wide aisles)"}[args.map_kind]
-            + ", largest component; distinct starts/goals; uniform random actions)"
+            + ", largest component; distinct starts/goals; "
+            + ("actions from a random-init token MLP)" if args.policy == "mlp" else "uniform random actions)")
         ),
         "config": {
             "workload": (
@@ -956,6 +1000,8 @@ def main() -> int:
                 else "resident step + MAPF-GPT token build (C2+C3 shape)"
             ),
             "launch": "hip-graph replay" if args.graph else "eager",
+            "policy": "random-init token MLP (PyTorch, bf16 256-64-5)" if args.policy == "mlp"
+                      else "pre-staged random actions",
             "envs": args.envs,
             "agents": args.agents,
             "map": f"{args.map}x{args.map}",

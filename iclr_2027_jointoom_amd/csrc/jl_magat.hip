@@ -87,7 +87,8 @@ __host__ __device__ inline size_t a16n(size_t v) { return (v + 15) & ~(size_t)15
 
 constexpr int kNodeEgos = 64;  // agents per node workgroup: an env spans ceil(A / 64)
 constexpr int kWinCells = kDiam * kDiam;
-constexpr int kWinStride = 128;  // LDS bytes per staged window
+constexpr int kWinRow = 16;                  // LDS bytes per staged window row (11 used)
+constexpr int kWinStride = kDiam * kWinRow;  // LDS bytes per staged window
 constexpr int kWinItems = (kNodeEgos * kDiam + kNodeThreads - 1) / kNodeThreads;  // window rows per thread
 
 __host__ __device__ inline NodeLayout node_layout(int A, int W, int H) {
@@ -193,20 +194,22 @@ __global__ __launch_bounds__(kNodeThreads) void nodes_kernel(jl_magat_t m) {
         if (lane == 0) m.env_edge_base[E + 1 + (size_t)env * parts + part] = count;
     }
 
-    // Energy windows of the slice: item i = (agent i / 11, window row i % 11),
-    // 11 byte loads each at clamped addresses, 0 off the map.  Every thread
-    // has at most kWinItems items (a slice of kNodeEgos agents); an item past
-    // the slice repeats item 0 (same bytes, same LDS addresses), so all loads
-    // are issued before the first wait, and the row phase below reads LDS
-    // only, so its stores are never waited on.
+    // Energy windows of the slice: item i = (agent i / 11, window row i % 11).
+    // The row's 11 bytes lie in two aligned 16-byte words of the field row,
+    // read with two vector loads at clamped addresses (a word off the map or
+    // off the row reads as 0), then shifted into place and stored as one
+    // 16-byte LDS word.  Every thread has at most kWinItems items (a slice of
+    // kNodeEgos agents); an item past the slice repeats item 0 (same bytes,
+    // same LDS address), so all loads are issued before the first wait, and
+    // the row phase below reads LDS only, so its stores are never waited on.
     uint8_t* s_win = smem + L.win_off;
     float* s_tenths = reinterpret_cast<float*>(smem + L.tenths_off);
     if (tid < 21) s_tenths[tid] = kTenths[tid];
     {
         const uint8_t* env_energy = m.energy + base * cells;
         const int nitems = (e_end - e_begin) * kDiam;
-        uint32_t v[kWinItems][kDiam];
-        int dst[kWinItems];
+        uint4 lo[kWinItems], hi[kWinItems];
+        int shift[kWinItems], dst[kWinItems];
 #pragma unroll
         for (int it = 0; it < kWinItems; ++it) {
             const int i = tid + it * kNodeThreads < nitems ? tid + it * kNodeThreads : 0;
@@ -216,20 +219,34 @@ __global__ __launch_bounds__(kNodeThreads) void nodes_kernel(jl_magat_t m) {
             const int x = (int16_t)(pos & 0xFFFF) + r - kRadius;
             const int y0 = (int16_t)(pos >> 16) - kRadius;
             const bool rok = s_valid[a] && x >= 0 && x < W;
-            const uint8_t* src = env_energy + (size_t)a * cells + (size_t)(rok ? x : 0) * H;
-            dst[it] = el * kWinStride + r * kDiam;
-#pragma unroll
-            for (int j = 0; j < kDiam; ++j) {
-                const int y = y0 + j;
-                const bool ok = rok && y >= 0 && y < H;
-                const uint32_t b = src[ok ? y : 0];
-                v[it][j] = ok ? b : 0u;
-            }
+            const int c0 = y0 >> 4;  // word of column y0 (-1 for the columns left of the map)
+            const bool ok0 = rok && c0 >= 0 && c0 < H / 16;
+            const bool ok1 = rok && c0 + 1 >= 0 && c0 + 1 < H / 16;
+            const uint4* row4 =
+                reinterpret_cast<const uint4*>(env_energy + (size_t)a * cells + (size_t)(rok ? x : 0) * H);
+            const uint4 l = row4[ok0 ? c0 : 0], h = row4[ok1 ? c0 + 1 : 0];
+            lo[it] = ok0 ? l : make_uint4(0u, 0u, 0u, 0u);
+            hi[it] = ok1 ? h : make_uint4(0u, 0u, 0u, 0u);
+            shift[it] = y0 - c0 * 16;  // 0..15: byte of column y0 in lo
+            dst[it] = el * kWinStride + r * kWinRow;
         }
 #pragma unroll
-        for (int it = 0; it < kWinItems; ++it)
+        for (int it = 0; it < kWinItems; ++it) {
+            // bytes shift .. shift + 11 of the 32 bytes lo:hi
+            const uint32_t w = (uint32_t)shift[it] >> 2, b = (uint32_t)shift[it] & 3u;
+            const uint32_t d[8] = {lo[it].x, lo[it].y, lo[it].z, lo[it].w,
+                                   hi[it].x, hi[it].y, hi[it].z, hi[it].w};
+            uint32_t sel[4];
 #pragma unroll
-            for (int j = 0; j < kDiam; ++j) s_win[dst[it] + j] = (uint8_t)v[it][j];
+            for (int q = 0; q < 4; ++q)
+                sel[q] = w == 0 ? d[q] : (w == 1 ? d[q + 1] : (w == 2 ? d[q + 2] : d[q + 3]));
+            uint4 v;
+            v.x = __builtin_amdgcn_alignbyte(sel[1], sel[0], b);
+            v.y = __builtin_amdgcn_alignbyte(sel[2], sel[1], b);
+            v.z = __builtin_amdgcn_alignbyte(sel[3], sel[2], b);
+            v.w = 0u;
+            *reinterpret_cast<uint4*>(s_win + dst[it]) = v;
+        }
     }
     __syncthreads();
 
@@ -249,7 +266,7 @@ __global__ __launch_bounds__(kNodeThreads) void nodes_kernel(jl_magat_t m) {
         prow[k] = p / kPygDiam;
         pcol[k] = p - prow[k] * kPygDiam;
         pwin[k] = prow[k] >= 1 && prow[k] <= kDiam && pcol[k] >= 1 && pcol[k] <= kDiam;
-        pwc[k] = pwin[k] ? (prow[k] - 1) * kDiam + (pcol[k] - 1) : 0;
+        pwc[k] = pwin[k] ? (prow[k] - 1) * kWinRow + (pcol[k] - 1) : 0;
     }
     for (int a = e_begin + wave; a < e_end; a += nwaves) {
         if (!s_valid[a]) continue;
@@ -258,7 +275,7 @@ __global__ __launch_bounds__(kNodeThreads) void nodes_kernel(jl_magat_t m) {
         const int cx = (int16_t)(pos & 0xFFFF), cy = (int16_t)(pos >> 16);
         if (lane < 2) m.pyg_pos[(base + a) * 2 + lane] = (float)(lane ? cy : cx);
         // the centre is window cell (5, 5); 0 when the agent is off the map
-        const int center = win[kRadius * kDiam + kRadius];
+        const int center = win[kRadius * kWinRow + kRadius];
         const int goal_p = s_part[kNodeEgos + a - e_begin];
         float* row = m.pyg_x + (base + a) * kPygFeatures;
 #pragma unroll
