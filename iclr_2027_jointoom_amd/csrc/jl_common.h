@@ -35,6 +35,22 @@ constexpr int kCommRadiusSq = 49;
 constexpr int kScratchAccum = 0;     // [0..3]
 constexpr int kScratchTicket = 4;
 
+// The builder's tiled copies of the distance fields (cost_tiles) of maps of
+// at most 4096 cells carry each reachable cell's greedy-move mask in bits
+// 12-15: a distance there is below 4095 (at most the number of free cells
+// minus one, and a map with every cell free has a far smaller diameter), so
+// it fits in bits 0-11 and a marked value never equals kUnreachable, which
+// unreachable cells keep.  Readers take the distance as field_distance(v,
+// field_mask(W, H)).  cost_to_go, the API tensor, holds plain distances.
+constexpr int kMarkedCells = 4096;
+__host__ __device__ inline bool marked_fields(int W, int H) { return W * H <= kMarkedCells; }
+__host__ __device__ inline uint32_t field_mask(int W, int H) {
+    return marked_fields(W, H) ? 0x0FFFu : 0xFFFFu;
+}
+__device__ __forceinline__ uint32_t field_distance(uint32_t v, uint32_t mask) {
+    return v == kUnreachable ? v : (v & mask);
+}
+
 inline bool profile_ok(int w, int h) {
     return (h == 32 || h == 64 || h == 128 || h == 256) && w >= 1 && w <= 256;
 }

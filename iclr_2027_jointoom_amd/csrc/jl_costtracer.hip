@@ -8,9 +8,9 @@
 // bank of episodes when the horizon is reached.
 //
 // Distances are read from the builder's tiled fields (8 x 8 tiles of uint16,
-// one 128-byte line each), which hold exactly what the builder last wrote into
-// cost_to_go: an 11 x 11 window touches 4 to 9 lines instead of 11 to 22
-// row-major ones.  The observation runs four agents per wavefront (two
+// one 128-byte line each), which hold what the builder last wrote into
+// cost_to_go (plus, on small maps, greedy marks that field_distance strips):
+// an 11 x 11 window touches 4 to 9 lines instead of 11 to 22 row-major ones.  The observation runs four agents per wavefront (two
 // window cells per lane and agent, all loads of the four in flight together,
 // the window reductions as DPP steps); the 16 agents of a workgroup assemble
 // their floats in LDS, which leave as one contiguous run of 16-byte stores.
@@ -72,7 +72,8 @@ __global__ __launch_bounds__(256) void reward_goals_kernel(jl_sim_t s, const uin
     const int b0 = best[i];
     const int k = cursor[i];
     const int xc = x < W ? x : W - 1, yc = y < H ? y : H - 1;
-    const int d = tiles[(size_t)i * tiled_field_cells(W, H) + tile_at<H>(xc, yc)];
+    const int d = (int)field_distance(tiles[(size_t)i * tiled_field_cells(W, H) + tile_at<H>(xc, yc)],
+                                      field_mask(W, H));
     rewards[i] = d < b0 ? 0.1f : 0.0f;
     int bn = min(b0, d);
     const bool hit = x == gx && y == gy;
@@ -102,6 +103,7 @@ __device__ __forceinline__ void observe_agents(const jl_sim_t& s, const jl_mapfg
                                                int nvalid, int lane) {
     const int W = s.map_w, A = s.n_agents;
     const size_t tcells = tiled_field_cells(W, H);
+    const uint32_t fmask = field_mask(W, H);
     const int words = W * H / 32;
     // lane k < nvalid fetches agent i0 + k's position, best and refresh flag
     const int il = i0 + (lane < nvalid ? lane : 0);
@@ -132,8 +134,8 @@ __device__ __forceinline__ void observe_agents(const jl_sim_t& s, const jl_mapfg
         const uint32_t* ocp = s.grid_ocp + (size_t)(i / A) * words;
         c0[k] = (uint32_t)(xa * H + ya);
         c1[k] = (uint32_t)(xb * H + yb);
-        raw0[k] = f[tile_at<H>(xa, ya)];
-        raw1[k] = f[tile_at<H>(xb, yb)];
+        raw0[k] = field_distance(f[tile_at<H>(xa, ya)], fmask);
+        raw1[k] = field_distance(f[tile_at<H>(xb, yb)], fmask);
         w0[k] = ocp[c0[k] >> 5];
         w1[k] = ocp[c1[k] >> 5];
     }

@@ -106,6 +106,45 @@ __device__ __forceinline__ uint32_t tile_offset(int x, int y) {
            (uint32_t)((x & 7) * 8 + (y & 7));
 }
 
+// One 8-cell tile row (x, y0 .. y0 + 7) of a field in LDS (row-major, H
+// columns, x < W), every reachable cell marked in bits 12-15 with its
+// greedy-move mask (greedy_mask's rule: a neighbour off the map or
+// unreachable is never closer, since a reachable distance is below
+// kUnreachable).
+template <int H>
+__device__ __forceinline__ uint4 marked_segment(const uint16_t* f, int W, int x, int y0) {
+    const uint4* f4 = reinterpret_cast<const uint4*>(f);
+    constexpr uint32_t kNone = 0xFFFFFFFFu;
+    const uint4 mid = f4[(x * H + y0) >> 3];
+    const uint4 up = x > 0 ? f4[((x - 1) * H + y0) >> 3] : make_uint4(kNone, kNone, kNone, kNone);
+    const uint4 dn = x + 1 < W ? f4[((x + 1) * H + y0) >> 3] : make_uint4(kNone, kNone, kNone, kNone);
+    const uint32_t left = y0 > 0 ? f[x * H + y0 - 1] : kUnreachable;
+    const uint32_t right = y0 + 8 < H ? f[x * H + y0 + 8] : kUnreachable;
+    const uint32_t cw[4] = {mid.x, mid.y, mid.z, mid.w};
+    const uint32_t uw[4] = {up.x, up.y, up.z, up.w};
+    const uint32_t dw[4] = {dn.x, dn.y, dn.z, dn.w};
+    uint32_t c[8], u[8], d[8];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        c[2 * k] = cw[k] & 0xFFFFu;
+        c[2 * k + 1] = cw[k] >> 16;
+        u[2 * k] = uw[k] & 0xFFFFu;
+        u[2 * k + 1] = uw[k] >> 16;
+        d[2 * k] = dw[k] & 0xFFFFu;
+        d[2 * k + 1] = dw[k] >> 16;
+    }
+    uint32_t o[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        const uint32_t v = c[k];
+        const uint32_t l = k > 0 ? c[k - 1] : left;
+        const uint32_t r = k < 7 ? c[k + 1] : right;
+        const uint32_t m = (v > u[k] ? 8u : 0u) | (v > d[k] ? 4u : 0u) | (v > l ? 2u : 0u) | (v > r ? 1u : 0u);
+        o[k] = v == kUnreachable ? v : (v | (m << 12));
+    }
+    return make_uint4(o[0] | (o[1] << 16), o[2] | (o[3] << 16), o[4] | (o[5] << 16), o[6] | (o[7] << 16));
+}
+
 // ---------------------------------------------------------------------------
 // Pass 1a: unpack + goal-cache refresh + agent info, one lane per agent, no
 // LDS.  kRows: raw 13-column rows (mapf_gpt_unpack_kernel,
@@ -274,11 +313,12 @@ __global__ __launch_bounds__(kWave* kWaves) void bfs_kernel(jl_mapfgpt_t b, int 
 }
 
 // ---------------------------------------------------------------------------
-// Pass 1 for small maps (a field of at most kCombinedField bytes): 1a and 1b
+// Pass 1 for maps of at most kMarkedCells cells (8 KB fields): 1a and 1b
 // in one launch, one lane per agent and 4 wavefronts per workgroup, each
-// wavefront refreshing the fields of its own marked agents in its LDS field
-// (the fields are small enough not to limit occupancy, and one launch saves
-// a kernel boundary).
+// wavefront refreshing the fields of its own agents whose goal changed in
+// its LDS field (the fields are small enough not to limit occupancy, and
+// one launch saves a kernel boundary).  The tiled copies it writes carry
+// the greedy marks (jl_common.h, marked_fields).
 // ---------------------------------------------------------------------------
 template <int H, int R, bool kRows, int kWaves>
 __global__ __launch_bounds__(kWave* kWaves) void unpack_bfs_kernel(
@@ -354,14 +394,22 @@ __global__ __launch_bounds__(kWave* kWaves) void unpack_bfs_kernel(
     }
 
     // Fields this launch does not rewrite are read from HBM (written by an
-    // earlier launch), from the tiled copy where the cross of five cells
-    // spans 1-3 lines; refreshed ones are read from LDS below.
+    // earlier launch): the tiled copy of these small maps holds the greedy
+    // mask of every reachable cell, so one read of the agent's own cell
+    // gives it; an agent on an unreachable cell (an obstacle, or a component
+    // without its goal) reads the cross of five cells instead.  Refreshed
+    // fields are read from LDS below.
     const bool on_map = i < N && px < (uint32_t)W && py < (uint32_t)H;
     const size_t tcells = tiled_cells(W, H);
     if (on_map && !reset) {
         const uint16_t* f = b.cost_tiles + (size_t)i * tcells;
-        info |= greedy_mask<H>([f](int x, int y) { return (uint32_t)f[tile_offset<H>(x, y)]; },
-                               (int)px, (int)py, W);
+        const uint32_t c = f[tile_offset<H>((int)px, (int)py)];
+        if (c != kUnreachable) {
+            info |= c >> 12;
+        } else {
+            info |= greedy_mask<H>([f](int x, int y) { return (uint32_t)f[tile_offset<H>(x, y)]; },
+                                   (int)px, (int)py, W);
+        }
     }
 
     constexpr int HW = RowWords<H>::HW;
@@ -411,7 +459,7 @@ __global__ __launch_bounds__(kWave* kWaves) void unpack_bfs_kernel(
             const int t = c >> 3, r = c & 7;  // tile, row inside the tile
             const int x = (t / (H / 8)) * 8 + r, y0 = (t % (H / 8)) * 8;
             const bool in = x < W;  // rows past the map in the last tile row: unreachable
-            uint4 v = lds4[((in ? x : 0) * H + y0) >> 3];
+            uint4 v = marked_segment<H>(s_dist, W, in ? x : 0, y0);
             v.x = in ? v.x : 0xFFFFFFFFu;
             v.y = in ? v.y : 0xFFFFFFFFu;
             v.z = in ? v.z : 0xFFFFFFFFu;
@@ -550,6 +598,7 @@ __global__ __launch_bounds__(kTokThreads) void tokens_kernel(jl_mapfgpt_t b) {
     uint32_t* my_slots = reinterpret_cast<uint32_t*>(my_lds + kWinBytes + kRowBytes);
     const uint32_t hmask = (uint32_t)L.hash_slots - 1;
     const size_t cells = (size_t)W * H;
+    const uint32_t fmask = field_mask(W, H);  // distance bits of a tiled field value
 
     // ---- phase 1 -----------------------------------------------------------
     if (kDense) {
@@ -691,9 +740,9 @@ __global__ __launch_bounds__(kTokThreads) void tokens_kernel(jl_mapfgpt_t b) {
             const int ex = (int)(pos & 0xFFFFu), ey = (int)(pos >> 16);
             // region row = dx + 5, column = ey + dy - 8 * tyl (see seg_load)
             const uint16_t* win = win_base + (ey - 8 * (((ey - kRadius + 64) >> 3) - 8) - kRadius);
-            const uint32_t center = win[kRadius * kRegionCols + kRadius];
-            const uint32_t v0 = win[win0];
-            const uint32_t v1 = win[win1];
+            const uint32_t center = field_distance(win[kRadius * kRegionCols + kRadius], fmask);
+            const uint32_t v0 = field_distance(win[win0], fmask);
+            const uint32_t v1 = field_distance(win[win1], fmask);
             uint32_t id0, id1;
             if (kDense) {
                 const uint32_t* mrow = s_map + (ex + kRadius) * MH + (ey + kRadius);
@@ -907,8 +956,6 @@ int check_builder(const jl_mapfgpt_t* b) {
     return JL_OK;
 }
 
-// Largest field (bytes) for which pass 1 runs as one launch.
-constexpr size_t kCombinedField = 8192;
 
 // Pass 1b wavefronts per workgroup: each owns a W*H uint16 LDS field; up to
 // 64 KB of them per workgroup, at most 4.
@@ -930,7 +977,9 @@ template <int H, int R, bool kRows>
 int launch_pass1(const jl_mapfgpt_t* b, const int16_t* rows, const int16_t* cx, const int16_t* cy,
                  const int16_t* gx, const int16_t* gy, hipStream_t stream) {
     const int N = b->n_envs * b->n_agents;
-    if ((size_t)b->map_w * H * sizeof(uint16_t) <= kCombinedField) {
+    // maps whose tiled fields carry greedy marks (at most 4096 cells, 8 KB
+    // LDS fields) run pass 1 as one launch; only that launch writes marks
+    if (marked_fields(b->map_w, H)) {
         const dim3 grid((N + kWave * 4 - 1) / (kWave * 4));
         const size_t lds = (size_t)4 * b->map_w * H * sizeof(uint16_t);
         hipLaunchKernelGGL((unpack_bfs_kernel<H, R, kRows, 4>), grid, dim3(kWave * 4), lds, stream,

@@ -170,7 +170,9 @@ typedef struct jl_mapfgpt {
     uint32_t* agent_info;       /* [N] workspace: greedy-move mask and diagnostic flags of
                                    each agent, written by the first pass of a build */
     uint16_t* cost_tiles;       /* [E, A, ceil(W/8), H/8, 8, 8] workspace: the same fields as
-                                   cost_to_go in 8x8 tiles (one 128-byte line per tile) */
+                                   cost_to_go in 8x8 tiles (one 128-byte line per tile); on
+                                   maps of at most 4096 cells bits 12-15 of a reachable cell
+                                   hold its greedy-move mask */
     void* token_events[2];      /* optional hipEvent_t pair recorded on the stream right
                                    before / after the token kernel (profiling); NULL = off */
 } jl_mapfgpt_t;

@@ -406,3 +406,47 @@ def test_raw_row_history_values_outside_action_range(oracle):
     torch.cuda.synchronize()
     assert np.array_equal(b.tokens.cpu().numpy(), ob.tokens)
     assert ob.tokens.max() > 66  # the unbounded history tokens are really present
+
+
+@pytest.mark.parametrize("W,H", [(64, 64), (36, 32)])
+def test_kept_fields_greedy_tokens_match_oracle(oracle, W, H):
+    """Maps of at most 4096 cells keep each field's greedy-move masks in its
+    tiled copy: builds that keep the fields (goals unchanged, reset flag 0)
+    read an agent's mask from its own cell, and agents on unreachable cells
+    (obstacles, components without the goal) take the five-cell path."""
+    from iclr_2027_jointoom_amd import profile
+
+    rng = np.random.default_rng(W + H)
+    E, A = 3, 40
+    grids = (rng.random((E, W, H)) < 0.3).astype(np.int32)
+    rows = np.zeros((E * A, 13), np.uint16)
+    rows[:, 0] = np.repeat(np.arange(E), A)
+    rows[:, 1] = np.tile(np.arange(A), E)
+    for e in range(E):
+        free = np.flatnonzero(grids[e].ravel() == 0)
+        g = rng.choice(free, A, replace=False)
+        rows[e * A:(e + 1) * A, 4] = g // H
+        rows[e * A:(e + 1) * A, 5] = g % H
+    rows[:, 8:13] = 5
+    ext = profile(W, H)
+    b = ext.MapfGPTObservationBuilder(torch.from_numpy(grids).cuda(), A)
+    ob = oracle.OracleMapfGPT(grids, A)
+    on_obstacle = 0
+    for it in range(4):
+        rows[:, 7] = 1 if it == 0 else 0
+        for e in range(E):
+            cells = rng.choice(W * H, A, replace=False)  # anywhere, obstacles included
+            rows[e * A:(e + 1) * A, 2] = cells // H
+            rows[e * A:(e + 1) * A, 3] = cells % H
+            on_obstacle += int(grids[e].ravel()[cells].sum())
+        rows[:, 6] = rng.integers(0, 5, E * A)
+        b.build_tokens(torch.from_numpy(rows.astype(np.int16)).cuda())
+        ob.build_rows(rows)
+        torch.cuda.synchronize()
+        assert np.array_equal(b.tokens.cpu().numpy(), ob.tokens), it
+        assert np.array_equal(b.cost_to_go.cpu().numpy(), ob.cost_to_go.view(np.int16)), it
+        assert b.diagnostics.cpu().tolist() == ob.diagnostics.tolist(), it
+    assert on_obstacle > 0
+    # the greedy tokens cover every mask value class seen on such maps
+    greedy = ob.tokens[:, 121 + 9::10][:, :1].ravel()
+    assert len(np.unique(greedy)) > 4
