@@ -62,6 +62,10 @@ MAGAT_TRAFFIC_FILE = ROOT / "profiles" / "magat_nodes_pmc_512x256_64.txt"
 
 # Algorithmic bytes per agent (derivation in DESIGN.md).
 B_TOKEN_KERNEL = 8 + 10 + 242 + 1024 + 1  # pos+goal, history, 11x11 u16 window, tokens, mask
+# The whole build as one launch (maps of at most 4096 cells): split-array
+# position and goal, goal-cache read (written only on a change), history,
+# window, state row and label written, tokens, mask.
+B_BUILD_SINGLE = 8 + 4 + 10 + 242 + 16 + 8 + 1024 + 1
 B_STEP_NORTH_STAR = 1385  # step + token build + append + update_actions per agent-step
 # MAGAT node pass: state row, bitmaps share, 11x11 u8 window, 676-float row, pos, count
 B_MAGAT_NODES = 16 + 4 + 121 + 2704 + 8 + 4
@@ -325,7 +329,9 @@ def run_gpu(args) -> dict:
     ms_per_step = wall * 1000.0 / args.steps
     value = N * args.steps / wall
     tok_avg_s = float(np.mean(tok_ms)) / 1000.0
-    tok_bytes = B_TOKEN_KERNEL * N
+    # with a single-launch build the event pair brackets the whole build
+    single = builder.single_launch
+    tok_bytes = (B_BUILD_SINGLE if single else B_TOKEN_KERNEL) * N
     achieved = tok_bytes / tok_avg_s
     return {
         "value": value,
@@ -333,7 +339,7 @@ def run_gpu(args) -> dict:
         "gpu_ms_per_step": gpu_ms / args.steps,
         "roofline": {
             "bound": "hbm",
-            "kernel": f"tokens_kernel<{W}>",
+            "kernel": f"tokens_kernel<{W}>" + (" (single-launch build)" if single else ""),
             "achieved": achieved / 1e9,
             "peak": PEAK_HBM_BPS / 1e9,
             "unit": "GB/s",

@@ -77,6 +77,7 @@ class MapfGPTDesc(ctypes.Structure):
         ("diagnostics", c_void_p),
         ("agent_info", c_void_p),
         ("cost_tiles", c_void_p),
+        ("build_scratch", c_void_p),
         ("token_events", c_void_p * 2),
     ]
 
@@ -174,6 +175,7 @@ SIGNATURES = {
     "jl_magat_occupancy": (c_int32, [ctypes.POINTER(MagatDesc), c_void_p]),
     "jl_magat_nodes": (c_int32, [ctypes.POINTER(MagatDesc), c_void_p]),
     "jl_magat_edges": (c_int32, [ctypes.POINTER(MagatDesc), c_void_p]),
+    "jl_mapfgpt_single_launch": (c_int32, [ctypes.POINTER(MapfGPTDesc)]),
     "jl_mapfgpt_refresh_state": (
         c_int32,
         [ctypes.POINTER(MapfGPTDesc), c_void_p, c_void_p, c_void_p, c_void_p, c_void_p],

@@ -21,6 +21,8 @@
 // (mapf_gpt_builder.cpp:108-110, mapf_gpt_cuda.cu:544-610) with the
 // top-13 search done serially by one lane per ego (:395-496) and every
 // window row read from the row-major field (one 128-byte line per row).
+#include <atomic>
+
 #include "jl_bfs.h"
 #include "jl_common.h"
 
@@ -58,17 +60,6 @@ __device__ __forceinline__ uint32_t hash_find(const uint32_t* keys, uint32_t mas
         if (k == kEmptyKey) return kEmptyKey;
         h = (h + 1) & mask;
     }
-}
-
-__device__ __forceinline__ void store_state_row(uint16_t* dst, uint32_t env, uint32_t agent,
-                                                uint32_t px, uint32_t py, uint32_t gx,
-                                                uint32_t gy, uint32_t action, uint32_t reset) {
-    uint4 v;
-    v.x = (env & 0xFFFFu) | (agent << 16);
-    v.y = (px & 0xFFFFu) | (py << 16);
-    v.z = (gx & 0xFFFFu) | (gy << 16);
-    v.w = (action & 0xFFFFu) | (reset << 16);
-    *reinterpret_cast<uint4*>(dst) = v;
 }
 
 // Greedy-move mask of one agent (mapf_gpt_cuda.cu:459-480): bit (3 - dir)
@@ -146,14 +137,147 @@ __device__ __forceinline__ uint4 marked_segment(const uint16_t* f, int W, int x,
 }
 
 // ---------------------------------------------------------------------------
-// Pass 1a: unpack + goal-cache refresh + agent info, one lane per agent, no
-// LDS.  kRows: raw 13-column rows (mapf_gpt_unpack_kernel,
-// mapf_gpt_cuda.cu:75-118); otherwise resident split arrays
-// (mapf_gpt_state_unpack_kernel, :121-152).  An agent whose field is kept
+// Per-agent steps shared by the launches of a build.
+// ---------------------------------------------------------------------------
+constexpr uint32_t kInfoNeedsBfs = 1u << 6;  // agent_info: field to refresh in pass 1b
+
+__device__ __forceinline__ uint4 state_row(uint32_t env, uint32_t agent, uint32_t px, uint32_t py,
+                                           uint32_t gx, uint32_t gy, uint32_t action,
+                                           uint32_t reset) {
+    return make_uint4((env & 0xFFFFu) | (agent << 16), (px & 0xFFFFu) | (py << 16),
+                      (gx & 0xFFFFu) | (gy << 16), (action & 0xFFFFu) | (reset << 16));
+}
+
+// One agent's unpack: state row, goal cache, label and (raw rows) history.
+// kRows: raw 13-column rows (mapf_gpt_unpack_kernel, mapf_gpt_cuda.cu:75-118);
+// otherwise resident split arrays (mapf_gpt_state_unpack_kernel, :121-152).
+// Returns the agent's state row as it now stands in state_packed (a
+// rejected raw row keeps the old one, reset flag included, :90-92, :186-189)
+// and sets info to kInfoBadRow for such a row, else 0.
+template <bool kRows>
+__device__ __forceinline__ uint4 unpack_agent(const jl_mapfgpt_t& b, int i,
+                                              const int16_t* __restrict__ raw_rows,
+                                              const int16_t* __restrict__ cur_x,
+                                              const int16_t* __restrict__ cur_y,
+                                              const int16_t* __restrict__ goal_x,
+                                              const int16_t* __restrict__ goal_y, uint32_t& info) {
+    const int A = b.n_agents;
+    uint4* st = reinterpret_cast<uint4*>(b.state_packed + (size_t)i * 8);
+    uint32_t* gc = reinterpret_cast<uint32_t*>(b.goal_cache + (size_t)i * 2);
+    info = 0;
+    if (kRows) {
+        const uint16_t* row = reinterpret_cast<const uint16_t*>(raw_rows) + (size_t)i * 13;
+        uint16_t c[13];
+#pragma unroll
+        for (int k = 0; k < 13; ++k) c[k] = row[k];
+        if (c[0] >= b.n_envs || c[1] >= A || i != (int)c[0] * A + c[1]) {
+            info = kInfoBadRow;
+            return *st;
+        }
+        const uint32_t goal = (uint32_t)c[4] | ((uint32_t)c[5] << 16);
+        const bool changed = *gc != goal;
+        if (changed) *gc = goal;
+        const uint4 v = state_row(c[0], c[1], c[2], c[3], c[4], c[5], c[6], (c[7] != 0 || changed) ? 1u : 0u);
+        *st = v;
+        uint16_t* h = b.histories + (size_t)i * 5;
+#pragma unroll
+        for (int k = 0; k < 5; ++k) h[k] = c[8 + k];
+        b.labels[i] = (int64_t)c[6];
+        return v;
+    }
+    const uint32_t env = (uint32_t)(i / A);
+    const uint32_t agent = (uint32_t)(i - (int)env * A);
+    const uint32_t tx = (uint16_t)goal_x[i], ty = (uint16_t)goal_y[i];
+    const uint32_t goal = tx | (ty << 16);
+    const bool changed = *gc != goal;
+    if (changed) *gc = goal;
+    const uint4 v = state_row(env, agent, (uint16_t)cur_x[i], (uint16_t)cur_y[i], tx, ty, 0u, changed ? 1u : 0u);
+    *st = v;
+    b.labels[i] = 0;
+    return v;
+}
+
+// Greedy mask of an agent at (px, py) on the map whose field this build
+// keeps, from the tiled copy written by an earlier build.  kMarked (maps of
+// at most kMarkedCells cells): the mark of the agent's own cell, one read;
+// an agent on an unreachable cell (an obstacle, or a component without its
+// goal) and unmarked maps read the cross of five cells (1-3 lines).
+template <int H, bool kMarked>
+__device__ __forceinline__ uint32_t kept_greedy(const jl_mapfgpt_t& b, size_t i, int px, int py) {
+    const int W = b.map_w;
+    const uint16_t* f = b.cost_tiles + i * tiled_cells(W, H);
+    if (kMarked) {
+        const uint32_t c = f[tile_offset<H>(px, py)];
+        if (c != kUnreachable) return c >> 12;
+    }
+    return greedy_mask<H>([f](int x, int y) { return (uint32_t)f[tile_offset<H>(x, y)]; }, px, py, W);
+}
+
+// Refresh of one agent's field (mapf_gpt_cost_to_go_kernel, :181-325) by the
+// calling wavefront (every lane, wavefront-uniform arguments): the
+// bit-parallel BFS (jl_bfs.h) from the goal (gx, gy) over env e's free cells
+// in the wavefront's LDS field s_dist (W * H uint16), then the field
+// row-major into cost_to_go (the API tensor) and in 8x8 tiles into
+// cost_tiles (with greedy marks when kMarked), 16-byte stores.  Returns the
+// agent's info bits: the frontier overflow count, or kInfoBadGoal for a goal
+// off the map or on an obstacle (an all-unreachable field, :224-236), and the
+// greedy mask at its position (spx, spy) when that is on the map.
+template <int H, int R, bool kMarked>
+__device__ uint32_t refresh_field(const jl_mapfgpt_t& b, size_t agent_index, uint32_t e, int gx,
+                                  int gy, int spx, int spy, uint16_t* s_dist) {
+    constexpr int HW = RowWords<H>::HW;
+    const int W = b.map_w;
+    const int lane = threadIdx.x & (kWave - 1);
+    const int cells = W * H;
+    const int words = cells / 32;
+    const size_t tcells = tiled_cells(W, H);
+    for (int c = lane; c < cells; c += kWave) s_dist[c] = kUnreachable;
+    wave_sync();
+    bool ok = e < (uint32_t)b.n_envs && (uint32_t)gx < (uint32_t)W && (uint32_t)gy < (uint32_t)H;
+    const uint32_t* env_bits = b.grid_bits + (size_t)(ok ? e : 0) * words;
+    if (ok && bit_at(env_bits, gx * H + gy)) ok = false;
+    int overflow = 0;
+    if (ok) {
+        uint64_t fr[R][HW];
+        load_free_rows<H, R>(env_bits, W, fr);
+        if (lane == 0) s_dist[gx * H + gy] = 0;
+        wave_sync();
+        if (W * H > kMaxFrontier + 1) {
+            overflow = wave_bfs<H, R, uint16_t, true>(fr, gx, gy, 0x7FFFFFFF, s_dist);
+        } else {
+            overflow = wave_bfs<H, R, uint16_t, false>(fr, gx, gy, 0x7FFFFFFF, s_dist);
+        }
+    }
+    wave_sync();
+    uint32_t info = ok ? (uint32_t)(overflow < 0xFFFFFF ? overflow : 0xFFFFFF) << kInfoOverflowShift
+                       : kInfoBadGoal;
+    if ((uint32_t)spx < (uint32_t)W && (uint32_t)spy < (uint32_t)H)
+        info |= greedy_mask<H>([s_dist](int x, int y) { return (uint32_t)s_dist[x * H + y]; }, spx, spy, W);
+    const uint4* lds4 = reinterpret_cast<const uint4*>(s_dist);
+    uint4* out = reinterpret_cast<uint4*>(b.cost_to_go + agent_index * (size_t)cells);
+    for (int c = lane; c < cells / 8; c += kWave) out[c] = lds4[c];
+    uint4* tout = reinterpret_cast<uint4*>(b.cost_tiles + agent_index * tcells);
+    for (int c = lane; c < (int)(tcells / 8); c += kWave) {
+        const int t = c >> 3, r = c & 7;  // tile, row inside the tile
+        const int x = (t / (H / 8)) * 8 + r, y0 = (t % (H / 8)) * 8;
+        const bool in = x < W;  // rows past the map in the last tile row: unreachable
+        uint4 v = kMarked ? marked_segment<H>(s_dist, W, in ? x : 0, y0) : lds4[((in ? x : 0) * H + y0) >> 3];
+        v.x = in ? v.x : 0xFFFFFFFFu;
+        v.y = in ? v.y : 0xFFFFFFFFu;
+        v.z = in ? v.z : 0xFFFFFFFFu;
+        v.w = in ? v.w : 0xFFFFFFFFu;
+        tout[c] = v;
+    }
+    wave_sync();  // the LDS field is rewritten by the next refresh
+    return info;
+}
+
+// ---------------------------------------------------------------------------
+// Pass 1a (maps of more than kMarkedCells cells): unpack + goal-cache refresh
+// + agent info, one lane per agent, no LDS.  An agent whose field is kept
 // gets its greedy mask from the tiled field; one whose reset flag is set is
 // marked for pass 1b.
 // ---------------------------------------------------------------------------
-constexpr uint32_t kInfoNeedsBfs = 1u << 6;  // agent_info: field to refresh in pass 1b
 constexpr int kUnpackThreads = 256;
 
 template <int H, bool kRows>
@@ -161,93 +285,35 @@ __global__ __launch_bounds__(kUnpackThreads) void unpack_kernel(
     jl_mapfgpt_t b, const int16_t* __restrict__ raw_rows, const int16_t* __restrict__ cur_x,
     const int16_t* __restrict__ cur_y, const int16_t* __restrict__ goal_x,
     const int16_t* __restrict__ goal_y) {
-    const int A = b.n_agents, W = b.map_w;
-    const int N = b.n_envs * A;
+    const int N = b.n_envs * b.n_agents;
     const int i = blockIdx.x * kUnpackThreads + threadIdx.x;
     // the build's diagnostics start from zero; pass 2 and append_actions add
     if (blockIdx.x == 0 && threadIdx.x < 4) b.diagnostics[threadIdx.x] = 0;
     if (i >= N) return;
-
-    bool reset = false;
-    uint32_t px = kUnreachable, py = kUnreachable;  // position of the row this lane now holds
-    uint32_t info = 0;
-    uint16_t* st = b.state_packed + (size_t)i * 8;
-    if (kRows) {
-        const uint16_t* row = reinterpret_cast<const uint16_t*>(raw_rows) + (size_t)i * 13;
-        uint16_t c[13];
-#pragma unroll
-        for (int k = 0; k < 13; ++k) c[k] = row[k];
-        if (c[0] >= b.n_envs || c[1] >= A || i != (int)c[0] * A + c[1]) {
-            // rejected row: every output of this agent keeps its old value,
-            // including the reset flag the BFS pass reads (:90-92, :186-189)
-            info = kInfoBadRow;
-            const uint4 old = *reinterpret_cast<const uint4*>(st);
-            px = old.y & 0xFFFFu;
-            py = old.y >> 16;
-            reset = (old.w >> 16) != 0;
-        } else {
-            uint16_t* gc = b.goal_cache + (size_t)i * 2;
-            const uint32_t cache = *reinterpret_cast<const uint32_t*>(gc);
-            const uint32_t goal = (uint32_t)c[4] | ((uint32_t)c[5] << 16);
-            const bool changed = cache != goal;
-            if (changed) *reinterpret_cast<uint32_t*>(gc) = goal;
-            reset = c[7] != 0 || changed;
-            px = c[2];
-            py = c[3];
-            store_state_row(st, c[0], c[1], c[2], c[3], c[4], c[5], c[6], reset ? 1u : 0u);
-            uint16_t* h = b.histories + (size_t)i * 5;
-#pragma unroll
-            for (int k = 0; k < 5; ++k) h[k] = c[8 + k];
-            b.labels[i] = (int64_t)c[6];
-        }
-    } else {
-        const uint32_t env = (uint32_t)(i / A);
-        const uint32_t agent = (uint32_t)(i - (int)env * A);
-        px = (uint16_t)cur_x[i];
-        py = (uint16_t)cur_y[i];
-        const uint32_t tx = (uint16_t)goal_x[i], ty = (uint16_t)goal_y[i];
-        uint16_t* gc = b.goal_cache + (size_t)i * 2;
-        const uint32_t cache = *reinterpret_cast<const uint32_t*>(gc);
-        const uint32_t goal = tx | (ty << 16);
-        reset = cache != goal;
-        if (reset) *reinterpret_cast<uint32_t*>(gc) = goal;
-        store_state_row(st, env, agent, px, py, tx, ty, 0u, reset ? 1u : 0u);
-        b.labels[i] = 0;
-    }
-    if (reset) {
+    uint32_t info;
+    const uint4 st = unpack_agent<kRows>(b, i, raw_rows, cur_x, cur_y, goal_x, goal_y, info);
+    const uint32_t px = st.y & 0xFFFFu, py = st.y >> 16;
+    if ((st.w >> 16) != 0) {
         info |= kInfoNeedsBfs;
-    } else if (px < (uint32_t)W && py < (uint32_t)H) {
-        // a kept field is read from the tiled copy (written by an earlier
-        // build), where the cross of five cells spans 1-3 lines
-        const uint16_t* f = b.cost_tiles + (size_t)i * tiled_cells(W, H);
-        info |= greedy_mask<H>([f](int x, int y) { return (uint32_t)f[tile_offset<H>(x, y)]; },
-                               (int)px, (int)py, W);
+    } else if (px < (uint32_t)b.map_w && py < (uint32_t)H) {
+        info |= kept_greedy<H, false>(b, (size_t)i, (int)px, (int)py);
     }
     b.agent_info[i] = info;
 }
 
 // ---------------------------------------------------------------------------
-// Pass 1b: BFS of the marked agents (mapf_gpt_cost_to_go_kernel, :181-325).
-// A fixed grid sized to the CUs the LDS fields allow; wavefront g scans agents
-// [g * per_wave, (g + 1) * per_wave) for the mark, so a build without a
-// changed goal costs one scan of agent_info.  Each refresh runs the
-// bit-parallel BFS (jl_bfs.h) in the wavefront's LDS field, stores it
-// row-major (cost_to_go, the API tensor) and in 8x8 tiles (cost_tiles), and
-// completes the agent's info word (greedy mask, overflow count or bad goal).
+// Pass 1b: BFS of the marked agents.  A fixed grid sized to the CUs the LDS
+// fields allow; wavefront g scans agents [g * per_wave, (g + 1) * per_wave)
+// for the mark, so a build without a changed goal costs one scan of
+// agent_info.  Each refresh completes the agent's info word.
 // ---------------------------------------------------------------------------
 template <int H, int R, int kWaves>
 __global__ __launch_bounds__(kWave* kWaves) void bfs_kernel(jl_mapfgpt_t b, int per_wave) {
     extern __shared__ __align__(16) uint16_t s_dist_all[];
-    const int A = b.n_agents, W = b.map_w;
-    const int N = b.n_envs * A;
-    (void)A;
+    const int N = b.n_envs * b.n_agents;
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
-    const int cells = W * H;
-    uint16_t* s_dist = s_dist_all + (size_t)wave * cells;  // this wavefront's field
-    constexpr int HW = RowWords<H>::HW;
-    const int words = cells / 32;
-    const size_t tcells = tiled_cells(W, H);
+    uint16_t* s_dist = s_dist_all + (size_t)wave * b.map_w * H;  // this wavefront's field
     const int begin = (blockIdx.x * kWaves + wave) * per_wave;
     const int end = (begin + per_wave) < N ? (begin + per_wave) : N;
     for (int c0 = begin; c0 < end; c0 += kWave) {
@@ -260,65 +326,20 @@ __global__ __launch_bounds__(kWave* kWaves) void bfs_kernel(jl_mapfgpt_t b, int 
             const size_t agent_index = (size_t)c0 + src;
             // the agent's state row as pass 1a left it
             const uint4 row = *reinterpret_cast<const uint4*>(b.state_packed + agent_index * 8);
-            const uint32_t e = row.x & 0xFFFFu;
-            const int spx = (int)(row.y & 0xFFFFu), spy = (int)(row.y >> 16);
-            const int gx = (int)(row.z & 0xFFFFu), gy = (int)(row.z >> 16);
-            for (int c = lane; c < cells; c += kWave) s_dist[c] = kUnreachable;
-            wave_sync();
-            bool ok = e < (uint32_t)b.n_envs && gx < W && gy < H;
-            const uint32_t* env_bits = b.grid_bits + (size_t)(ok ? e : 0) * words;
-            if (ok && bit_at(env_bits, gx * H + gy)) ok = false;
-            int overflow = 0;
-            if (ok) {
-                uint64_t fr[R][HW];
-                load_free_rows<H, R>(env_bits, W, fr);
-                if (lane == 0) s_dist[gx * H + gy] = 0;
-                wave_sync();
-                if (W * H > kMaxFrontier + 1) {
-                    overflow = wave_bfs<H, R, uint16_t, true>(fr, gx, gy, 0x7FFFFFFF, s_dist);
-                } else {
-                    overflow = wave_bfs<H, R, uint16_t, false>(fr, gx, gy, 0x7FFFFFFF, s_dist);
-                }
-            }
-            wave_sync();
-            if (lane == src) {
-                // goal off the map or on an obstacle: all-unreachable field (:224-236)
-                uint32_t info = mine & ~(kInfoNeedsBfs | kInfoGreedy);
-                info |= ok ? (uint32_t)(overflow < 0xFFFFFF ? overflow : 0xFFFFFF) << kInfoOverflowShift
-                           : kInfoBadGoal;
-                if (spx < W && spy < H)
-                    info |= greedy_mask<H>([s_dist](int x, int y) { return (uint32_t)s_dist[x * H + y]; },
-                                           spx, spy, W);
-                b.agent_info[agent_index] = info;
-            }
-            // row-major field (the API tensor) and the tiled copy, 16-byte stores
-            const uint4* lds4 = reinterpret_cast<const uint4*>(s_dist);
-            uint4* out = reinterpret_cast<uint4*>(b.cost_to_go + agent_index * (size_t)cells);
-            for (int c = lane; c < cells / 8; c += kWave) out[c] = lds4[c];
-            uint4* tout = reinterpret_cast<uint4*>(b.cost_tiles + agent_index * tcells);
-            for (int c = lane; c < (int)(tcells / 8); c += kWave) {
-                const int t = c >> 3, r = c & 7;  // tile, row inside the tile
-                const int x = (t / (H / 8)) * 8 + r, y0 = (t % (H / 8)) * 8;
-                const bool in = x < W;  // rows past the map in the last tile row: unreachable
-                uint4 v = lds4[((in ? x : 0) * H + y0) >> 3];
-                v.x = in ? v.x : 0xFFFFFFFFu;
-                v.y = in ? v.y : 0xFFFFFFFFu;
-                v.z = in ? v.z : 0xFFFFFFFFu;
-                v.w = in ? v.w : 0xFFFFFFFFu;
-                tout[c] = v;
-            }
-            wave_sync();  // the LDS field is rewritten by the next refresh
+            const uint32_t bits = refresh_field<H, R, false>(
+                b, agent_index, row.x & 0xFFFFu, (int)(row.z & 0xFFFFu), (int)(row.z >> 16),
+                (int)(row.y & 0xFFFFu), (int)(row.y >> 16), s_dist);
+            if (lane == src) b.agent_info[agent_index] = (mine & ~(kInfoNeedsBfs | kInfoGreedy)) | bits;
         }
     }
 }
 
 // ---------------------------------------------------------------------------
-// Pass 1 for maps of at most kMarkedCells cells (8 KB fields): 1a and 1b
-// in one launch, one lane per agent and 4 wavefronts per workgroup, each
-// wavefront refreshing the fields of its own agents whose goal changed in
-// its LDS field (the fields are small enough not to limit occupancy, and
-// one launch saves a kernel boundary).  The tiled copies it writes carry
-// the greedy marks (jl_common.h, marked_fields).
+// Pass 1 for maps of at most kMarkedCells cells (8 KB fields) when the
+// single-launch build does not apply: 1a and 1b in one launch, one lane per
+// agent and 4 wavefronts per workgroup, each wavefront refreshing the fields
+// of its own agents whose goal changed in its LDS field.  The tiled copies
+// it writes carry the greedy marks (jl_common.h, marked_fields).
 // ---------------------------------------------------------------------------
 template <int H, int R, bool kRows, int kWaves>
 __global__ __launch_bounds__(kWave* kWaves) void unpack_bfs_kernel(
@@ -326,147 +347,34 @@ __global__ __launch_bounds__(kWave* kWaves) void unpack_bfs_kernel(
     const int16_t* __restrict__ cur_y, const int16_t* __restrict__ goal_x,
     const int16_t* __restrict__ goal_y) {
     extern __shared__ __align__(16) uint16_t s_dist_all[];
-    const int A = b.n_agents, W = b.map_w;
-    const int N = b.n_envs * A;
+    const int W = b.map_w;
+    const int N = b.n_envs * b.n_agents;
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
     const int i = blockIdx.x * (kWave * kWaves) + threadIdx.x;
-    const int cells = W * H;
-    uint16_t* s_dist = s_dist_all + (size_t)wave * cells;  // this wavefront's field
+    uint16_t* s_dist = s_dist_all + (size_t)wave * W * H;  // this wavefront's field
     // the build's diagnostics start from zero; pass 2 and append_actions add
     if (blockIdx.x == 0 && threadIdx.x < 4) b.diagnostics[threadIdx.x] = 0;
 
-    bool reset = false;
-    uint32_t env = 0, tx = 0, ty = 0;
-    uint32_t px = kUnreachable, py = kUnreachable;  // position of the row this lane now holds
+    uint4 st = make_uint4(0u, 0u, 0u, 0u);
     uint32_t info = 0;
-    if (i < N) {
-        uint16_t* st = b.state_packed + (size_t)i * 8;
-        if (kRows) {
-            const uint16_t* row = reinterpret_cast<const uint16_t*>(raw_rows) + (size_t)i * 13;
-            uint16_t c[13];
-#pragma unroll
-            for (int k = 0; k < 13; ++k) c[k] = row[k];
-            if (c[0] >= b.n_envs || c[1] >= A || i != (int)c[0] * A + c[1]) {
-                // rejected row: every output of this agent keeps its old value,
-                // including the reset flag the BFS pass reads (:90-92, :186-189)
-                info = kInfoBadRow;
-                const uint4 old = *reinterpret_cast<const uint4*>(st);
-                env = old.x & 0xFFFFu;
-                px = old.y & 0xFFFFu;
-                py = old.y >> 16;
-                tx = old.z & 0xFFFFu;
-                ty = old.z >> 16;
-                reset = (old.w >> 16) != 0;
-            } else {
-                uint16_t* gc = b.goal_cache + (size_t)i * 2;
-                const uint32_t cache = *reinterpret_cast<const uint32_t*>(gc);
-                const uint32_t goal = (uint32_t)c[4] | ((uint32_t)c[5] << 16);
-                const bool changed = cache != goal;
-                if (changed) *reinterpret_cast<uint32_t*>(gc) = goal;
-                reset = c[7] != 0 || changed;
-                env = c[0];
-                px = c[2];
-                py = c[3];
-                tx = c[4];
-                ty = c[5];
-                store_state_row(st, c[0], c[1], c[2], c[3], c[4], c[5], c[6], reset ? 1u : 0u);
-                uint16_t* h = b.histories + (size_t)i * 5;
-#pragma unroll
-                for (int k = 0; k < 5; ++k) h[k] = c[8 + k];
-                b.labels[i] = (int64_t)c[6];
-            }
-        } else {
-            env = (uint32_t)(i / A);
-            const uint32_t agent = (uint32_t)(i - (int)env * A);
-            px = (uint16_t)cur_x[i];
-            py = (uint16_t)cur_y[i];
-            tx = (uint16_t)goal_x[i];
-            ty = (uint16_t)goal_y[i];
-            uint16_t* gc = b.goal_cache + (size_t)i * 2;
-            const uint32_t cache = *reinterpret_cast<const uint32_t*>(gc);
-            const uint32_t goal = tx | (ty << 16);
-            reset = cache != goal;
-            if (reset) *reinterpret_cast<uint32_t*>(gc) = goal;
-            store_state_row(st, env, agent, px, py, tx, ty, 0u, reset ? 1u : 0u);
-            b.labels[i] = 0;
-        }
-    }
+    if (i < N) st = unpack_agent<kRows>(b, i, raw_rows, cur_x, cur_y, goal_x, goal_y, info);
+    const bool reset = i < N && (st.w >> 16) != 0;
+    const uint32_t px = st.y & 0xFFFFu, py = st.y >> 16;
+    if (i < N && !reset && px < (uint32_t)W && py < (uint32_t)H)
+        info |= kept_greedy<H, true>(b, (size_t)i, (int)px, (int)py);
 
-    // Fields this launch does not rewrite are read from HBM (written by an
-    // earlier launch): the tiled copy of these small maps holds the greedy
-    // mask of every reachable cell, so one read of the agent's own cell
-    // gives it; an agent on an unreachable cell (an obstacle, or a component
-    // without its goal) reads the cross of five cells instead.  Refreshed
-    // fields are read from LDS below.
-    const bool on_map = i < N && px < (uint32_t)W && py < (uint32_t)H;
-    const size_t tcells = tiled_cells(W, H);
-    if (on_map && !reset) {
-        const uint16_t* f = b.cost_tiles + (size_t)i * tcells;
-        const uint32_t c = f[tile_offset<H>((int)px, (int)py)];
-        if (c != kUnreachable) {
-            info |= c >> 12;
-        } else {
-            info |= greedy_mask<H>([f](int x, int y) { return (uint32_t)f[tile_offset<H>(x, y)]; },
-                                   (int)px, (int)py, W);
-        }
-    }
-
-    constexpr int HW = RowWords<H>::HW;
-    const int words = cells / 32;
     uint64_t todo = __ballot(reset);
     while (todo) {
         const int src = __ffsll((unsigned long long)todo) - 1;
         todo &= todo - 1;
-        const uint32_t e = (uint32_t)__shfl((int)env, src, kWave);
-        const int gx = __shfl((int)tx, src, kWave);
-        const int gy = __shfl((int)ty, src, kWave);
-        const int spx = __shfl((int)px, src, kWave);
-        const int spy = __shfl((int)py, src, kWave);
-        const size_t agent_index = (size_t)(i - lane) + src;
-        for (int c = lane; c < cells; c += kWave) s_dist[c] = kUnreachable;
-        wave_sync();
-        bool ok = e < (uint32_t)b.n_envs && gx < W && gy < H;
-        const uint32_t* env_bits = b.grid_bits + (size_t)(ok ? e : 0) * words;
-        if (ok && bit_at(env_bits, gx * H + gy)) ok = false;
-        int overflow = 0;
-        if (ok) {
-            uint64_t fr[R][HW];
-            load_free_rows<H, R>(env_bits, W, fr);
-            if (lane == 0) s_dist[gx * H + gy] = 0;
-            wave_sync();
-            if (W * H > kMaxFrontier + 1) {
-                overflow = wave_bfs<H, R, uint16_t, true>(fr, gx, gy, 0x7FFFFFFF, s_dist);
-            } else {
-                overflow = wave_bfs<H, R, uint16_t, false>(fr, gx, gy, 0x7FFFFFFF, s_dist);
-            }
-        }
-        wave_sync();
-        if (lane == src) {
-            // goal off the map or on an obstacle: all-unreachable field (:224-236)
-            info |= ok ? (uint32_t)(overflow < 0xFFFFFF ? overflow : 0xFFFFFF) << kInfoOverflowShift
-                       : kInfoBadGoal;
-            if (spx < W && spy < H)
-                info |= greedy_mask<H>([s_dist](int x, int y) { return (uint32_t)s_dist[x * H + y]; },
-                                       spx, spy, W);
-        }
-        // row-major field (the API tensor) and the tiled copy, 16-byte stores
-        const uint4* lds4 = reinterpret_cast<const uint4*>(s_dist);
-        uint4* out = reinterpret_cast<uint4*>(b.cost_to_go + agent_index * (size_t)cells);
-        for (int c = lane; c < cells / 8; c += kWave) out[c] = lds4[c];
-        uint4* tout = reinterpret_cast<uint4*>(b.cost_tiles + agent_index * tcells);
-        for (int c = lane; c < (int)(tcells / 8); c += kWave) {
-            const int t = c >> 3, r = c & 7;  // tile, row inside the tile
-            const int x = (t / (H / 8)) * 8 + r, y0 = (t % (H / 8)) * 8;
-            const bool in = x < W;  // rows past the map in the last tile row: unreachable
-            uint4 v = marked_segment<H>(s_dist, W, in ? x : 0, y0);
-            v.x = in ? v.x : 0xFFFFFFFFu;
-            v.y = in ? v.y : 0xFFFFFFFFu;
-            v.z = in ? v.z : 0xFFFFFFFFu;
-            v.w = in ? v.w : 0xFFFFFFFFu;
-            tout[c] = v;
-        }
-        wave_sync();  // the LDS field is rewritten by the next refresh
+        const uint32_t sx = (uint32_t)__shfl((int)st.x, src, kWave);
+        const uint32_t sy = (uint32_t)__shfl((int)st.y, src, kWave);
+        const uint32_t sz = (uint32_t)__shfl((int)st.z, src, kWave);
+        const uint32_t bits = refresh_field<H, R, true>(
+            b, (size_t)(i - lane) + src, sx & 0xFFFFu, (int)(sz & 0xFFFFu), (int)(sz >> 16),
+            (int)(sy & 0xFFFFu), (int)(sy >> 16), s_dist);
+        if (lane == src) info |= bits;
     }
     if (i < N) b.agent_info[i] = info;
 }
@@ -495,6 +403,10 @@ __global__ __launch_bounds__(kWave* kWaves) void unpack_bfs_kernel(
 // wavefront's LDS row, which is then stored as 64 x 16-byte writes.
 // ---------------------------------------------------------------------------
 constexpr int kTokThreads = 1024;
+// Bound of a single-launch workgroup's wait for its launch's cleared totals
+// (each try sleeps ~128 cycles; workgroup 0 clears them at its start, so the
+// bound is never reached by a healthy launch).
+constexpr int kDiagSpinLimit = 1 << 20;
 constexpr int kTokWaves = kTokThreads / kWave;
 // Egos per workgroup: every workgroup stages its whole env, so a workgroup
 // takes the whole env (in steps of 128) up to 1024 egos; larger envs span
@@ -523,13 +435,20 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 struct TokLayout {
     bool dense;
     int hash_slots;
+    int bfs_waves;  // single-launch build: wavefronts refreshing fields at once
     size_t map_off, occ_off, keys_off, vals_off, pos_off, rec_off, copy_off, wave_off, diag_off,
-        total;
+        info_off, list_off, nlist_off, total;
 };
 
 __host__ __device__ inline size_t align16(size_t v) { return (v + 15) & ~(size_t)15; }
 
-__host__ __device__ inline TokLayout tok_layout(int A, int W, int H) {
+// fused: the single-launch build, whose refresh phase lays W*H uint16 LDS
+// fields, one per refreshing wavefront, over the token pass's area (filled
+// only after the refreshes) and keeps each agent's info word and the list of
+// agents to refresh beyond it.  As many wavefronts refresh as fields fit in
+// the larger of that area and 64 KB (at least 8 on these maps of at most
+// 4096 cells).
+__host__ __device__ inline TokLayout tok_layout(int A, int W, int H, bool fused = false) {
     TokLayout L;
     const size_t cells = (size_t)W * H;
     L.dense = cells <= (size_t)kDenseCellLimit;
@@ -555,6 +474,22 @@ __host__ __device__ inline TokLayout tok_layout(int A, int W, int H) {
     off = align16(off + (size_t)kTokWaves * kWaveBytes);
     L.diag_off = off;
     off = align16(off + 4 * 4);
+    L.bfs_waves = 0;
+    L.info_off = L.list_off = L.nlist_off = off;
+    if (fused) {
+        const size_t field = cells * 2;
+        const size_t room = off > 65536 ? off : 65536;
+        const size_t w = room / field;
+        L.bfs_waves = (int)(w < (size_t)kTokWaves ? w : (size_t)kTokWaves);
+        const size_t fields = (size_t)L.bfs_waves * field;
+        off = align16(off > fields ? off : fields);
+        L.info_off = off;
+        off = align16(off + (size_t)A * 4);
+        L.list_off = off;
+        off = align16(off + (size_t)A * 16);
+        L.nlist_off = off;
+        off = align16(off + 4);
+    }
     L.total = off;
     return L;
 }
@@ -568,8 +503,42 @@ __device__ __forceinline__ int cost_token_flat(uint32_t v, int center_minus_limi
     return v == kUnreachable ? kTokUnreachable : r;
 }
 
-template <int H, bool kDense>
-__global__ __launch_bounds__(kTokThreads) void tokens_kernel(jl_mapfgpt_t b) {
+// Diagnostics of a single-launch build.  No earlier launch of the build
+// cleared them: workgroup 0 clears them at its start and then stores the
+// launch's number (strictly increasing over the library's single launches)
+// in build_scratch; a workgroup with counts to add (d, its env's sums) waits
+// (bounded) for that number, then adds.  Totals and the number move only
+// through device-scope atomics, performed where every XCD sees them.
+// Workgroups without counts, the usual case, touch neither.
+__device__ __forceinline__ void publish_single_diagnostics(const jl_mapfgpt_t& b, const int* d,
+                                                           unsigned long long launch) {
+    if ((d[0] | d[1] | d[2] | d[3]) == 0) return;
+    const unsigned long long* cleared = reinterpret_cast<const unsigned long long*>(b.build_scratch);
+    for (int spin = 0; spin < kDiagSpinLimit; ++spin) {
+        if (__hip_atomic_load(cleared, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= launch) break;
+        __builtin_amdgcn_s_sleep(2);
+    }
+    for (int k = 0; k < 4; ++k)
+        if (d[k]) atomicAdd(b.diagnostics + k, d[k]);
+}
+
+// kFuse: 0 = the token pass of a two-launch build; 1 (raw rows) and 2
+// (resident split arrays) = the whole build in one launch (maps of at most
+// kMarkedCells cells, A <= kTokThreads, one workgroup per env), which first
+// unpacks thread t's agent t, then refreshes the env's changed fields with
+// L.bfs_waves wavefronts (BFS with R rows per lane), then runs phases 1-2.
+// A single launch's LDS (under 80 KB) allows two workgroups per CU, 8
+// wavefronts per SIMD, which its SGPRs must allow too: above 80 per
+// wavefront only one workgroup fits (56 vs 48 us per build of 1024 envs x
+// 128 agents on 64x64 maps), so the
+// compiler is held to 8 wavefronts per SIMD (a few SGPRs then live in VGPR
+// lanes).  Not for H = 256, where that bound would spill VGPRs to scratch.
+template <int H, bool kDense, int kFuse, int R>
+__global__ __launch_bounds__(kTokThreads)
+__attribute__((amdgpu_waves_per_eu((kFuse != 0 && H <= 128) ? 8 : 1))) void tokens_kernel(
+    jl_mapfgpt_t b, const int16_t* __restrict__ raw_rows, const int16_t* __restrict__ cur_x,
+    const int16_t* __restrict__ cur_y, const int16_t* __restrict__ goal_x,
+    const int16_t* __restrict__ goal_y, unsigned long long launch) {
     extern __shared__ __align__(16) uint8_t smem[];
     const int A = b.n_agents, W = b.map_w;
     // workgroup = (env, slice of egos); every slice stages the whole env
@@ -582,7 +551,7 @@ __global__ __launch_bounds__(kTokThreads) void tokens_kernel(jl_mapfgpt_t b) {
     const int tid = threadIdx.x;
     const int lane = tid & (kWave - 1);
     const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);  // uniform per wavefront
-    const TokLayout L = tok_layout(A, W, H);
+    const TokLayout L = tok_layout(A, W, H, kFuse != 0);
     constexpr int MH = H + 2 * kRadius;  // dense map columns
     uint32_t* s_map = reinterpret_cast<uint32_t*>(smem + L.map_off);
     uint32_t* s_occ = reinterpret_cast<uint32_t*>(smem + L.occ_off);
@@ -599,6 +568,75 @@ __global__ __launch_bounds__(kTokThreads) void tokens_kernel(jl_mapfgpt_t b) {
     const uint32_t hmask = (uint32_t)L.hash_slots - 1;
     const size_t cells = (size_t)W * H;
     const uint32_t fmask = field_mask(W, H);  // distance bits of a tiled field value
+    uint32_t* s_info = reinterpret_cast<uint32_t*>(smem + L.info_off);  // single launch only
+
+    // ---- phase 0 (single launch): unpack, then the env's field refreshes -----
+    // Agent tid's state row, history and (kept field) the marked value of its
+    // own cell: the history load joins the unpack's, and the cell's is left
+    // in flight until the end of phase 1, so the env's dependent loads cost
+    // one round trip before phase 1 starts.
+    uint4 f_st = make_uint4(0u, 0u, 0u, 0u);
+    uint32_t f_hist[5] = {5u, 5u, 5u, 5u, 5u};
+    uint32_t f_center = kUnreachable;
+    if (kFuse) {
+        uint4* s_list = reinterpret_cast<uint4*>(smem + L.list_off);
+        int* s_nlist = reinterpret_cast<int*>(smem + L.nlist_off);
+        if (tid == 0) *s_nlist = 0;
+        if (blockIdx.x == 0 && tid == 0) {
+            // this launch's diagnostics start from zero, then `launch` is
+            // published (see the end of phase 1)
+            int z = 0;
+            for (int k = 0; k < 4; ++k) z |= atomicExch(b.diagnostics + k, 0);
+            asm volatile("" ::"v"(z));  // cleared before the launch is published
+            atomicExch(reinterpret_cast<unsigned long long*>(b.build_scratch), launch);
+        }
+        bool reset = false;
+        if (tid < A) {
+            const int g = env * A + tid;
+            const uint16_t* h = b.histories + (size_t)g * 5;
+            if (kFuse == 2) {
+#pragma unroll
+                for (int k = 0; k < 5; ++k) f_hist[k] = h[k];
+            }
+            uint32_t info;
+            f_st = unpack_agent<kFuse == 1>(b, g, raw_rows, cur_x, cur_y, goal_x, goal_y, info);
+            if (kFuse == 1) {
+                // a raw row's history, or the kept one of a rejected row
+#pragma unroll
+                for (int k = 0; k < 5; ++k) f_hist[k] = h[k];
+            }
+            reset = (f_st.w >> 16) != 0;
+            const uint32_t px = f_st.y & 0xFFFFu, py = f_st.y >> 16;
+            if (!reset && px < (uint32_t)W && py < (uint32_t)H)
+                f_center = b.cost_tiles[(size_t)g * tiled_cells(W, H) + tile_offset<H>((int)px, (int)py)];
+            s_info[tid] = info;
+        }
+
+        lds_barrier();
+        if (reset) s_list[atomicAdd(s_nlist, 1)] = make_uint4((uint32_t)tid, f_st.x, f_st.y, f_st.z);
+        lds_barrier();
+        const int nlist = __builtin_amdgcn_readfirstlane(*s_nlist);
+        if (nlist > 0) {
+            if (wave < L.bfs_waves) {
+                uint16_t* s_dist = reinterpret_cast<uint16_t*>(smem) + (size_t)wave * cells;
+                for (int k = wave; k < nlist; k += L.bfs_waves) {
+                    const uint4 it = s_list[k];
+                    const uint32_t a = (uint32_t)__builtin_amdgcn_readfirstlane((int)it.x);
+                    const uint32_t sx = (uint32_t)__builtin_amdgcn_readfirstlane((int)it.y);
+                    const uint32_t sy = (uint32_t)__builtin_amdgcn_readfirstlane((int)it.z);
+                    const uint32_t sz = (uint32_t)__builtin_amdgcn_readfirstlane((int)it.w);
+                    const uint32_t bits = refresh_field<H, R, true>(
+                        b, (size_t)env * A + a, sx & 0xFFFFu, (int)(sz & 0xFFFFu), (int)(sz >> 16),
+                        (int)(sy & 0xFFFFu), (int)(sy >> 16), s_dist);
+                    if (lane == 0) s_info[a] |= bits;
+                }
+            }
+            // the refreshed fields are stored before any window load of this
+            // workgroup (its wavefronts share the CU's vector cache), and the
+            // LDS fields are free for phase 1
+            __syncthreads();
+        }
+    }
 
     // ---- phase 1 -----------------------------------------------------------
     if (kDense) {
@@ -622,8 +660,9 @@ __global__ __launch_bounds__(kTokThreads) void tokens_kernel(jl_mapfgpt_t b) {
     int d_over = 0, d_row = 0, d_dup = 0, d_bad = 0;
     for (int a = tid; a < A; a += kTokThreads) {
         const size_t g = (size_t)env * A + a;
-        const uint4 st = *reinterpret_cast<const uint4*>(b.state_packed + g * 8);
-        const uint32_t info = b.agent_info[g];
+        // a single launch holds its agents' rows and info words already (A <= kTokThreads)
+        const uint4 st = kFuse ? f_st : *reinterpret_cast<const uint4*>(b.state_packed + g * 8);
+        const uint32_t info = kFuse ? s_info[a] : b.agent_info[g];
         const uint32_t px = st.y & 0xFFFFu, py = st.y >> 16;
         const uint32_t gx = st.z & 0xFFFFu, gy = st.z >> 16;
         if (a >= e_begin && a < e_end) b.active_mask[g] = (px != gx || py != gy) ? 1 : 0;
@@ -632,15 +671,14 @@ __global__ __launch_bounds__(kTokThreads) void tokens_kernel(jl_mapfgpt_t b) {
         s_rec[a * kRecWords + 0] = st.y;
         s_rec[a * kRecWords + 1] = st.z;
         // history tokens from the raw values (any uint16 is legal in a raw
-        // row, :442-451) and the greedy token (:452-456)
+        // row, :442-451); the greedy token (:452-456) last, below
         const uint16_t* h = b.histories + g * 5;
         int* cp = s_copy + a * kCopyTokens;
 #pragma unroll
         for (int k = 0; k < 5; ++k) {
-            const int v = (int)h[k];
+            const int v = kFuse ? (int)f_hist[k] : (int)h[k];
             cp[k] = v == 5 ? kTokEmptyAction : kTokWait + v;
         }
-        cp[5] = kTokGreedy + (int)(info & kInfoGreedy);
         d_over += (int)(info >> kInfoOverflowShift);
         d_row += (info & kInfoBadRow) ? 1 : 0;
         d_bad += (info & kInfoBadGoal) ? 1 : 0;
@@ -659,6 +697,13 @@ __global__ __launch_bounds__(kTokThreads) void tokens_kernel(jl_mapfgpt_t b) {
         } else {
             ++d_bad;  // position off the map (scatter, :336-339)
         }
+        // a single launch's kept fields: the mark of the agent's own cell,
+        // or the cross of five cells where that cell is unreachable
+        uint32_t greedy = info & kInfoGreedy;
+        if (kFuse && (st.w >> 16) == 0 && valid)
+            greedy = f_center != kUnreachable ? f_center >> 12
+                                              : kept_greedy<H, false>(b, g, (int)px, (int)py);
+        cp[5] = kTokGreedy + (int)greedy;
     }
     if (part != 0) d_over = d_row = d_dup = d_bad = 0;  // the env's counts come from its first slice
     if (d_over) atomicAdd(&s_diag[0], d_over);
@@ -666,9 +711,13 @@ __global__ __launch_bounds__(kTokThreads) void tokens_kernel(jl_mapfgpt_t b) {
     if (d_dup) atomicAdd(&s_diag[2], d_dup);
     if (d_bad) atomicAdd(&s_diag[3], d_bad);
     lds_barrier();
-    // relaxed device-scope adds: the build's totals are complete when the
-    // kernel is, and pass 1 of the build cleared them
-    if (tid < 4 && s_diag[tid]) atomicAdd(b.diagnostics + tid, s_diag[tid]);
+    if (kFuse) {
+        // published after phase 2 (publish_single_diagnostics)
+    } else if (tid < 4 && s_diag[tid]) {
+        // relaxed device-scope adds: the build's totals are complete when
+        // the kernel is, and pass 1 of the build cleared them
+        atomicAdd(b.diagnostics + tid, s_diag[tid]);
+    }
 
     // ---- phase 2: lane constants ---------------------------------------------
     // Window cells q0 = lane and q1 = lane + 64 (row-major over the 11x11
@@ -847,6 +896,8 @@ __global__ __launch_bounds__(kTokThreads) void tokens_kernel(jl_mapfgpt_t b) {
         produce(pos_b, ego_b(p), win_b);
         commit();
     }
+    // wavefront 0 always has pairs (npairs >= 1) and reaches this point
+    if (kFuse && tid == 0) publish_single_diagnostics(b, s_diag, launch);
 }
 
 // History roll (mapf_gpt_append_actions_kernel, mapf_gpt_cuda.cu:155-178): one
@@ -1012,6 +1063,40 @@ int launch_pass1(const jl_mapfgpt_t* b, const int16_t* rows, const int16_t* cx, 
     return launch_status();
 }
 
+// The whole build runs as one launch (tokens_kernel with kFuse) on maps of
+// at most kMarkedCells cells when an env fits one workgroup and the builder
+// has its build scratch.
+bool single_launch(const jl_mapfgpt_t* b) {
+    if (!b->build_scratch || !marked_fields(b->map_w, b->map_h) || b->n_agents > kTokThreads)
+        return false;
+    const TokLayout L = tok_layout(b->n_agents, b->map_w, b->map_h, true);
+    return L.dense && L.total <= 160 * 1024;
+}
+
+// Numbers of single launches, strictly increasing over every builder of the
+// process (a builder's build_scratch only ever sees larger ones).
+std::atomic<unsigned long long> g_single_launches{0};
+
+template <int H, int kFuse>
+int launch_single(const jl_mapfgpt_t* b, const int16_t* rows, const int16_t* cx, const int16_t* cy,
+                  const int16_t* gx, const int16_t* gy, hipStream_t stream) {
+    const TokLayout L = tok_layout(b->n_agents, b->map_w, H, true);
+    const unsigned long long launch = ++g_single_launches;
+    if (b->map_w <= 64) {
+        hipLaunchKernelGGL((tokens_kernel<H, true, kFuse, 1>), dim3(b->n_envs), dim3(kTokThreads),
+                           L.total, stream, *b, rows, cx, cy, gx, gy, launch);
+    } else {
+        // W > 64 with W * H <= kMarkedCells: H == 32 only
+        if constexpr (H == 32) {
+            hipLaunchKernelGGL((tokens_kernel<H, true, kFuse, 2>), dim3(b->n_envs), dim3(kTokThreads),
+                               L.total, stream, *b, rows, cx, cy, gx, gy, launch);
+        } else {
+            return JL_ERR_PROFILE;
+        }
+    }
+    return launch_status();
+}
+
 template <bool kRows>
 int build(const jl_mapfgpt_t* b, const int16_t* rows, const int16_t* cx, const int16_t* cy,
           const int16_t* gx, const int16_t* gy, hipStream_t stream) {
@@ -1020,6 +1105,26 @@ int build(const jl_mapfgpt_t* b, const int16_t* rows, const int16_t* cx, const i
     const int W = b->map_w;
     const TokLayout L = tok_layout(b->n_agents, W, b->map_h);
     if (L.total > 160 * 1024) return JL_ERR_PROFILE;
+    // a build captured into a graph keeps two launches: a replay repeats the
+    // captured launch number, which then orders nothing
+    hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+    rc = status(hipStreamIsCapturing(stream, &capture));
+    if (rc) return rc;
+    if (single_launch(b) && capture == hipStreamCaptureStatusNone) {
+        JL_DISPATCH_H(b->map_h, {
+            if (b->token_events[0]) {
+                rc = status(hipEventRecord((hipEvent_t)b->token_events[0], stream));
+                if (rc) return rc;
+            }
+            rc = launch_single<H, kRows ? 1 : 2>(b, rows, cx, cy, gx, gy, stream);
+            if (rc) return rc;
+            if (b->token_events[1]) {
+                rc = status(hipEventRecord((hipEvent_t)b->token_events[1], stream));
+                if (rc) return rc;
+            }
+        });
+        return JL_OK;
+    }
     JL_DISPATCH_H(b->map_h, {
         if (W <= 64) {
             rc = launch_pass1<H, 1, kRows>(b, rows, cx, cy, gx, gy, stream);
@@ -1035,10 +1140,13 @@ int build(const jl_mapfgpt_t* b, const int16_t* rows, const int16_t* cx, const i
         }
         const int slice = ego_slice(b->n_agents);
         const dim3 grid2((unsigned)b->n_envs * ((b->n_agents + slice - 1) / slice));
+        const int16_t* none = nullptr;
         if (L.dense) {
-            hipLaunchKernelGGL((tokens_kernel<H, true>), grid2, dim3(kTokThreads), L.total, stream, *b);
+            hipLaunchKernelGGL((tokens_kernel<H, true, 0, 1>), grid2, dim3(kTokThreads), L.total, stream,
+                               *b, none, none, none, none, none, 0ull);
         } else {
-            hipLaunchKernelGGL((tokens_kernel<H, false>), grid2, dim3(kTokThreads), L.total, stream, *b);
+            hipLaunchKernelGGL((tokens_kernel<H, false, 0, 1>), grid2, dim3(kTokThreads), L.total,
+                               stream, *b, none, none, none, none, none, 0ull);
         }
         rc = launch_status();
         if (rc) return rc;
@@ -1066,6 +1174,11 @@ extern "C" int jl_mapfgpt_build_state(const jl_mapfgpt_t* b, const int16_t* cur_
                                       const int16_t* goal_y, jl_stream_t stream) {
     if (!cur_x || !cur_y || !goal_x || !goal_y) return JL_ERR_ARG;
     return build<false>(b, nullptr, cur_x, cur_y, goal_x, goal_y, (hipStream_t)stream);
+}
+
+extern "C" int jl_mapfgpt_single_launch(const jl_mapfgpt_t* b) {
+    if (check_builder(b)) return 0;
+    return single_launch(b) ? 1 : 0;
 }
 
 extern "C" int jl_mapfgpt_refresh_state(const jl_mapfgpt_t* b, const int16_t* cur_x,

@@ -276,6 +276,9 @@ class MapfGPTObservationBuilder(_Base):
             self._cost_tiles = torch.full(
                 (E, n_agents, (W + 7) // 8 * 8 * H), -1, dtype=torch.int16, device=device
             )
+            # single-launch builds: number of the last launch whose diagnostics
+            # were cleared (uint64); zero at construction
+            self._build_scratch = torch.zeros((8,), dtype=torch.int32, device=device)
         self._desc = MapfGPTDesc(
             n_envs=E,
             n_agents=n_agents,
@@ -293,6 +296,7 @@ class MapfGPTObservationBuilder(_Base):
             diagnostics=_ptr(self.t_diagnostics),
             agent_info=_ptr(self._agent_info),
             cost_tiles=_ptr(self._cost_tiles),
+            build_scratch=_ptr(self._build_scratch),
         )
         self._desc_ref = ctypes.byref(self._desc)
 
@@ -315,6 +319,14 @@ class MapfGPTObservationBuilder(_Base):
             self._lib.jl_mapfgpt_build_rows(self._desc_ref, raw_rows.data_ptr(), _stream(self._device)),
             "MAPF-GPT cost-to-go generation",
         )
+
+    @property
+    def single_launch(self) -> bool:
+        """True when an eager build runs as one launch (unpack, field
+        refreshes and tokens of an env in one workgroup): maps of at most 4096
+        cells and at most 1024 agents per env; builds captured into a graph
+        keep two launches.  No counterpart in the reference."""
+        return bool(self._lib.jl_mapfgpt_single_launch(self._desc_ref))
 
     def _check_state(self, t: torch.Tensor, name: str) -> None:
         _require(t.is_cuda, f"{name} must be on a CUDA device")

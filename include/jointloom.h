@@ -173,6 +173,11 @@ typedef struct jl_mapfgpt {
                                    cost_to_go in 8x8 tiles (one 128-byte line per tile); on
                                    maps of at most 4096 cells bits 12-15 of a reachable cell
                                    hold its greedy-move mask */
+    int32_t* build_scratch;     /* [8] workspace, zero at construction, 8-byte aligned: the
+                                   single-launch build of small maps keeps in [0..1] the
+                                   uint64 number of the last launch whose diagnostics were
+                                   cleared, which orders the clearing before that launch's
+                                   adds.  NULL = two-launch builds only */
     void* token_events[2];      /* optional hipEvent_t pair recorded on the stream right
                                    before / after the token kernel (profiling); NULL = off */
 } jl_mapfgpt_t;
@@ -195,8 +200,14 @@ int jl_mapfgpt_build_state(const jl_mapfgpt_t* b, const int16_t* cur_x,
                            const int16_t* cur_y, const int16_t* goal_x,
                            const int16_t* goal_y, jl_stream_t stream);
 
-/* append_actions(uint8 [E, A]).  Replaces mapf_gpt_append_actions_kernel,
- * mapf_gpt_cuda.cu:155-178. */
+/* 1 when an eager build of this builder runs as one launch (maps of at most
+ * 4096 cells, an env of at most 1024 agents, build_scratch set): unpack,
+ * field refreshes and tokens of an env in one workgroup; 0 when it runs as
+ * two or three launches (as do builds captured into a graph).  No
+ * counterpart in the reference (a profiling query: the token_events pair
+ * then brackets the whole build). */
+int jl_mapfgpt_single_launch(const jl_mapfgpt_t* b);
+
 /* Goal-cache refresh and BFS of changed goals from the resident split state,
  * without tokens: state rows, labels, goal cache, cost_to_go (and its tiled
  * copy), diagnostics [0] and [3].  Replaces
@@ -206,6 +217,8 @@ int jl_mapfgpt_refresh_state(const jl_mapfgpt_t* b, const int16_t* cur_x,
                              const int16_t* cur_y, const int16_t* goal_x,
                              const int16_t* goal_y, jl_stream_t stream);
 
+/* append_actions(uint8 [E, A]).  Replaces mapf_gpt_append_actions_kernel,
+ * mapf_gpt_cuda.cu:155-178. */
 int jl_mapfgpt_append_actions(const jl_mapfgpt_t* b, const uint8_t* actions,
                               jl_stream_t stream);
 

@@ -408,45 +408,92 @@ def test_raw_row_history_values_outside_action_range(oracle):
     assert ob.tokens.max() > 66  # the unbounded history tokens are really present
 
 
-@pytest.mark.parametrize("W,H", [(64, 64), (36, 32)])
-def test_kept_fields_greedy_tokens_match_oracle(oracle, W, H):
-    """Maps of at most 4096 cells keep each field's greedy-move masks in its
-    tiled copy: builds that keep the fields (goals unchanged, reset flag 0)
-    read an agent's mask from its own cell, and agents on unreachable cells
-    (obstacles, components without the goal) take the five-cell path."""
-    from iclr_2027_jointoom_amd import profile
-
-    rng = np.random.default_rng(W + H)
-    E, A = 3, 40
-    grids = (rng.random((E, W, H)) < 0.3).astype(np.int32)
+def _rows_case(rng, grids, A, goals=None):
+    """Raw rows of every agent at distinct random cells (obstacles included);
+    goals on free cells unless given."""
+    E, W, H = grids.shape
     rows = np.zeros((E * A, 13), np.uint16)
     rows[:, 0] = np.repeat(np.arange(E), A)
     rows[:, 1] = np.tile(np.arange(A), E)
     for e in range(E):
-        free = np.flatnonzero(grids[e].ravel() == 0)
-        g = rng.choice(free, A, replace=False)
-        rows[e * A:(e + 1) * A, 4] = g // H
-        rows[e * A:(e + 1) * A, 5] = g % H
-    rows[:, 8:13] = 5
+        cells = rng.choice(W * H, A, replace=False)
+        rows[e * A:(e + 1) * A, 2] = cells // H
+        rows[e * A:(e + 1) * A, 3] = cells % H
+        if goals is None:
+            free = np.flatnonzero(grids[e].ravel() == 0)
+            g = rng.choice(free, A, replace=False)
+            rows[e * A:(e + 1) * A, 4] = g // H
+            rows[e * A:(e + 1) * A, 5] = g % H
+    if goals is not None:
+        rows[:, 4:6] = goals
+    rows[:, 6] = rng.integers(0, 5, E * A)
+    rows[:, 8:13] = rng.integers(0, 6, (E * A, 5))
+    return rows
+
+
+@pytest.mark.parametrize("W,H,A", [(64, 64, 40), (36, 32, 40), (128, 32, 96), (64, 64, 1024)])
+def test_single_launch_build_matches_oracle_and_two_launch_build(oracle, W, H, A):
+    """Maps of at most 4096 cells with at most 1024 agents per env build in
+    one launch: unpack, the env's field refreshes (with the greedy marks of
+    the tiled copy) and tokens in one workgroup, diagnostics summed across
+    workgroups.  Every output equals the oracle's and the two-launch build's
+    (the same builder without its build scratch), over builds that keep,
+    change and re-mark fields, with rejected rows, shared cells, positions
+    off the map, goals on obstacles and agents on unreachable cells."""
+    from iclr_2027_jointoom_amd import profile
+
+    rng = np.random.default_rng(W + H + A)
+    E = 3
+    grids = (rng.random((E, W, H)) < 0.3).astype(np.int32)
     ext = profile(W, H)
-    b = ext.MapfGPTObservationBuilder(torch.from_numpy(grids).cuda(), A)
+    g = torch.from_numpy(grids).cuda()
+    one = ext.MapfGPTObservationBuilder(g, A)
+    two = ext.MapfGPTObservationBuilder(g, A)
+    two._desc.build_scratch = None
+    assert one.single_launch and not two.single_launch
     ob = oracle.OracleMapfGPT(grids, A)
-    on_obstacle = 0
-    for it in range(4):
-        rows[:, 7] = 1 if it == 0 else 0
-        for e in range(E):
-            cells = rng.choice(W * H, A, replace=False)  # anywhere, obstacles included
-            rows[e * A:(e + 1) * A, 2] = cells // H
-            rows[e * A:(e + 1) * A, 3] = cells % H
-            on_obstacle += int(grids[e].ravel()[cells].sum())
-        rows[:, 6] = rng.integers(0, 5, E * A)
-        b.build_tokens(torch.from_numpy(rows.astype(np.int16)).cuda())
+    rows = _rows_case(rng, grids, A)
+    goals = rows[:, 4:6].copy()
+    diag_seen = np.zeros(4, np.int64)
+    last_launch = 0
+    for it in range(5):
+        rows = _rows_case(rng, grids, A, goals)
+        rows[:, 7] = 1 if it in (0, 3) else 0
+        if it >= 1:
+            rows[5, 0] = E + 1                     # rejected row (env out of range)
+            rows[A + 2, 1] = A                     # rejected row (agent out of range)
+            rows[7, 2:4] = rows[8, 2:4]            # two agents on one cell
+            rows[2 * A + 1, 2] = W + 3             # position off the map
+        if it == 2:
+            obst = np.argwhere(grids[1] != 0)[0]
+            rows[A + 5, 4:6] = obst                # goal on an obstacle
+            rows[A + 6, 4:6] = (W + 1, 0)          # goal off the map
+            rows[9, 4:6] = rows[10, 4:6]           # a changed goal
+        t = torch.from_numpy(rows.astype(np.int16)).cuda()
+        one.build_tokens(t)
+        two.build_tokens(t)
         ob.build_rows(rows)
         torch.cuda.synchronize()
-        assert np.array_equal(b.tokens.cpu().numpy(), ob.tokens), it
-        assert np.array_equal(b.cost_to_go.cpu().numpy(), ob.cost_to_go.view(np.int16)), it
-        assert b.diagnostics.cpu().tolist() == ob.diagnostics.tolist(), it
-    assert on_obstacle > 0
-    # the greedy tokens cover every mask value class seen on such maps
-    greedy = ob.tokens[:, 121 + 9::10][:, :1].ravel()
+        for name in ("tokens", "labels", "active_mask", "cost_to_go", "state_packed", "histories",
+                     "goal_cache", "diagnostics"):
+            assert torch.equal(getattr(one, name), getattr(two, name)), (it, name)
+        assert np.array_equal(one.tokens.cpu().numpy(), ob.tokens), it
+        assert np.array_equal(one.cost_to_go.cpu().numpy(), ob.cost_to_go.view(np.int16)), it
+        assert np.array_equal(one.state_packed.cpu().numpy(), ob.state_packed.view(np.int16)), it
+        assert one.diagnostics.cpu().tolist() == ob.diagnostics.tolist(), it
+        diag_seen += np.array(ob.diagnostics.tolist()) != 0
+        # the number of this launch, published after the clearing (uint64)
+        published = one._build_scratch.cpu().view(torch.int64)[0].item()
+        assert published > last_launch, it
+        last_launch = published
+        # the resident builds of the same states agree as well
+        st = one.state_packed.view(E, A, 8)
+        if it == 4:
+            one.build_tokens_from_state(*(st[:, :, k].contiguous() for k in (2, 3, 4, 5)))
+            two.build_tokens_from_state(*(st[:, :, k].contiguous() for k in (2, 3, 4, 5)))
+            torch.cuda.synchronize()
+            for name in ("tokens", "active_mask", "cost_to_go", "diagnostics"):
+                assert torch.equal(getattr(one, name), getattr(two, name)), name
+    assert diag_seen[1] > 0 and diag_seen[2] > 0 and diag_seen[3] > 0
+    greedy = ob.tokens[:, 121 + 9]
     assert len(np.unique(greedy)) > 4
