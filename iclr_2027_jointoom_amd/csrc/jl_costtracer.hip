@@ -134,16 +134,16 @@ __device__ __forceinline__ void observe_agents(const jl_sim_t& s, const jl_mapfg
         const uint32_t* ocp = s.grid_ocp + (size_t)(i / A) * words;
         c0[k] = (uint32_t)(xa * H + ya);
         c1[k] = (uint32_t)(xb * H + yb);
-        raw0[k] = field_distance(f[tile_at<H>(xa, ya)], fmask);
-        raw1[k] = field_distance(f[tile_at<H>(xb, yb)], fmask);
+        raw0[k] = f[tile_at<H>(xa, ya)];  // marks stripped where the distance is taken
+        raw1[k] = f[tile_at<H>(xb, yb)];
         w0[k] = ocp[c0[k] >> 5];
         w1[k] = ocp[c1[k] >> 5];
     }
 #pragma unroll
     for (int k = 0; k < kObsPer; ++k) {
         if (k >= nvalid) break;  // wavefront-uniform
-        const int d0 = (in0[k] && raw0[k] != kUnreachable) ? (int)raw0[k] : -1;
-        const int d1 = (in1[k] && raw1[k] != kUnreachable) ? (int)raw1[k] : -1;
+        const int d0 = (in0[k] && raw0[k] != kUnreachable) ? (int)(raw0[k] & fmask) : -1;
+        const int d1 = (in1[k] && raw1[k] != kUnreachable) ? (int)(raw1[k] & fmask) : -1;
         // largest reachable distance in the window (0 if none)
         const int M = wave_max(max(max(0, d0), has1 ? max(0, d1) : 0));
         // cells without a distance sit 4 past the largest one
@@ -154,7 +154,8 @@ __device__ __forceinline__ void observe_agents(const jl_sim_t& s, const jl_mapfg
         v1 -= m;
         const int V = wave_max(has1 ? max(v0, v1) : v0);
         // the distance at the agent's cell is the window centre (t = 60, lane 60)
-        const int current = __builtin_amdgcn_readlane((int)raw0[k], kObsCentre);
+        const int current =
+            (int)field_distance((uint32_t)__builtin_amdgcn_readlane((int)raw0[k], kObsCentre), fmask);
         int bi = __builtin_amdgcn_readlane(bestl, k);
         if (bi < 0 || __builtin_amdgcn_readlane(resetl, k) != 0) {
             bi = current;

@@ -1,7 +1,10 @@
 // jl_mapfgpt.hip - MAPF-GPT observation builder for gfx950.
 //
-// A build is three launches (two on maps of up to 4096 cells, where 1a and
-// 1b are one kernel):
+// On maps of at most 4096 cells with at most 1024 agents per env an eager
+// build is one launch of the token kernel, one workgroup per env: its phase 0
+// unpacks the env's agents and refreshes their changed fields (the work of
+// 1a and 1b below), then phases 1 and 2 follow.  Otherwise a build is three
+// launches (two on maps of up to 4096 cells, where 1a and 1b are one kernel):
 //   1a. unpack: one lane per agent, no LDS.  Unpacks the state (raw rows or
 //      resident split arrays), refreshes the goal cache and writes every
 //      agent's info word: the greedy-move mask from the kept tiled field, or a
@@ -10,7 +13,8 @@
 //      words and runs the bit-parallel BFS (jl_bfs.h) for the marked agents
 //      in its own LDS field, stores the field row-major (cost_to_go, the API
 //      tensor) and in 8x8 tiles (cost_tiles), and completes the info word.
-//   2. tokens: one 1024-thread workgroup per 128 egos of an env.  Phase 1
+//   2. tokens: one 1024-thread workgroup per env (per 1024 egos of a larger
+//      env).  Phase 1
 //      stages the env's agents (position, goal, the six ego-independent
 //      tokens) and a cell -> agent map in LDS and sums the env's diagnostics.
 //      Phase 2: every wavefront on its own gathers the 11x11 windows of its
@@ -495,9 +499,10 @@ __host__ __device__ inline TokLayout tok_layout(int A, int W, int H, bool fused 
 }
 
 // Cost token of a window value (mapf_gpt_cuda.cu:413-428) without branches;
-// unreachable cells, including those outside the map, hold kUnreachable.
-__device__ __forceinline__ int cost_token_flat(uint32_t v, int center_minus_limit) {
-    const int t = (int)v - center_minus_limit;  // d + kCostLimit
+// unreachable cells, including those outside the map, hold kUnreachable, and
+// fmask strips a reachable value's greedy marks (field_mask).
+__device__ __forceinline__ int cost_token_flat(uint32_t v, int center_minus_limit, uint32_t fmask) {
+    const int t = (int)(v & fmask) - center_minus_limit;  // d + kCostLimit (marks stripped)
     const int clip = t < 0 ? kTokNegClip : kTokPosClip;
     const int r = (uint32_t)t <= (uint32_t)(2 * kCostLimit) ? t : clip;
     return v == kUnreachable ? kTokUnreachable : r;
@@ -790,8 +795,8 @@ __attribute__((amdgpu_waves_per_eu((kFuse != 0 && H <= 128) ? 8 : 1))) void toke
             // region row = dx + 5, column = ey + dy - 8 * tyl (see seg_load)
             const uint16_t* win = win_base + (ey - 8 * (((ey - kRadius + 64) >> 3) - 8) - kRadius);
             const uint32_t center = field_distance(win[kRadius * kRegionCols + kRadius], fmask);
-            const uint32_t v0 = field_distance(win[win0], fmask);
-            const uint32_t v1 = field_distance(win[win1], fmask);
+            const uint32_t v0 = win[win0];  // raw tiled values: cost_token_flat strips the marks
+            const uint32_t v1 = win[win1];
             uint32_t id0, id1;
             if (kDense) {
                 const uint32_t* mrow = s_map + (ex + kRadius) * MH + (ey + kRadius);
@@ -825,8 +830,8 @@ __attribute__((amdgpu_waves_per_eu((kFuse != 0 && H <= 128) ? 8 : 1))) void toke
             if (has_q1 && id1 != kNoAgent && r1 < kVisible) my_slots[r1] = id1;
             // cost tokens
             const int cml = (int)center - kCostLimit;
-            my_row[q0] = cost_token_flat(v0, cml);
-            if (has_q1) my_row[q1] = cost_token_flat(v1, cml);
+            my_row[q0] = cost_token_flat(v0, cml, fmask);
+            if (has_q1) my_row[q1] = cost_token_flat(v1, cml, fmask);
             wave_sync();
             // agent tokens; a slot at or past nsel is padding
             if (lane < kCoordLanes) {
