@@ -13,7 +13,7 @@
 //      words and runs the bit-parallel BFS (jl_bfs.h) for the marked agents
 //      in its own LDS field, stores the field row-major (cost_to_go, the API
 //      tensor) and in 8x8 tiles (cost_tiles), and completes the info word.
-//   2. tokens: one 1024-thread workgroup per env (per 1024 egos of a larger
+//   2. tokens: one 1024-thread workgroup per env (per 512 egos of a larger
 //      env).  Phase 1
 //      stages the env's agents (position, goal, the six ego-independent
 //      tokens) and a cell -> agent map in LDS and sums the env's diagnostics.
@@ -387,9 +387,11 @@ __global__ __launch_bounds__(kWave* kWaves) void unpack_bfs_kernel(
 // Pass 2: tokens (mapf_gpt_materialize_tokens_kernel, :350-497) plus the
 // agent scatter and its diagnostics (:328-347).
 //
-// Phase 1 (whole workgroup, one env): positions, each agent's record
-// (position and goal words) and its six ego-independent tokens (five history
-// tokens and the greedy token, :437-456) and a cell -> agent map live in LDS.
+// Phase 1 (whole workgroup, one env): each agent's record (position word,
+// kNoAgent off the map, and goal word), the raw values of its six
+// ego-independent tokens (five history values and the greedy mask, :437-456;
+// 16 bits each, turned into tokens where a row copies them) and a cell ->
+// agent map live in LDS.
 // The map is dense (one int32 per cell of the map grown by a kRadius border
 // of empty cells, so a window probe needs no bounds test) while it fits, an
 // occupancy bitmap + hash beyond.
@@ -412,10 +414,12 @@ constexpr int kTokThreads = 1024;
 // bound is never reached by a healthy launch).
 constexpr int kDiagSpinLimit = 1 << 20;
 constexpr int kTokWaves = kTokThreads / kWave;
-// Egos per workgroup: every workgroup stages its whole env, so a workgroup
-// takes the whole env (in steps of 128) up to 1024 egos; larger envs span
-// ceil(A / 1024) workgroups.
-__host__ __device__ inline int ego_slice(int A) { return A > 1024 ? 1024 : (A + 127) / 128 * 128; }
+// Egos per workgroup of a two-launch build: every workgroup stages its whole
+// env, so a workgroup takes the whole env (in steps of 128) up to 512 egos;
+// larger envs span ceil(A / 512) workgroups, whose LDS (under 80 KB up to
+// 1024 agents on any map) lets two share a CU (a single launch takes its
+// whole env).
+__host__ __device__ inline int ego_slice(int A) { return A > 512 ? 512 : (A + 127) / 128 * 128; }
 constexpr int kDenseCellLimit = 16384;     // map cells up to which the agent map is dense
 // A window is read as 11 rows x 3 tile columns of 16-byte tile-row segments
 // (8 cells each): the 11 columns of a row span 2 or 3 tile columns.
@@ -423,7 +427,8 @@ constexpr int kSegPerEgo = kDiam * 3;
 constexpr int kRegionCols = 24;            // cells per region row (3 tile columns)
 constexpr int kSlotStride = 16;            // per-wave top-13 slot array (words)
 constexpr int kRecWords = 2;               // per-agent record: position word, goal word
-constexpr int kCopyTokens = 6;             // per-agent tokens independent of the ego
+constexpr int kCopyTokens = 6;             // per-agent tokens independent of the ego, kept
+                                           // as uint16 raw values: 5 history values, greedy mask
 constexpr int kCoordLanes = kVisible * 4;  // lanes producing the 52 coordinate tokens
 constexpr int kCopyItems = kVisible * kCopyTokens;  // 78 copied tokens per row
 // per-wavefront LDS: two egos' windows, the token row, the slot array
@@ -440,7 +445,7 @@ struct TokLayout {
     bool dense;
     int hash_slots;
     int bfs_waves;  // single-launch build: wavefronts refreshing fields at once
-    size_t map_off, occ_off, keys_off, vals_off, pos_off, rec_off, copy_off, wave_off, diag_off,
+    size_t map_off, occ_off, keys_off, vals_off, rec_off, copy_off, wave_off, diag_off,
         info_off, list_off, nlist_off, total;
 };
 
@@ -468,12 +473,10 @@ __host__ __device__ inline TokLayout tok_layout(int A, int W, int H, bool fused 
     off = align16(off + (size_t)L.hash_slots * 4);
     L.vals_off = off;
     off = align16(off + (size_t)L.hash_slots * 4);
-    L.pos_off = off;
-    off = align16(off + (size_t)A * 4);
     L.rec_off = off;
     off = align16(off + (size_t)A * kRecWords * 4);
     L.copy_off = off;
-    off = align16(off + (size_t)A * kCopyTokens * 4);
+    off = align16(off + (size_t)A * kCopyTokens * 2);
     L.wave_off = off;
     off = align16(off + (size_t)kTokWaves * kWaveBytes);
     L.diag_off = off;
@@ -506,6 +509,13 @@ __device__ __forceinline__ int cost_token_flat(uint32_t v, int center_minus_limi
     const int clip = t < 0 ? kTokNegClip : kTokPosClip;
     const int r = (uint32_t)t <= (uint32_t)(2 * kCostLimit) ? t : clip;
     return v == kUnreachable ? kTokUnreachable : r;
+}
+
+// Token of a copied per-agent value: a raw history value v (5 = empty,
+// else kTokWait + v, any uint16, mapf_gpt_cuda.cu:437-451) or, for k = 5, the
+// greedy mask (:452-456).
+__device__ __forceinline__ int copy_token(uint32_t v, int k) {
+    return k == kCopyTokens - 1 ? kTokGreedy + (int)v : (v == 5 ? kTokEmptyAction : kTokWait + (int)v);
 }
 
 // Diagnostics of a single-launch build.  No earlier launch of the build
@@ -547,7 +557,7 @@ __attribute__((amdgpu_waves_per_eu((kFuse != 0 && H <= 128) ? 8 : 1))) void toke
     extern __shared__ __align__(16) uint8_t smem[];
     const int A = b.n_agents, W = b.map_w;
     // workgroup = (env, slice of egos); every slice stages the whole env
-    const int slice = ego_slice(A);
+    const int slice = kFuse ? A : ego_slice(A);  // a single launch: one workgroup per env
     const int parts = (A + slice - 1) / slice;
     const int env = blockIdx.x / parts;
     const int part = blockIdx.x - env * parts;
@@ -562,9 +572,8 @@ __attribute__((amdgpu_waves_per_eu((kFuse != 0 && H <= 128) ? 8 : 1))) void toke
     uint32_t* s_occ = reinterpret_cast<uint32_t*>(smem + L.occ_off);
     uint32_t* s_keys = reinterpret_cast<uint32_t*>(smem + L.keys_off);
     uint32_t* s_vals = reinterpret_cast<uint32_t*>(smem + L.vals_off);
-    uint32_t* s_pos = reinterpret_cast<uint32_t*>(smem + L.pos_off);
     uint32_t* s_rec = reinterpret_cast<uint32_t*>(smem + L.rec_off);    // kRecWords per agent
-    int* s_copy = reinterpret_cast<int*>(smem + L.copy_off);            // kCopyTokens per agent
+    uint16_t* s_copy = reinterpret_cast<uint16_t*>(smem + L.copy_off);  // kCopyTokens per agent
     int* s_diag = reinterpret_cast<int*>(smem + L.diag_off);
     uint8_t* my_lds = smem + L.wave_off + (size_t)wave * kWaveBytes;
     uint4* my_win = reinterpret_cast<uint4*>(my_lds);                  // [2 egos][11 rows][3 segments]
@@ -672,18 +681,15 @@ __attribute__((amdgpu_waves_per_eu((kFuse != 0 && H <= 128) ? 8 : 1))) void toke
         const uint32_t gx = st.z & 0xFFFFu, gy = st.z >> 16;
         if (a >= e_begin && a < e_end) b.active_mask[g] = (px != gx || py != gy) ? 1 : 0;
         const bool valid = px < (uint32_t)W && py < (uint32_t)H;
-        s_pos[a] = valid ? (px | (py << 16)) : kNoAgent;
-        s_rec[a * kRecWords + 0] = st.y;
+        // position word (kNoAgent off the map: such an ego's row is padding)
+        s_rec[a * kRecWords + 0] = valid ? st.y : kNoAgent;
         s_rec[a * kRecWords + 1] = st.z;
-        // history tokens from the raw values (any uint16 is legal in a raw
-        // row, :442-451); the greedy token (:452-456) last, below
+        // raw history values (any uint16 is legal in a raw row, :442-451);
+        // the greedy mask (:452-456) last, below
         const uint16_t* h = b.histories + g * 5;
-        int* cp = s_copy + a * kCopyTokens;
+        uint16_t* cp = s_copy + a * kCopyTokens;
 #pragma unroll
-        for (int k = 0; k < 5; ++k) {
-            const int v = kFuse ? (int)f_hist[k] : (int)h[k];
-            cp[k] = v == 5 ? kTokEmptyAction : kTokWait + v;
-        }
+        for (int k = 0; k < 5; ++k) cp[k] = kFuse ? (uint16_t)f_hist[k] : h[k];
         d_over += (int)(info >> kInfoOverflowShift);
         d_row += (info & kInfoBadRow) ? 1 : 0;
         d_bad += (info & kInfoBadGoal) ? 1 : 0;
@@ -708,7 +714,7 @@ __attribute__((amdgpu_waves_per_eu((kFuse != 0 && H <= 128) ? 8 : 1))) void toke
         if (kFuse && (st.w >> 16) == 0 && valid)
             greedy = f_center != kUnreachable ? f_center >> 12
                                               : kept_greedy<H, false>(b, g, (int)px, (int)py);
-        cp[5] = kTokGreedy + (int)greedy;
+        cp[5] = (uint16_t)greedy;
     }
     if (part != 0) d_over = d_row = d_dup = d_bad = 0;  // the env's counts come from its first slice
     if (d_over) atomicAdd(&s_diag[0], d_over);
@@ -842,12 +848,12 @@ __attribute__((amdgpu_waves_per_eu((kFuse != 0 && H <= 128) ? 8 : 1))) void toke
             }
             {
                 const uint32_t o = my_slots[k_slot0];
-                const int t = s_copy[o * kCopyTokens + k_tok0];
+                const int t = copy_token(s_copy[o * kCopyTokens + k_tok0], k_tok0);
                 my_row[k_pos0] = k_slot0 < nsel ? t : kTokPad;
             }
             if (lane + kWave < kCopyItems) {
                 const uint32_t o = my_slots[k_slot1];
-                const int t = s_copy[o * kCopyTokens + k_tok1];
+                const int t = copy_token(s_copy[o * kCopyTokens + k_tok1], k_tok1);
                 my_row[k_pos1] = k_slot1 < nsel ? t : kTokPad;
             }
             wave_sync();
@@ -871,7 +877,9 @@ __attribute__((amdgpu_waves_per_eu((kFuse != 0 && H <= 128) ? 8 : 1))) void toke
     const uint16_t* win_b = reinterpret_cast<const uint16_t*>(my_win + kSegPerEgo);
     auto ego_a = [&](int p) { return e_begin + 2 * p; };
     auto ego_b = [&](int p) { return (e_begin + 2 * p + 1) < e_end ? e_begin + 2 * p + 1 : e_begin + 2 * p; };
-    auto uniform_pos = [&](int e) { return (uint32_t)__builtin_amdgcn_readfirstlane((int)s_pos[e]); };
+    auto uniform_pos = [&](int e) {
+        return (uint32_t)__builtin_amdgcn_readfirstlane((int)s_rec[e * kRecWords]);
+    };
     uint4 ga, gb;
     uint32_t fa, fb;
     auto stage = [&](int p) {
