@@ -785,7 +785,9 @@ __global__ __launch_bounds__(256) void copy_actions_kernel(uint8_t* __restrict__
 // before its range itself (16 bytes per load, from the L2), so workgroups
 // never wait for each other, scans its own range through LDS and writes the
 // prefixes with consecutive lanes on consecutive values.
-constexpr int kScanThreads = 256;
+constexpr int kScanThreads = 1024;  // at 4096 values per workgroup, a thread's share of the
+                                    // values before its chunk (<= 8 x 16 bytes per 128 K
+                                    // values) is one batch of loads
 constexpr int kScanPer = 4;                             // values per thread
 constexpr int kScanChunk = kScanThreads * kScanPer;     // values per workgroup
 
@@ -803,6 +805,12 @@ __global__ __launch_bounds__(kScanThreads) void goal_changed_scan_kernel(jl_sim_
     const int64_t N = (int64_t)s.n_envs * s.n_agents;
     const int64_t c0 = (int64_t)blockIdx.x * kScanChunk;
     const uint8_t* f = s.goal_changed;
+    // this thread's kScanPer consecutive values, loaded first so that they
+    // travel with the loads of the values before the chunk
+    const int64_t e0 = c0 + (int64_t)tid * kScanPer;
+    uint32_t v[kScanPer];
+#pragma unroll
+    for (int j = 0; j < kScanPer; ++j) v[j] = e0 + j < N ? f[e0 + j] : 0u;
     // the changed-row buffer is cleared before the energy pass packs into it
     // (the reference zero-fills it, grid_world_simulator.cpp:724-733)
     if (changed) {
@@ -817,6 +825,7 @@ __global__ __launch_bounds__(kScanThreads) void goal_changed_scan_kernel(jl_sim_
     const bool vec = (reinterpret_cast<uintptr_t>(f) & 15u) == 0;
     const int64_t words = vec ? c0 / 16 : 0;
     uint64_t before = 0;
+#pragma unroll 8
     for (int64_t k = tid; k < words; k += kScanThreads) {
         const uint4 w = reinterpret_cast<const uint4*>(f)[k];
         before += byte_sum(w.x) + byte_sum(w.y) + byte_sum(w.z) + byte_sum(w.w);
@@ -828,11 +837,7 @@ __global__ __launch_bounds__(kScanThreads) void goal_changed_scan_kernel(jl_sim_
     int64_t base = 0;
     for (int k = 0; k < kScanThreads / kWave; ++k) base += s_wave[k];
     __syncthreads();
-    // this thread's kScanPer consecutive values, scanned across the workgroup
-    const int64_t e0 = c0 + (int64_t)tid * kScanPer;
-    uint32_t v[kScanPer];
-#pragma unroll
-    for (int j = 0; j < kScanPer; ++j) v[j] = e0 + j < N ? f[e0 + j] : 0u;
+    // this thread's values, scanned across the workgroup
     uint32_t local = 0;
 #pragma unroll
     for (int j = 0; j < kScanPer; ++j) local += v[j];
