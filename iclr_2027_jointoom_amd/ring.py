@@ -37,6 +37,13 @@ Device side (this module's own design):
 * the consumer orders its stream after ``dma_event``, copies the stage into
   ``stage_batch_buffer`` on the device, validates env/agent order and
   releases the stage so producers can reuse the slot.
+
+Compact records (no reference counterpart; ``record_format="compact"`` of the
+pipelines): ``CompactRingBuffer`` carries 5 bytes per agent-step (int16
+position, uint8 action) plus per-env episode starts and the starting envs'
+goals; ``CompactDMAWorker`` uploads a stage and expands it into the 8- or
+13-column rows on the device in one native call (``jl_ring_upload_compact``),
+so the consumer reads the same rows as from the row ring.
 """
 from __future__ import annotations
 
