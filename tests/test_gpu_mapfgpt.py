@@ -431,7 +431,8 @@ def _rows_case(rng, grids, A, goals=None):
     return rows
 
 
-@pytest.mark.parametrize("W,H,A", [(64, 64, 40), (36, 32, 40), (128, 32, 96), (64, 64, 1024)])
+@pytest.mark.parametrize("W,H,A", [(64, 64, 40), (36, 32, 40), (128, 32, 96), (64, 64, 1024), (32, 128, 77),
+                                   (16, 256, 65)])
 def test_single_launch_build_matches_oracle_and_two_launch_build(oracle, W, H, A):
     """Maps of at most 4096 cells with at most 1024 agents per env build in
     one launch: unpack, the env's field refreshes (with the greedy marks of
