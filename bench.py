@@ -60,7 +60,7 @@ TRAFFIC_FILE = ROOT / "profiles" / "tokens_kernel_pmc_1024x128_64.txt"
 
 MAGAT_TRAFFIC_FILE = ROOT / "profiles" / "magat_nodes_pmc_512x256_64.txt"
 
-# Algorithmic bytes per agent (derivation in DESIGN.md).
+# Algorithmic bytes per agent: the compulsory reads and writes of each operation.
 B_TOKEN_KERNEL = 8 + 10 + 242 + 1024 + 1  # pos+goal, history, 11x11 u16 window, tokens, mask
 # The whole build as one launch (maps of at most 4096 cells): split-array
 # position and goal, goal-cache read (written only on a change), history,
