@@ -498,3 +498,48 @@ def test_single_launch_build_matches_oracle_and_two_launch_build(oracle, W, H, A
     assert diag_seen[1] > 0 and diag_seen[2] > 0 and diag_seen[3] > 0
     greedy = ob.tokens[:, 121 + 9]
     assert len(np.unique(greedy)) > 4
+
+
+def test_c2_full_size_build(oracle):
+    """BASELINE C2/C3 shape (1024 envs x 128 agents, 64x64, p = 0.2) through
+    three resident steps: the single-launch and the two-launch builds agree
+    bit for bit on every output, three sampled envs equal the oracle, and
+    every ego's own slot and window centre hold their closed-form tokens
+    (relative position 0 -> 20, d - d = 0 -> 20, all egos reachable here)."""
+    from iclr_2027_jointoom_amd import profile
+    from iclr_2027_jointoom_amd.synthetic import make_batch
+
+    E, W, A = 1024, 64, 128
+    grids, starts, goals = make_batch(2027, E, W, W, A)
+    ext = profile(W, W)
+    g = torch.from_numpy(grids.astype(np.int32)).cuda()
+    one = ext.MapfGPTObservationBuilder(g, A)
+    two = ext.MapfGPTObservationBuilder(g, A)
+    two._desc.build_scratch = None
+    assert one.single_launch and not two.single_launch
+    sim = ext.GridWorldSimulator(g, A, 0, E * W * W, 7, "standard_mapf", 512)
+    sim.load_state(torch.from_numpy(starts).cuda(), torch.from_numpy(goals).cuda(),
+                   torch.zeros((E, A), dtype=torch.uint8, device="cuda"),
+                   torch.zeros(E, dtype=torch.int32, device="cuda"))
+    sample = [0, 511, 1023]
+    ob = oracle.OracleMapfGPT(grids[sample], A)
+    gen = torch.Generator(device="cuda").manual_seed(5)
+    for t in range(3):
+        state = (sim.cur_x, sim.cur_y, sim.goal_x, sim.goal_y)
+        one.build_tokens_from_state(*state)
+        two.build_tokens_from_state(*state)
+        ob.build_state(*(v.cpu().numpy()[sample] for v in state))
+        torch.cuda.synchronize()
+        for name in ("tokens", "active_mask", "cost_to_go", "state_packed", "labels", "goal_cache", "diagnostics"):
+            assert torch.equal(getattr(one, name), getattr(two, name)), (t, name)
+        assert one.diagnostics.cpu().tolist() == [0, 0, 0, 0]
+        tok = one.tokens.view(E, A, 256)
+        assert np.array_equal(tok[sample].cpu().numpy().reshape(-1, 256), ob.tokens), t
+        assert bool((tok[:, :, 121] == 20).all() and (tok[:, :, 122] == 20).all()), t
+        assert bool((tok[:, :, 60] == 20).all()), t
+        acts = torch.randint(0, 5, (E, A), dtype=torch.uint8, device="cuda", generator=gen)
+        one.append_actions(acts)
+        two.append_actions(acts)
+        ob.append(acts.cpu().numpy()[sample])
+        sim.update_actions(acts)
+        sim.step_sim_only()
