@@ -415,3 +415,66 @@ def test_more_than_256_agents():
     torch.cuda.synchronize()
     assert torch.equal(sim.pyg_pos.cpu(), st[:, 2:4].to(torch.float32).cpu())
     assert sim.pyg_num_edges.item() > 0
+
+
+def test_c4_full_size_stateful(oracle):
+    """BASELINE C4 shape (512 envs x 256 agents, 64x64, p = 0.3) through three
+    stateful steps: node features, edge counts and edges of three sampled envs
+    equal the oracle's, and over the whole batch the edge count is the sum of
+    the counts, the prefix is their exclusive scan, edges are ordered by
+    (source, target), stay within squared radius 49 inside one env, and their
+    attributes are the position differences."""
+    from iclr_2027_jointoom_amd.synthetic import make_batch, random_actions
+
+    E, W, A = 512, 64, 256
+    grids, starts, goals = make_batch(78, E, W, W, A, density=0.3)
+    ext = ext_for(W, W)
+    sim = ext.GridWorldSimulator(torch.from_numpy(grids.astype(np.int32)).cuda(), A, 0, E * W * W, 5,
+                                 "standard_mapf", 256)
+    sim.load_state(torch.from_numpy(starts).cuda(), torch.from_numpy(goals).cuda(),
+                   torch.zeros((E, A), dtype=torch.uint8, device="cuda"),
+                   torch.zeros(E, dtype=torch.int32, device="cuda"))
+    sample = [0, 255, 511]
+    acts = random_actions(np.random.default_rng(4), 3, E, A)
+    for s in range(3):
+        sim.update_actions(torch.from_numpy(acts[s]).cuda())
+        sim.step_sim_only()
+        sim.update_derived_state()
+        sim.build_magat_plus_nodes()
+        sim.finalize_magat_plus_graph()
+        torch.cuda.synchronize()
+        rows = sim.state_packed.cpu().numpy().reshape(E, A, 8)
+        sub = rows[sample].copy()
+        sub[:, :, 0] = np.arange(len(sample))[:, None]
+        sub = sub.reshape(-1, 8)
+        reset = sub.copy()
+        reset[:, 7] = 1
+        m = _oracle_stateless(oracle, grids[sample], reset, sub)
+        k = len(sample)
+        assert np.array_equal(sim.pyg_x.view(E, A, -1)[sample].cpu().numpy(), m.pyg_x.reshape(k, A, -1)), s
+        counts = sim.memory_tensors["edge_counts"].view(E, A)
+        assert np.array_equal(counts[sample].cpu().numpy(), m.edge_counts.reshape(k, A)), s
+        ei = sim.pyg_edge_index
+        ea = sim.pyg_edge_attr
+        src_env = ei[0] // A
+        m_ei, m_ea = m.valid_edges()
+        for j, e in enumerate(sample):
+            sel = src_env == e
+            got = (ei[:, sel] - e * A + j * A).cpu().numpy()
+            want_sel = (m_ei[0] // A) == j
+            assert np.array_equal(got, m_ei[:, want_sel]), (s, e)
+            assert np.array_equal(ea[sel].cpu().numpy(), m_ea[want_sel]), (s, e)
+        # whole-batch properties
+        flat = counts.reshape(-1).long()
+        n = int(sim.pyg_num_edges.item())
+        assert n == int(flat.sum().item()) == ei.shape[1]
+        prefix = sim.memory_tensors["pyg_edge_prefix"]
+        assert torch.equal(prefix[1:], flat.cumsum(0)) and int(prefix[0].item()) == 0
+        key = ei[0] * (E * A) + ei[1]
+        assert bool((key[1:] > key[:-1]).all())
+        assert bool((ei[0] // A == ei[1] // A).all()) and bool((ei[0] != ei[1]).all())
+        pos = sim.pyg_pos
+        d = pos[ei[0]] - pos[ei[1]]
+        assert torch.equal(ea[:, :2], d)
+        assert torch.equal(ea[:, 2], d.abs().sum(1))
+        assert bool(((d * d).sum(1) <= 49).all())
