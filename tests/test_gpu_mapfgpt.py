@@ -543,3 +543,41 @@ def test_c2_full_size_build(oracle):
         ob.append(acts.cpu().numpy()[sample])
         sim.update_actions(acts)
         sim.step_sim_only()
+
+
+def test_c5_full_size_build(oracle):
+    """BASELINE C5 shape (256 envs x 1024 agents, 256x256 warehouses; hash
+    cell -> agent map, two 512-ego workgroups per env) through two resident
+    steps: two sampled envs equal the oracle, and every ego's own slot and
+    window centre hold their closed-form tokens."""
+    from iclr_2027_jointoom_amd import profile
+    from iclr_2027_jointoom_amd.synthetic import make_batch
+
+    E, W, A = 256, 256, 1024
+    grids, starts, goals = make_batch(2028, E, W, W, A, kind="warehouse")
+    ext = profile(W, W)
+    g = torch.from_numpy(grids.astype(np.int32)).cuda()
+    b = ext.MapfGPTObservationBuilder(g, A)
+    assert not b.single_launch
+    sim = ext.GridWorldSimulator(g, A, 0, E * 1024, 7, "standard_mapf", 512)
+    sim.load_state(torch.from_numpy(starts).cuda(), torch.from_numpy(goals).cuda(),
+                   torch.zeros((E, A), dtype=torch.uint8, device="cuda"),
+                   torch.zeros(E, dtype=torch.int32, device="cuda"))
+    sample = [3, 250]
+    ob = oracle.OracleMapfGPT(grids[sample], A)
+    gen = torch.Generator(device="cuda").manual_seed(6)
+    for t in range(2):
+        state = (sim.cur_x, sim.cur_y, sim.goal_x, sim.goal_y)
+        b.build_tokens_from_state(*state)
+        ob.build_state(*(v.cpu().numpy()[sample] for v in state))
+        torch.cuda.synchronize()
+        assert b.diagnostics.cpu().tolist() == [0, 0, 0, 0]
+        tok = b.tokens.view(E, A, 256)
+        assert np.array_equal(tok[sample].cpu().numpy().reshape(-1, 256), ob.tokens), t
+        assert bool((tok[:, :, 121] == 20).all() and (tok[:, :, 122] == 20).all()), t
+        assert bool((tok[:, :, 60] == 20).all()), t
+        acts = torch.randint(0, 5, (E, A), dtype=torch.uint8, device="cuda", generator=gen)
+        b.append_actions(acts)
+        ob.append(acts.cpu().numpy()[sample])
+        sim.update_actions(acts)
+        sim.step_sim_only()
