@@ -388,10 +388,10 @@ __global__ __launch_bounds__(kWave* kWaves) void unpack_bfs_kernel(
 // agent scatter and its diagnostics (:328-347).
 //
 // Phase 1 (whole workgroup, one env): each agent's record (position word,
-// kNoAgent off the map, and goal word), the raw values of its six
-// ego-independent tokens (five history values and the greedy mask, :437-456;
-// 16 bits each, turned into tokens where a row copies them) and a cell ->
-// agent map live in LDS.
+// kNoAgent off the map, and goal word), its six ego-independent tokens (five
+// history tokens and the greedy token, :437-456; on hash maps their 16-bit raw
+// values, turned into tokens where a row copies them, to keep the LDS of 1024
+// agents under 80 KB) and a cell -> agent map live in LDS.
 // The map is dense (one int32 per cell of the map grown by a kRadius border
 // of empty cells, so a window probe needs no bounds test) while it fits, an
 // occupancy bitmap + hash beyond.
@@ -427,8 +427,9 @@ constexpr int kSegPerEgo = kDiam * 3;
 constexpr int kRegionCols = 24;            // cells per region row (3 tile columns)
 constexpr int kSlotStride = 16;            // per-wave top-13 slot array (words)
 constexpr int kRecWords = 2;               // per-agent record: position word, goal word
-constexpr int kCopyTokens = 6;             // per-agent tokens independent of the ego, kept
-                                           // as uint16 raw values: 5 history values, greedy mask
+constexpr int kCopyTokens = 6;             // per-agent tokens independent of the ego: int32
+                                           // tokens on dense maps, uint16 raw values (5 history
+                                           // values, greedy mask) on hash maps, where LDS is short
 constexpr int kCoordLanes = kVisible * 4;  // lanes producing the 52 coordinate tokens
 constexpr int kCopyItems = kVisible * kCopyTokens;  // 78 copied tokens per row
 // per-wavefront LDS: two egos' windows, the token row, the slot array
@@ -476,7 +477,7 @@ __host__ __device__ inline TokLayout tok_layout(int A, int W, int H, bool fused 
     L.rec_off = off;
     off = align16(off + (size_t)A * kRecWords * 4);
     L.copy_off = off;
-    off = align16(off + (size_t)A * kCopyTokens * 2);
+    off = align16(off + (size_t)A * kCopyTokens * (L.dense ? 4 : 2));
     L.wave_off = off;
     off = align16(off + (size_t)kTokWaves * kWaveBytes);
     L.diag_off = off;
@@ -574,6 +575,7 @@ __attribute__((amdgpu_waves_per_eu((kFuse != 0 && H <= 128) ? 8 : 1))) void toke
     uint32_t* s_vals = reinterpret_cast<uint32_t*>(smem + L.vals_off);
     uint32_t* s_rec = reinterpret_cast<uint32_t*>(smem + L.rec_off);    // kRecWords per agent
     uint16_t* s_copy = reinterpret_cast<uint16_t*>(smem + L.copy_off);  // kCopyTokens per agent
+    int* s_copy_tok = reinterpret_cast<int*>(smem + L.copy_off);          // the same, dense maps
     int* s_diag = reinterpret_cast<int*>(smem + L.diag_off);
     uint8_t* my_lds = smem + L.wave_off + (size_t)wave * kWaveBytes;
     uint4* my_win = reinterpret_cast<uint4*>(my_lds);                  // [2 egos][11 rows][3 segments]
@@ -688,8 +690,16 @@ __attribute__((amdgpu_waves_per_eu((kFuse != 0 && H <= 128) ? 8 : 1))) void toke
         // the greedy mask (:452-456) last, below
         const uint16_t* h = b.histories + g * 5;
         uint16_t* cp = s_copy + a * kCopyTokens;
+        int* cpt = s_copy_tok + a * kCopyTokens;
 #pragma unroll
-        for (int k = 0; k < 5; ++k) cp[k] = kFuse ? (uint16_t)f_hist[k] : h[k];
+        for (int k = 0; k < 5; ++k) {
+            const uint16_t v = kFuse ? (uint16_t)f_hist[k] : h[k];
+            if (kDense) {
+                cpt[k] = copy_token(v, k);
+            } else {
+                cp[k] = v;
+            }
+        }
         d_over += (int)(info >> kInfoOverflowShift);
         d_row += (info & kInfoBadRow) ? 1 : 0;
         d_bad += (info & kInfoBadGoal) ? 1 : 0;
@@ -714,7 +724,11 @@ __attribute__((amdgpu_waves_per_eu((kFuse != 0 && H <= 128) ? 8 : 1))) void toke
         if (kFuse && (st.w >> 16) == 0 && valid)
             greedy = f_center != kUnreachable ? f_center >> 12
                                               : kept_greedy<H, false>(b, g, (int)px, (int)py);
-        cp[5] = (uint16_t)greedy;
+        if (kDense) {
+            cpt[5] = copy_token(greedy, 5);
+        } else {
+            cp[5] = (uint16_t)greedy;
+        }
     }
     if (part != 0) d_over = d_row = d_dup = d_bad = 0;  // the env's counts come from its first slice
     if (d_over) atomicAdd(&s_diag[0], d_over);
@@ -848,12 +862,14 @@ __attribute__((amdgpu_waves_per_eu((kFuse != 0 && H <= 128) ? 8 : 1))) void toke
             }
             {
                 const uint32_t o = my_slots[k_slot0];
-                const int t = copy_token(s_copy[o * kCopyTokens + k_tok0], k_tok0);
+                const int t = kDense ? s_copy_tok[o * kCopyTokens + k_tok0]
+                                     : copy_token(s_copy[o * kCopyTokens + k_tok0], k_tok0);
                 my_row[k_pos0] = k_slot0 < nsel ? t : kTokPad;
             }
             if (lane + kWave < kCopyItems) {
                 const uint32_t o = my_slots[k_slot1];
-                const int t = copy_token(s_copy[o * kCopyTokens + k_tok1], k_tok1);
+                const int t = kDense ? s_copy_tok[o * kCopyTokens + k_tok1]
+                                     : copy_token(s_copy[o * kCopyTokens + k_tok1], k_tok1);
                 my_row[k_pos1] = k_slot1 < nsel ? t : kTokPad;
             }
             wave_sync();
