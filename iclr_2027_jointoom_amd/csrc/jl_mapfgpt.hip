@@ -410,9 +410,10 @@ __global__ __launch_bounds__(kWave* kWaves) void unpack_bfs_kernel(
 // ---------------------------------------------------------------------------
 constexpr int kTokThreads = 1024;
 // Bound of a single-launch workgroup's wait for its launch's cleared totals
-// (each try sleeps ~128 cycles; workgroup 0 clears them at its start, so the
-// bound is never reached by a healthy launch).
-constexpr int kDiagSpinLimit = 1 << 20;
+// (each try is a device-scope load and a ~128-cycle sleep, about a
+// microsecond, so the bound is tens of milliseconds; workgroup 0, dispatched
+// first, clears them at its start, so a healthy launch never reaches it).
+constexpr int kDiagSpinLimit = 1 << 16;
 constexpr int kTokWaves = kTokThreads / kWave;
 // Egos per workgroup of a two-launch build: every workgroup stages its whole
 // env, so a workgroup takes the whole env (in steps of 128) up to 512 egos;
