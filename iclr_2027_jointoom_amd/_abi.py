@@ -13,6 +13,7 @@ from pathlib import Path
 
 _PKG_DIR = Path(__file__).resolve().parent
 LIBRARY_PATH = _PKG_DIR / "libjointloom.so"
+BUILD_SCRATCH_WORDS = 2080  # JL_BUILD_SCRATCH_WORDS of jointloom.h
 
 c_void_p = ctypes.c_void_p
 c_int32 = ctypes.c_int32

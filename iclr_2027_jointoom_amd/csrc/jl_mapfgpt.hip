@@ -25,7 +25,6 @@
 // (mapf_gpt_builder.cpp:108-110, mapf_gpt_cuda.cu:544-610) with the
 // top-13 search done serially by one lane per ego (:395-496) and every
 // window row read from the row-major field (one 128-byte line per row).
-#include <atomic>
 
 #include "jl_bfs.h"
 #include "jl_common.h"
@@ -520,13 +519,44 @@ __device__ __forceinline__ int copy_token(uint32_t v, int k) {
     return k == kCopyTokens - 1 ? kTokGreedy + (int)v : (v == 5 ? kTokEmptyAction : kTokWait + (int)v);
 }
 
+// build_scratch of the single-launch build (JL_BUILD_SCRATCH_WORDS int32):
+// at byte 0 the uint64 number of the last launch whose diagnostics were
+// cleared; from byte 128, kArriveClasses uint64 arrival counters, one
+// 128-byte line each.  Workgroup g belongs to class g % kArriveClasses and
+// adds 1 to its class's counter once, so every launch (n_envs workgroups,
+// the builder's fixed env count) adds the same per-class count.
+constexpr int kArriveClasses = 64;
+constexpr int kArriveBaseWords = 32;
+constexpr int kArriveStrideWords = 32;
+static_assert(kArriveBaseWords + kArriveClasses * kArriveStrideWords == JL_BUILD_SCRATCH_WORDS,
+              "build_scratch layout");
+
+__device__ __forceinline__ unsigned long long* arrival_counter(const jl_mapfgpt_t& b) {
+    return reinterpret_cast<unsigned long long*>(
+        b.build_scratch + kArriveBaseWords + (blockIdx.x % kArriveClasses) * kArriveStrideWords);
+}
+
+// The workgroup's arrival, returning the number of this launch on this
+// builder (1, 2, ...), the same in every workgroup: no workgroup of an
+// earlier launch is still running, so the counter's value before the add
+// is (launches so far) x (class count) plus the fewer than one class count
+// of this launch's arrivals that came first.  Derived on the device, it
+// stays right in builds captured into a graph and replayed.  Called once
+// per workgroup, by one lane.
+__device__ __forceinline__ unsigned long long single_launch_number(const jl_mapfgpt_t& b) {
+    const unsigned cls = blockIdx.x % kArriveClasses;
+    const unsigned long long per = (gridDim.x - 1 - cls) / kArriveClasses + 1;
+    return __hip_atomic_fetch_add(arrival_counter(b), 1ull, __ATOMIC_RELAXED,
+                                  __HIP_MEMORY_SCOPE_AGENT) / per + 1;
+}
+
 // Diagnostics of a single-launch build.  No earlier launch of the build
 // cleared them: workgroup 0 clears them at its start and then stores the
-// launch's number (strictly increasing over the library's single launches)
-// in build_scratch; a workgroup with counts to add (d, its env's sums) waits
-// (bounded) for that number, then adds.  Totals and the number move only
-// through device-scope atomics, performed where every XCD sees them.
-// Workgroups without counts, the usual case, touch neither.
+// launch's number (single_launch_number) in build_scratch; a workgroup with
+// counts to add (d, its env's sums) waits (bounded) for that number, then
+// adds.  Totals, the number and the arrival counters move only through
+// device-scope atomics, performed where every XCD sees them.  Workgroups
+// without counts, the usual case, touch neither.
 __device__ __forceinline__ void publish_single_diagnostics(const jl_mapfgpt_t& b, const int* d,
                                                            unsigned long long launch) {
     if ((d[0] | d[1] | d[2] | d[3]) == 0) return;
@@ -555,8 +585,9 @@ __global__ __launch_bounds__(kTokThreads)
 __attribute__((amdgpu_waves_per_eu((kFuse != 0 && H <= 128) ? 8 : 1))) void tokens_kernel(
     jl_mapfgpt_t b, const int16_t* __restrict__ raw_rows, const int16_t* __restrict__ cur_x,
     const int16_t* __restrict__ cur_y, const int16_t* __restrict__ goal_x,
-    const int16_t* __restrict__ goal_y, unsigned long long launch) {
+    const int16_t* __restrict__ goal_y) {
     extern __shared__ __align__(16) uint8_t smem[];
+    unsigned long long launch = 0;  // single launch, lane 0: this launch's number
     const int A = b.n_agents, W = b.map_w;
     // workgroup = (env, slice of egos); every slice stages the whole env
     const int slice = kFuse ? A : ego_slice(A);  // a single launch: one workgroup per env
@@ -600,8 +631,9 @@ __attribute__((amdgpu_waves_per_eu((kFuse != 0 && H <= 128) ? 8 : 1))) void toke
         int* s_nlist = reinterpret_cast<int*>(smem + L.nlist_off);
         if (tid == 0) *s_nlist = 0;
         if (blockIdx.x == 0 && tid == 0) {
-            // this launch's diagnostics start from zero, then `launch` is
-            // published (see the end of phase 1)
+            // this launch's diagnostics start from zero, then its number is
+            // published (see the end of phase 2)
+            launch = single_launch_number(b);
             int z = 0;
             for (int k = 0; k < 4; ++k) z |= atomicExch(b.diagnostics + k, 0);
             asm volatile("" ::"v"(z));  // cleared before the launch is published
@@ -738,7 +770,10 @@ __attribute__((amdgpu_waves_per_eu((kFuse != 0 && H <= 128) ? 8 : 1))) void toke
     if (d_bad) atomicAdd(&s_diag[3], d_bad);
     lds_barrier();
     if (kFuse) {
-        // published after phase 2 (publish_single_diagnostics)
+        // published after phase 2 (publish_single_diagnostics); the launch
+        // number, needed only then, is taken here, where its round trip
+        // overlaps the first window loads
+        if (tid == 0 && blockIdx.x != 0) launch = single_launch_number(b);
     } else if (tid < 4 && s_diag[tid]) {
         // relaxed device-scope adds: the build's totals are complete when
         // the kernel is, and pass 1 of the build cleared them
@@ -1103,23 +1138,18 @@ bool single_launch(const jl_mapfgpt_t* b) {
     return L.dense && L.total <= 160 * 1024;
 }
 
-// Numbers of single launches, strictly increasing over every builder of the
-// process (a builder's build_scratch only ever sees larger ones).
-std::atomic<unsigned long long> g_single_launches{0};
-
 template <int H, int kFuse>
 int launch_single(const jl_mapfgpt_t* b, const int16_t* rows, const int16_t* cx, const int16_t* cy,
                   const int16_t* gx, const int16_t* gy, hipStream_t stream) {
     const TokLayout L = tok_layout(b->n_agents, b->map_w, H, true);
-    const unsigned long long launch = ++g_single_launches;
     if (b->map_w <= 64) {
         hipLaunchKernelGGL((tokens_kernel<H, true, kFuse, 1>), dim3(b->n_envs), dim3(kTokThreads),
-                           L.total, stream, *b, rows, cx, cy, gx, gy, launch);
+                           L.total, stream, *b, rows, cx, cy, gx, gy);
     } else {
         // W > 64 with W * H <= kMarkedCells: H == 32 only
         if constexpr (H == 32) {
             hipLaunchKernelGGL((tokens_kernel<H, true, kFuse, 2>), dim3(b->n_envs), dim3(kTokThreads),
-                               L.total, stream, *b, rows, cx, cy, gx, gy, launch);
+                               L.total, stream, *b, rows, cx, cy, gx, gy);
         } else {
             return JL_ERR_PROFILE;
         }
@@ -1135,12 +1165,7 @@ int build(const jl_mapfgpt_t* b, const int16_t* rows, const int16_t* cx, const i
     const int W = b->map_w;
     const TokLayout L = tok_layout(b->n_agents, W, b->map_h);
     if (L.total > 160 * 1024) return JL_ERR_PROFILE;
-    // a build captured into a graph keeps two launches: a replay repeats the
-    // captured launch number, which then orders nothing
-    hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
-    rc = status(hipStreamIsCapturing(stream, &capture));
-    if (rc) return rc;
-    if (single_launch(b) && capture == hipStreamCaptureStatusNone) {
+    if (single_launch(b)) {
         JL_DISPATCH_H(b->map_h, {
             if (b->token_events[0]) {
                 rc = status(hipEventRecord((hipEvent_t)b->token_events[0], stream));
@@ -1173,10 +1198,10 @@ int build(const jl_mapfgpt_t* b, const int16_t* rows, const int16_t* cx, const i
         const int16_t* none = nullptr;
         if (L.dense) {
             hipLaunchKernelGGL((tokens_kernel<H, true, 0, 1>), grid2, dim3(kTokThreads), L.total, stream,
-                               *b, none, none, none, none, none, 0ull);
+                               *b, none, none, none, none, none);
         } else {
             hipLaunchKernelGGL((tokens_kernel<H, false, 0, 1>), grid2, dim3(kTokThreads), L.total,
-                               stream, *b, none, none, none, none, none, 0ull);
+                               stream, *b, none, none, none, none, none);
         }
         rc = launch_status();
         if (rc) return rc;

@@ -22,7 +22,7 @@ import types
 
 import torch
 
-from ._abi import MagatDesc, MapfGPTDesc, SimDesc, check, load_library
+from ._abi import BUILD_SCRATCH_WORDS, MagatDesc, MapfGPTDesc, SimDesc, check, load_library
 
 TASK_LIFELONG = 0
 TASK_STANDARD_MAPF = 1
@@ -277,8 +277,11 @@ class MapfGPTObservationBuilder(_Base):
                 (E, n_agents, (W + 7) // 8 * 8 * H), -1, dtype=torch.int16, device=device
             )
             # single-launch builds: number of the last launch whose diagnostics
-            # were cleared (uint64); zero at construction
-            self._build_scratch = torch.zeros((8,), dtype=torch.int32, device=device)
+            # were cleared (uint64) and workgroup arrival counters; zero at
+            # construction
+            self._build_scratch = torch.zeros(
+                (BUILD_SCRATCH_WORDS,), dtype=torch.int32, device=device
+            )
         self._desc = MapfGPTDesc(
             n_envs=E,
             n_agents=n_agents,
@@ -322,10 +325,10 @@ class MapfGPTObservationBuilder(_Base):
 
     @property
     def single_launch(self) -> bool:
-        """True when an eager build runs as one launch (unpack, field
-        refreshes and tokens of an env in one workgroup): maps of at most 4096
-        cells and at most 1024 agents per env; builds captured into a graph
-        keep two launches.  No counterpart in the reference."""
+        """True when a build runs as one launch (unpack, field refreshes and
+        tokens of an env in one workgroup), eager or captured into a graph:
+        maps of at most 4096 cells and at most 1024 agents per env.  No
+        counterpart in the reference."""
         return bool(self._lib.jl_mapfgpt_single_launch(self._desc_ref))
 
     def _check_state(self, t: torch.Tensor, name: str) -> None:

@@ -34,6 +34,9 @@ extern "C" {
 
 typedef void* jl_stream_t; /* hipStream_t */
 
+/* int32 words of a MAPF-GPT builder's build_scratch (8448 bytes). */
+#define JL_BUILD_SCRATCH_WORDS 2080
+
 enum {
     JL_OK = 0,
     JL_ERR_ARG = -1,         /* null pointer, non-positive size, size overflow */
@@ -173,11 +176,14 @@ typedef struct jl_mapfgpt {
                                    cost_to_go in 8x8 tiles (one 128-byte line per tile); on
                                    maps of at most 4096 cells bits 12-15 of a reachable cell
                                    hold its greedy-move mask */
-    int32_t* build_scratch;     /* [8] workspace, zero at construction, 8-byte aligned: the
-                                   single-launch build of small maps keeps in [0..1] the
+    int32_t* build_scratch;     /* [JL_BUILD_SCRATCH_WORDS] workspace, zero at construction,
+                                   128-byte aligned, used with this builder's n_envs only:
+                                   the single-launch build of small maps keeps in it the
                                    uint64 number of the last launch whose diagnostics were
-                                   cleared, which orders the clearing before that launch's
-                                   adds.  NULL = two-launch builds only */
+                                   cleared and per-class workgroup arrival counters, from
+                                   which each launch derives its number on the device (so
+                                   builds captured into a graph keep one launch).  NULL =
+                                   two-launch builds only */
     void* token_events[2];      /* optional hipEvent_t pair recorded on the stream right
                                    before / after the token kernel (profiling); NULL = off */
 } jl_mapfgpt_t;
@@ -200,10 +206,10 @@ int jl_mapfgpt_build_state(const jl_mapfgpt_t* b, const int16_t* cur_x,
                            const int16_t* cur_y, const int16_t* goal_x,
                            const int16_t* goal_y, jl_stream_t stream);
 
-/* 1 when an eager build of this builder runs as one launch (maps of at most
+/* 1 when a build of this builder runs as one launch (maps of at most
  * 4096 cells, an env of at most 1024 agents, build_scratch set): unpack,
- * field refreshes and tokens of an env in one workgroup; 0 when it runs as
- * two or three launches (as do builds captured into a graph).  No
+ * field refreshes and tokens of an env in one workgroup, also when captured
+ * into a graph; 0 when it runs as two or three launches.  No
  * counterpart in the reference (a profiling query: the token_events pair
  * then brackets the whole build). */
 int jl_mapfgpt_single_launch(const jl_mapfgpt_t* b);

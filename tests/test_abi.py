@@ -82,7 +82,8 @@ def test_host_side_argument_checks_return_before_device_work(lib):
 
 
 def test_ctypes_structs_match_the_c_layout(tmp_path):
-    from iclr_2027_jointoom_amd._abi import MagatDesc, MapfGPTDesc, RecordsDesc, SimDesc, StageUploadDesc
+    from iclr_2027_jointoom_amd._abi import (BUILD_SCRATCH_WORDS, MagatDesc, MapfGPTDesc, RecordsDesc,
+                                             SimDesc, StageUploadDesc)
 
     structs = {"jl_sim_t": SimDesc, "jl_mapfgpt_t": MapfGPTDesc, "jl_magat_t": MagatDesc,
                "jl_records_t": RecordsDesc, "jl_stage_upload_t": StageUploadDesc}
@@ -91,6 +92,7 @@ def test_ctypes_structs_match_the_c_layout(tmp_path):
         lines.append(f'printf("{cname} size %zu\\n", sizeof({cname}));')
         for field, _ in py._fields_:
             lines.append(f'printf("{cname} {field} %zu\\n", offsetof({cname}, {field}));')
+    lines.append('printf("macro JL_BUILD_SCRATCH_WORDS %d\\n", JL_BUILD_SCRATCH_WORDS);')
     lines += ["return 0; }"]
     src = tmp_path / "layout.c"
     src.write_text("\n".join(lines))
@@ -98,6 +100,7 @@ def test_ctypes_structs_match_the_c_layout(tmp_path):
     subprocess.run(["gcc", "-std=c11", "-o", str(exe), str(src)], check=True)
     out = subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.split("\n")
     c = {(ln.split()[0], ln.split()[1]): int(ln.split()[2]) for ln in out if ln}
+    assert c[("macro", "JL_BUILD_SCRATCH_WORDS")] == BUILD_SCRATCH_WORDS
     for cname, py in structs.items():
         assert c[(cname, "size")] == ctypes.sizeof(py), cname
         for field, _ in py._fields_:

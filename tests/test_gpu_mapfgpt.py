@@ -483,10 +483,10 @@ def test_single_launch_build_matches_oracle_and_two_launch_build(oracle, W, H, A
         assert np.array_equal(one.state_packed.cpu().numpy(), ob.state_packed.view(np.int16)), it
         assert one.diagnostics.cpu().tolist() == ob.diagnostics.tolist(), it
         diag_seen += np.array(ob.diagnostics.tolist()) != 0
-        # the number of this launch, published after the clearing (uint64)
-        published = one._build_scratch.cpu().view(torch.int64)[0].item()
-        assert published > last_launch, it
-        last_launch = published
+        # the number of this launch on this builder, derived on the device and
+        # published after the clearing (uint64)
+        assert _published_launch(one) == last_launch + 1, it
+        last_launch += 1
         # the resident builds of the same states agree as well
         st = one.state_packed.view(E, A, 8)
         if it == 4:
@@ -498,6 +498,68 @@ def test_single_launch_build_matches_oracle_and_two_launch_build(oracle, W, H, A
     assert diag_seen[1] > 0 and diag_seen[2] > 0 and diag_seen[3] > 0
     greedy = ob.tokens[:, 121 + 9]
     assert len(np.unique(greedy)) > 4
+
+
+def _published_launch(builder) -> int:
+    return builder._build_scratch.cpu().view(torch.int64)[0].item()
+
+
+def test_single_launch_build_replayed_from_a_graph_matches_two_launch_build():
+    """A build captured into a graph keeps its single launch: every replay,
+    over rows that change between replays (rejected rows, shared cells,
+    positions off the map, a changed goal, resets), equals the eager
+    two-launch build on every output, diagnostics included, and publishes a
+    launch number one above the previous replay's.  Eager builds of the same
+    builder run between replays."""
+    from iclr_2027_jointoom_amd import profile
+
+    W, H, A, E = 64, 64, 40, 3
+    rng = np.random.default_rng(29)
+    grids = (rng.random((E, W, H)) < 0.3).astype(np.int32)
+    ext = profile(W, H)
+    g = torch.from_numpy(grids).cuda()
+    one = ext.MapfGPTObservationBuilder(g, A)
+    two = ext.MapfGPTObservationBuilder(g, A)
+    two._desc.build_scratch = None
+    assert one.single_launch and not two.single_launch
+    rows = _rows_case(rng, grids, A)
+    goals = rows[:, 4:6].copy()
+    static = torch.from_numpy(rows.astype(np.int16)).cuda()
+    one.build_tokens(static)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    stream = torch.cuda.Stream()  # default priority
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.graph(graph, stream=stream):
+        one.build_tokens(static)
+    torch.cuda.current_stream().wait_stream(stream)
+    torch.cuda.synchronize()
+    launch = _published_launch(one)
+    assert launch == 1
+    diag_seen = np.zeros(4, np.int64)
+    for it in range(6):
+        rows = _rows_case(rng, grids, A, goals)
+        rows[:, 7] = 1 if it in (0, 4) else 0
+        if it % 2:
+            rows[5, 0] = E + 1                     # rejected row (env out of range)
+            rows[7, 2:4] = rows[8, 2:4]            # two agents on one cell
+            rows[2 * A + 1, 2] = W + 3             # position off the map
+        if it == 3:
+            rows[9, 4:6] = rows[10, 4:6]           # a changed goal
+        static.copy_(torch.from_numpy(rows.astype(np.int16)))
+        if it == 2:
+            one.build_tokens(static)               # an eager build between replays
+            launch += 1
+        graph.replay()
+        launch += 1
+        two.build_tokens(static)
+        torch.cuda.synchronize()
+        for name in ("tokens", "labels", "active_mask", "cost_to_go", "state_packed", "histories",
+                     "goal_cache", "diagnostics"):
+            assert torch.equal(getattr(one, name), getattr(two, name)), (it, name)
+        assert _published_launch(one) == launch, it
+        diag_seen += one.diagnostics.cpu().numpy() != 0
+    assert diag_seen[1] > 0 and diag_seen[2] > 0 and diag_seen[3] > 0
 
 
 def test_c2_full_size_build(oracle):
