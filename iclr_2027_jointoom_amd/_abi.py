@@ -15,6 +15,12 @@ _PKG_DIR = Path(__file__).resolve().parent
 LIBRARY_PATH = _PKG_DIR / "libjointloom.so"
 BUILD_SCRATCH_WORDS = 2080  # JL_BUILD_SCRATCH_WORDS of jointloom.h
 
+
+def tiled_field_cells(map_w: int, map_h: int) -> int:
+    """uint16 cells of one tiled distance field (cost_tiles of jl_mapfgpt_t):
+    8x8 tiles over the map plus a one-tile border of unreachable cells."""
+    return ((map_w + 7) // 8 + 2) * (map_h // 8 + 2) * 64
+
 c_void_p = ctypes.c_void_p
 c_int32 = ctypes.c_int32
 c_int64 = ctypes.c_int64

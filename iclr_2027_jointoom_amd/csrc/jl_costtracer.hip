@@ -26,14 +26,6 @@ constexpr int kObsCells = kCostTokens;       // 121
 constexpr int kObsFloats = 2 * kObsCells;    // 242
 constexpr int kObsCentre = kRadius * kDiam + kRadius;  // 60
 
-__host__ __device__ inline size_t tiled_field_cells(int W, int H) { return (size_t)((W + 7) / 8) * 8 * H; }
-
-template <int H>
-__device__ __forceinline__ uint32_t tile_at(int x, int y) {
-    return ((uint32_t)(x >> 3) * (uint32_t)(H / 8) + (uint32_t)(y >> 3)) * 64u +
-           (uint32_t)((x & 7) * 8 + (y & 7));
-}
-
 // Wavefront max / min, wavefront-uniform result: DPP steps within quads,
 // half-rows and rows, then row 0 into row 1 and row 2 into row 3 (bcast15,
 // rows 1 and 3 written) and rows 0-1 into rows 2-3 (bcast31, rows 2 and 3
@@ -72,7 +64,7 @@ __global__ __launch_bounds__(256) void reward_goals_kernel(jl_sim_t s, const uin
     const int b0 = best[i];
     const int k = cursor[i];
     const int xc = x < W ? x : W - 1, yc = y < H ? y : H - 1;
-    const int d = (int)field_distance(tiles[(size_t)i * tiled_field_cells(W, H) + tile_at<H>(xc, yc)],
+    const int d = (int)field_distance(tiles[(size_t)i * tiled_cells(W, H) + tile_offset<H>(xc, yc)],
                                       field_mask(W, H));
     rewards[i] = d < b0 ? 0.1f : 0.0f;
     int bn = min(b0, d);
@@ -102,7 +94,7 @@ __device__ __forceinline__ void observe_agents(const jl_sim_t& s, const jl_mapfg
                                                int32_t* __restrict__ best, float* o, int i0,
                                                int nvalid, int lane) {
     const int W = s.map_w, A = s.n_agents;
-    const size_t tcells = tiled_field_cells(W, H);
+    const size_t tcells = tiled_cells(W, H);
     const uint32_t fmask = field_mask(W, H);
     const int words = W * H / 32;
     // lane k < nvalid fetches agent i0 + k's position, best and refresh flag
@@ -134,8 +126,8 @@ __device__ __forceinline__ void observe_agents(const jl_sim_t& s, const jl_mapfg
         const uint32_t* ocp = s.grid_ocp + (size_t)(i / A) * words;
         c0[k] = (uint32_t)(xa * H + ya);
         c1[k] = (uint32_t)(xb * H + yb);
-        raw0[k] = f[tile_at<H>(xa, ya)];  // marks stripped where the distance is taken
-        raw1[k] = f[tile_at<H>(xb, yb)];
+        raw0[k] = f[tile_offset<H>(xa, ya)];  // marks stripped where the distance is taken
+        raw1[k] = f[tile_offset<H>(xb, yb)];
         w0[k] = ocp[c0[k] >> 5];
         w1[k] = ocp[c1[k] >> 5];
     }

@@ -90,16 +90,6 @@ __device__ __forceinline__ uint32_t greedy_mask(Field f, int x, int y, int W) {
     return m;
 }
 
-// Tiled field: 8x8 tiles of uint16 (128 bytes, one cache line each), tiles
-// row-major with H/8 tiles per row, ceil(W/8) tile rows.
-__host__ __device__ inline size_t tiled_cells(int W, int H) { return (size_t)((W + 7) / 8) * 8 * H; }
-
-template <int H>
-__device__ __forceinline__ uint32_t tile_offset(int x, int y) {
-    return ((uint32_t)(x >> 3) * (uint32_t)(H / 8) + (uint32_t)(y >> 3)) * 64u +
-           (uint32_t)((x & 7) * 8 + (y & 7));
-}
-
 // One 8-cell tile row (x, y0 .. y0 + 7) of a field in LDS (row-major, H
 // columns, x < W), every reachable cell marked in bits 12-15 with its
 // greedy-move mask (greedy_mask's rule: a neighbour off the map or
@@ -259,17 +249,21 @@ __device__ uint32_t refresh_field(const jl_mapfgpt_t& b, size_t agent_index, uin
     const uint4* lds4 = reinterpret_cast<const uint4*>(s_dist);
     uint4* out = reinterpret_cast<uint4*>(b.cost_to_go + agent_index * (size_t)cells);
     for (int c = lane; c < cells / 8; c += kWave) out[c] = lds4[c];
+    // the map's tiles (the border ring keeps its unreachable cells)
     uint4* tout = reinterpret_cast<uint4*>(b.cost_tiles + agent_index * tcells);
-    for (int c = lane; c < (int)(tcells / 8); c += kWave) {
-        const int t = c >> 3, r = c & 7;  // tile, row inside the tile
-        const int x = (t / (H / 8)) * 8 + r, y0 = (t % (H / 8)) * 8;
+    const int map_tile_rows = (W + 7) / 8;
+    for (int c = lane; c < map_tile_rows * H; c += kWave) {
+        const int t = c >> 3, r = c & 7;  // map tile, row inside the tile
+        const int tr = t / (H / 8), tc = t - (t / (H / 8)) * (H / 8);
+        const int x = tr * 8 + r, y0 = tc * 8;
+        const int dst = ((tr + 1) * (H / 8 + 2) + tc + 1) * 8 + r;
         const bool in = x < W;  // rows past the map in the last tile row: unreachable
         uint4 v = kMarked ? marked_segment<H>(s_dist, W, in ? x : 0, y0) : lds4[((in ? x : 0) * H + y0) >> 3];
         v.x = in ? v.x : 0xFFFFFFFFu;
         v.y = in ? v.y : 0xFFFFFFFFu;
         v.z = in ? v.z : 0xFFFFFFFFu;
         v.w = in ? v.w : 0xFFFFFFFFu;
-        tout[c] = v;
+        tout[dst] = v;
     }
     wave_sync();  // the LDS field is rewritten by the next refresh
     return info;
@@ -445,20 +439,12 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 struct TokLayout {
     bool dense;
     int hash_slots;
-    int bfs_waves;  // single-launch build: wavefronts refreshing fields at once
-    size_t map_off, occ_off, keys_off, vals_off, rec_off, copy_off, wave_off, diag_off,
-        info_off, list_off, nlist_off, total;
+    size_t map_off, occ_off, keys_off, vals_off, rec_off, copy_off, wave_off, diag_off, total;
 };
 
 __host__ __device__ inline size_t align16(size_t v) { return (v + 15) & ~(size_t)15; }
 
-// fused: the single-launch build, whose refresh phase lays W*H uint16 LDS
-// fields, one per refreshing wavefront, over the token pass's area (filled
-// only after the refreshes) and keeps each agent's info word and the list of
-// agents to refresh beyond it.  As many wavefronts refresh as fields fit in
-// the larger of that area and 64 KB (at least 8 on these maps of at most
-// 4096 cells).
-__host__ __device__ inline TokLayout tok_layout(int A, int W, int H, bool fused = false) {
+__host__ __device__ inline TokLayout tok_layout(int A, int W, int H) {
     TokLayout L;
     const size_t cells = (size_t)W * H;
     L.dense = cells <= (size_t)kDenseCellLimit;
@@ -482,22 +468,6 @@ __host__ __device__ inline TokLayout tok_layout(int A, int W, int H, bool fused 
     off = align16(off + (size_t)kTokWaves * kWaveBytes);
     L.diag_off = off;
     off = align16(off + 4 * 4);
-    L.bfs_waves = 0;
-    L.info_off = L.list_off = L.nlist_off = off;
-    if (fused) {
-        const size_t field = cells * 2;
-        const size_t room = off > 65536 ? off : 65536;
-        const size_t w = room / field;
-        L.bfs_waves = (int)(w < (size_t)kTokWaves ? w : (size_t)kTokWaves);
-        const size_t fields = (size_t)L.bfs_waves * field;
-        off = align16(off > fields ? off : fields);
-        L.info_off = off;
-        off = align16(off + (size_t)A * 4);
-        L.list_off = off;
-        off = align16(off + (size_t)A * 16);
-        L.nlist_off = off;
-        off = align16(off + 4);
-    }
     L.total = off;
     return L;
 }
@@ -569,28 +539,14 @@ __device__ __forceinline__ void publish_single_diagnostics(const jl_mapfgpt_t& b
         if (d[k]) atomicAdd(b.diagnostics + k, d[k]);
 }
 
-// kFuse: 0 = the token pass of a two-launch build; 1 (raw rows) and 2
-// (resident split arrays) = the whole build in one launch (maps of at most
-// kMarkedCells cells, A <= kTokThreads, one workgroup per env), which first
-// unpacks thread t's agent t, then refreshes the env's changed fields with
-// L.bfs_waves wavefronts (BFS with R rows per lane), then runs phases 1-2.
-// A single launch's LDS (under 80 KB) allows two workgroups per CU, 8
-// wavefronts per SIMD, which its SGPRs must allow too: above 80 per
-// wavefront only one workgroup fits (56 vs 48 us per build of 1024 envs x
-// 128 agents on 64x64 maps), so the
-// compiler is held to 8 wavefronts per SIMD (a few SGPRs then live in VGPR
-// lanes).  Not for H = 256, where that bound would spill VGPRs to scratch.
-template <int H, bool kDense, int kFuse, int R>
-__global__ __launch_bounds__(kTokThreads)
-__attribute__((amdgpu_waves_per_eu((kFuse != 0 && H <= 128) ? 8 : 1))) void tokens_kernel(
-    jl_mapfgpt_t b, const int16_t* __restrict__ raw_rows, const int16_t* __restrict__ cur_x,
-    const int16_t* __restrict__ cur_y, const int16_t* __restrict__ goal_x,
-    const int16_t* __restrict__ goal_y) {
+// The token pass of a two-launch build (pass 1 has written the state rows and
+// agent info words).
+template <int H, bool kDense>
+__global__ __launch_bounds__(kTokThreads) void tokens_kernel(jl_mapfgpt_t b) {
     extern __shared__ __align__(16) uint8_t smem[];
-    unsigned long long launch = 0;  // single launch, lane 0: this launch's number
     const int A = b.n_agents, W = b.map_w;
     // workgroup = (env, slice of egos); every slice stages the whole env
-    const int slice = kFuse ? A : ego_slice(A);  // a single launch: one workgroup per env
+    const int slice = ego_slice(A);
     const int parts = (A + slice - 1) / slice;
     const int env = blockIdx.x / parts;
     const int part = blockIdx.x - env * parts;
@@ -599,7 +555,7 @@ __attribute__((amdgpu_waves_per_eu((kFuse != 0 && H <= 128) ? 8 : 1))) void toke
     const int tid = threadIdx.x;
     const int lane = tid & (kWave - 1);
     const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);  // uniform per wavefront
-    const TokLayout L = tok_layout(A, W, H, kFuse != 0);
+    const TokLayout L = tok_layout(A, W, H);
     constexpr int MH = H + 2 * kRadius;  // dense map columns
     uint32_t* s_map = reinterpret_cast<uint32_t*>(smem + L.map_off);
     uint32_t* s_occ = reinterpret_cast<uint32_t*>(smem + L.occ_off);
@@ -616,77 +572,6 @@ __attribute__((amdgpu_waves_per_eu((kFuse != 0 && H <= 128) ? 8 : 1))) void toke
     const uint32_t hmask = (uint32_t)L.hash_slots - 1;
     const size_t cells = (size_t)W * H;
     const uint32_t fmask = field_mask(W, H);  // distance bits of a tiled field value
-    uint32_t* s_info = reinterpret_cast<uint32_t*>(smem + L.info_off);  // single launch only
-
-    // ---- phase 0 (single launch): unpack, then the env's field refreshes -----
-    // Agent tid's state row, history and (kept field) the marked value of its
-    // own cell: the history load joins the unpack's, and the cell's is left
-    // in flight until the end of phase 1, so the env's dependent loads cost
-    // one round trip before phase 1 starts.
-    uint4 f_st = make_uint4(0u, 0u, 0u, 0u);
-    uint32_t f_hist[5] = {5u, 5u, 5u, 5u, 5u};
-    uint32_t f_center = kUnreachable;
-    if (kFuse) {
-        uint4* s_list = reinterpret_cast<uint4*>(smem + L.list_off);
-        int* s_nlist = reinterpret_cast<int*>(smem + L.nlist_off);
-        if (tid == 0) *s_nlist = 0;
-        if (blockIdx.x == 0 && tid == 0) {
-            // this launch's diagnostics start from zero, then its number is
-            // published (see the end of phase 2)
-            launch = single_launch_number(b);
-            int z = 0;
-            for (int k = 0; k < 4; ++k) z |= atomicExch(b.diagnostics + k, 0);
-            asm volatile("" ::"v"(z));  // cleared before the launch is published
-            atomicExch(reinterpret_cast<unsigned long long*>(b.build_scratch), launch);
-        }
-        bool reset = false;
-        if (tid < A) {
-            const int g = env * A + tid;
-            const uint16_t* h = b.histories + (size_t)g * 5;
-            if (kFuse == 2) {
-#pragma unroll
-                for (int k = 0; k < 5; ++k) f_hist[k] = h[k];
-            }
-            uint32_t info;
-            f_st = unpack_agent<kFuse == 1>(b, g, raw_rows, cur_x, cur_y, goal_x, goal_y, info);
-            if (kFuse == 1) {
-                // a raw row's history, or the kept one of a rejected row
-#pragma unroll
-                for (int k = 0; k < 5; ++k) f_hist[k] = h[k];
-            }
-            reset = (f_st.w >> 16) != 0;
-            const uint32_t px = f_st.y & 0xFFFFu, py = f_st.y >> 16;
-            if (!reset && px < (uint32_t)W && py < (uint32_t)H)
-                f_center = b.cost_tiles[(size_t)g * tiled_cells(W, H) + tile_offset<H>((int)px, (int)py)];
-            s_info[tid] = info;
-        }
-
-        lds_barrier();
-        if (reset) s_list[atomicAdd(s_nlist, 1)] = make_uint4((uint32_t)tid, f_st.x, f_st.y, f_st.z);
-        lds_barrier();
-        const int nlist = __builtin_amdgcn_readfirstlane(*s_nlist);
-        if (nlist > 0) {
-            if (wave < L.bfs_waves) {
-                uint16_t* s_dist = reinterpret_cast<uint16_t*>(smem) + (size_t)wave * cells;
-                for (int k = wave; k < nlist; k += L.bfs_waves) {
-                    const uint4 it = s_list[k];
-                    const uint32_t a = (uint32_t)__builtin_amdgcn_readfirstlane((int)it.x);
-                    const uint32_t sx = (uint32_t)__builtin_amdgcn_readfirstlane((int)it.y);
-                    const uint32_t sy = (uint32_t)__builtin_amdgcn_readfirstlane((int)it.z);
-                    const uint32_t sz = (uint32_t)__builtin_amdgcn_readfirstlane((int)it.w);
-                    const uint32_t bits = refresh_field<H, R, true>(
-                        b, (size_t)env * A + a, sx & 0xFFFFu, (int)(sz & 0xFFFFu), (int)(sz >> 16),
-                        (int)(sy & 0xFFFFu), (int)(sy >> 16), s_dist);
-                    if (lane == 0) s_info[a] |= bits;
-                }
-            }
-            // the refreshed fields are stored before any window load of this
-            // workgroup (its wavefronts share the CU's vector cache), and the
-            // LDS fields are free for phase 1
-            __syncthreads();
-        }
-    }
-
     // ---- phase 1 -----------------------------------------------------------
     if (kDense) {
         const int mcells = (W + 2 * kRadius) * MH;  // even: MH is
@@ -709,9 +594,8 @@ __attribute__((amdgpu_waves_per_eu((kFuse != 0 && H <= 128) ? 8 : 1))) void toke
     int d_over = 0, d_row = 0, d_dup = 0, d_bad = 0;
     for (int a = tid; a < A; a += kTokThreads) {
         const size_t g = (size_t)env * A + a;
-        // a single launch holds its agents' rows and info words already (A <= kTokThreads)
-        const uint4 st = kFuse ? f_st : *reinterpret_cast<const uint4*>(b.state_packed + g * 8);
-        const uint32_t info = kFuse ? s_info[a] : b.agent_info[g];
+        const uint4 st = *reinterpret_cast<const uint4*>(b.state_packed + g * 8);
+        const uint32_t info = b.agent_info[g];
         const uint32_t px = st.y & 0xFFFFu, py = st.y >> 16;
         const uint32_t gx = st.z & 0xFFFFu, gy = st.z >> 16;
         if (a >= e_begin && a < e_end) b.active_mask[g] = (px != gx || py != gy) ? 1 : 0;
@@ -726,7 +610,7 @@ __attribute__((amdgpu_waves_per_eu((kFuse != 0 && H <= 128) ? 8 : 1))) void toke
         int* cpt = s_copy_tok + a * kCopyTokens;
 #pragma unroll
         for (int k = 0; k < 5; ++k) {
-            const uint16_t v = kFuse ? (uint16_t)f_hist[k] : h[k];
+            const uint16_t v = h[k];
             if (kDense) {
                 cpt[k] = copy_token(v, k);
             } else {
@@ -751,12 +635,7 @@ __attribute__((amdgpu_waves_per_eu((kFuse != 0 && H <= 128) ? 8 : 1))) void toke
         } else {
             ++d_bad;  // position off the map (scatter, :336-339)
         }
-        // a single launch's kept fields: the mark of the agent's own cell,
-        // or the cross of five cells where that cell is unreachable
-        uint32_t greedy = info & kInfoGreedy;
-        if (kFuse && (st.w >> 16) == 0 && valid)
-            greedy = f_center != kUnreachable ? f_center >> 12
-                                              : kept_greedy<H, false>(b, g, (int)px, (int)py);
+        const uint32_t greedy = info & kInfoGreedy;
         if (kDense) {
             cpt[5] = copy_token(greedy, 5);
         } else {
@@ -769,12 +648,7 @@ __attribute__((amdgpu_waves_per_eu((kFuse != 0 && H <= 128) ? 8 : 1))) void toke
     if (d_dup) atomicAdd(&s_diag[2], d_dup);
     if (d_bad) atomicAdd(&s_diag[3], d_bad);
     lds_barrier();
-    if (kFuse) {
-        // published after phase 2 (publish_single_diagnostics); the launch
-        // number, needed only then, is taken here, where its round trip
-        // overlaps the first window loads
-        if (tid == 0 && blockIdx.x != 0) launch = single_launch_number(b);
-    } else if (tid < 4 && s_diag[tid]) {
+    if (tid < 4 && s_diag[tid]) {
         // relaxed device-scope adds: the build's totals are complete when
         // the kernel is, and pass 1 of the build cleared them
         atomicAdd(b.diagnostics + tid, s_diag[tid]);
@@ -816,16 +690,16 @@ __attribute__((amdgpu_waves_per_eu((kFuse != 0 && H <= 128) ? 8 : 1))) void toke
     // Window gather.  Lane l < 33 loads segment l = (row i, tile column j) of
     // an ego's window: cells (ex - 5 + i, 8 * (tyl + j) .. 8 * (tyl + j) + 7)
     // with tyl = floor((ey - 5) / 8), one 16-byte load from the tiled field.
-    // Rows and tile columns outside the map are clamped into it for the load
-    // and staged as unreachable, a third tile column the window does not
-    // reach re-reads the second, and lanes 33..63 repeat segments 0..30, so
-    // every load is issued without a branch and touches only the window's
-    // lines.  Offsets are 32-bit bytes from the env's first tiled field (the
-    // host checks that they fit).
+    // Rows and tile columns outside the map fall in the field's border of
+    // unreachable cells, a third tile column the window does not reach
+    // re-reads the second, and lanes 33..63 repeat segments 0..30, so every
+    // load is issued without a branch and touches only the window's lines.
+    // Offsets are 32-bit bytes from the env's first tiled field (the host
+    // checks that they fit).
     const size_t tcells = tiled_cells(W, H);
     const uint8_t* env_tiles =
         reinterpret_cast<const uint8_t*>(b.cost_tiles + (size_t)env * A * tcells);
-    constexpr int TH = H / 8;
+    constexpr int TC = H / 8 + 2;  // tile grid columns
     const int g_seg = lane < kSegPerEgo ? lane : lane - kSegPerEgo;
     const int g_i = g_seg / 3, g_j = g_seg - (g_seg / 3) * 3;
     auto seg_load = [&](uint32_t pos, int e, uint32_t& fill) -> uint4 {
@@ -833,13 +707,11 @@ __attribute__((amdgpu_waves_per_eu((kFuse != 0 && H <= 128) ? 8 : 1))) void toke
         const int ex = ok ? (int)(pos & 0xFFFFu) : 0, ey = ok ? (int)(pos >> 16) : 0;
         const int tyl = ((ey - kRadius + 64) >> 3) - 8;  // floor((ey - 5) / 8)
         const bool third = (tyl + 2) * 8 <= ey + kRadius;
-        const int xr = ex - kRadius + g_i;
-        const int x = xr < 0 ? 0 : (xr >= W ? W - 1 : xr);
-        const int tr = tyl + ((g_j == 2 && !third) ? 1 : g_j);
-        const int tcol = tr < 0 ? 0 : (tr >= TH ? TH - 1 : tr);
-        fill = (xr == x && tr == tcol) ? 0u : 0xFFFFFFFFu;
+        const int x = ex - kRadius + g_i;  // in [-5, W + 4]: the border covers it
+        const int tcol = tyl + 1 + ((g_j == 2 && !third) ? 1 : g_j);
+        fill = 0u;
         const uint32_t off = (uint32_t)e * (uint32_t)tcells * 2u +
-                             ((uint32_t)(x >> 3) * TH + (uint32_t)tcol) * 128u + (uint32_t)(x & 7) * 16u;
+                             ((uint32_t)((x >> 3) + 1) * TC + (uint32_t)tcol) * 128u + (uint32_t)(x & 7) * 16u;
         return *reinterpret_cast<const uint4*>(env_tiles + off);
     };
 
@@ -961,8 +833,443 @@ __attribute__((amdgpu_waves_per_eu((kFuse != 0 && H <= 128) ? 8 : 1))) void toke
         produce(pos_b, ego_b(p), win_b);
         commit();
     }
+}
+
+// ---------------------------------------------------------------------------
+// Single-launch build (maps of at most kMarkedCells cells, A <= 1024): one
+// workgroup per env does the whole build of build_tokens / build_tokens_from_state
+// (mapf_gpt_builder.cpp:89-114, 140-167): unpack and goal-cache refresh, BFS of
+// the env's changed goals, scatter, tokens.  512-thread workgroups (1024 when
+// A > 512) whose LDS stays under 40 KB at the C2/C3 shape, so four share a CU
+// and a grid of up to 4 x CUs envs runs in one round: each workgroup's start
+// (two dependent HBM round trips) is paid once per launch, not once per round.
+//
+// Start: thread t unpacks agent t (state, goal cache, history in one round
+// trip); the env's changed goals are listed and refreshed by up to
+// L.bfs_waves wavefronts, whose BFS fields overlay the token area.  Then, in
+// one second round trip, every agent's own tiled cell (its greedy-move mark)
+// and every wavefront's first ego pair of windows are loaded while the cell
+// -> agent map (uint16 ids, a 5-cell empty border so that window probes need
+// no bounds test) and a 10-word slot template per agent (position, goal, the
+// six copied tokens) are laid out in LDS.
+//
+// Egos (pairs per wavefront, no workgroup barrier, the next pair's windows in
+// flight while the current pair is turned into tokens), per ego:
+//  * visible agents: lane l probes window cells l and l + 64 in the map.  The
+//    window centre holds the ego's cell, whose agent has the only distance-0
+//    key and takes slot 0; the other candidates' keys (distance << 16 | id)
+//    are compacted into LDS by ballot position and each compacted lane counts
+//    the smaller keys, four per broadcast read, which gives its slot;
+//  * cost tokens: two cells per lane from the window staged in LDS;
+//  * agent section: token 121 + l on lane l (and l + 64 when more than six
+//    slots are in use): the slot's template word, made relative to the ego for
+//    the four coordinates.  The row buffer keeps the previous ego's agent
+//    section, so only slots in use now or then are rewritten, which is one
+//    pass for up to six visible agents;
+//  * the row leaves as 64 x 16-byte streaming stores.
+// ---------------------------------------------------------------------------
+constexpr uint16_t kNoAgent16 = 0xFFFFu;
+constexpr int kTmplWords = 10;  // slot template: x, y, goal x, goal y, 5 history tokens, greedy token
+// LDS the BFS fields of a refresh may overlay: at least this much, so that
+// four 64x64 fields refresh at once in each workgroup
+constexpr size_t kBuildFieldRoom = 32768;
+constexpr int kCentreCell = kRadius * kDiam + kRadius;  // 60: the ego's own cell
+static_assert(kCentreCell < kWave, "the centre is a first-cell probe");
+
+struct BuildLayout {
+    int bfs_waves;
+    size_t map_off, tmpl_off, wave_off, overlay;  // token area, overlaid by BFS fields
+    size_t rec_off, info_off, list_off, nlist_off, diag_off, total;
+};
+
+__host__ __device__ inline BuildLayout build_layout(int A, int W, int H, int waves) {
+    BuildLayout L;
+    const size_t cells = (size_t)W * H;
+    size_t off = 0;
+    L.map_off = off;
+    off = align16(off + (size_t)(W + 2 * kRadius) * (H + 2 * kRadius) * 2);
+    L.tmpl_off = off;
+    off = align16(off + (size_t)A * kTmplWords * 4);
+    L.wave_off = off;
+    off = align16(off + (size_t)waves * kWaveBytes);
+    const size_t field = cells * 2;
+    const size_t room = off > kBuildFieldRoom ? off : kBuildFieldRoom;
+    const size_t fit = room / field;
+    L.bfs_waves = (int)(fit < (size_t)waves ? fit : (size_t)waves);
+    const size_t fields = (size_t)L.bfs_waves * field;
+    L.overlay = align16(off > fields ? off : fields);
+    off = L.overlay;
+    L.rec_off = off;
+    off = align16(off + (size_t)A * kRecWords * 4);
+    L.info_off = off;
+    off = align16(off + (size_t)A * 4);
+    L.list_off = off;
+    off = align16(off + (size_t)A * 8);
+    L.nlist_off = off;
+    off = align16(off + 4);
+    L.diag_off = off;
+    off = align16(off + 4 * 4);
+    L.total = off;
+    return L;
+}
+
+// Workgroup size of the single-launch build: one thread per agent.
+__host__ __device__ inline int build_threads(int A) { return A <= 512 ? 512 : 1024; }
+
+// Lowest agent id keeps a shared cell of the uint16 map: min of the 16-bit
+// half of its dword by compare-and-swap (LDS has no 16-bit atomic min).
+// Returns the id the cell held before.
+__device__ __forceinline__ uint32_t map16_min(uint16_t* map, uint32_t cell, uint32_t id) {
+    uint32_t* word = reinterpret_cast<uint32_t*>(map) + (cell >> 1);
+    const uint32_t shift = (cell & 1u) * 16u;
+    uint32_t cur = *word;
+    while (true) {
+        const uint32_t held = (cur >> shift) & 0xFFFFu;
+        if (held <= id) return held;
+        const uint32_t next = (cur & ~(0xFFFFu << shift)) | (id << shift);
+        const uint32_t seen = atomicCAS(word, cur, next);
+        if (seen == cur) return held;
+        cur = seen;
+    }
+}
+
+// Lanes of an agent-section pass whose token t = base + lane is a
+// coordinate field (t % 10 < 4), and of those the y fields (odd).
+__host__ __device__ constexpr uint64_t coord_lanes(int base, bool y_only) {
+    uint64_t m = 0;
+    for (int l = 0; l < kWave; ++l) {
+        const int f = (base + l) % kAgentTokens;
+        if (f < 4 && (!y_only || (f & 1))) m |= 1ull << l;
+    }
+    return m;
+}
+
+template <int H, bool kRows, int R, int kThreads>
+// Held to 8 wavefronts per SIMD (4 workgroups of 512 threads per CU); not
+// for H = 256 (16-row maps), whose BFS registers would then spill.
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(H <= 128 ? 8 : 1))) void build_kernel(
+    jl_mapfgpt_t b, const int16_t* __restrict__ raw_rows, const int16_t* __restrict__ cur_x,
+    const int16_t* __restrict__ cur_y, const int16_t* __restrict__ goal_x,
+    const int16_t* __restrict__ goal_y) {
+    constexpr int kWaves = kThreads / kWave;
+    constexpr int MH = H + 2 * kRadius;  // map columns
+    constexpr int TC = H / 8 + 2;        // tile grid columns of a tiled field
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int A = b.n_agents, W = b.map_w;
+    const int env = blockIdx.x;
+    const int tid = threadIdx.x;
+    const int lane = tid & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+    const BuildLayout L = build_layout(A, W, H, kWaves);
+    const size_t cells = (size_t)W * H;
+    const size_t tcells = tiled_cells(W, H);
+    const uint32_t fmask = field_mask(W, H);
+    uint16_t* s_map = reinterpret_cast<uint16_t*>(smem + L.map_off);
+    int* s_tmpl = reinterpret_cast<int*>(smem + L.tmpl_off);
+    uint32_t* s_rec = reinterpret_cast<uint32_t*>(smem + L.rec_off);
+    uint32_t* s_info = reinterpret_cast<uint32_t*>(smem + L.info_off);
+    uint2* s_list = reinterpret_cast<uint2*>(smem + L.list_off);
+    int* s_nlist = reinterpret_cast<int*>(smem + L.nlist_off);
+    int* s_diag = reinterpret_cast<int*>(smem + L.diag_off);
+    uint8_t* my_lds = smem + L.wave_off + (size_t)wave * kWaveBytes;
+    uint4* my_win = reinterpret_cast<uint4*>(my_lds);
+    int* my_row = reinterpret_cast<int*>(my_lds + kWinBytes);
+    uint32_t* my_slots = reinterpret_cast<uint32_t*>(my_lds + kWinBytes + kRowBytes);
+
+    unsigned long long launch = 0;  // lane 0 of thread 0: this launch's number
+    if (tid == 0) {
+        *s_nlist = 0;
+        s_diag[0] = s_diag[1] = s_diag[2] = s_diag[3] = 0;
+    }
+    if (blockIdx.x == 0 && tid == 0) {
+        // this launch's diagnostics start from zero, then its number is
+        // published (publish_single_diagnostics, at the end)
+        launch = single_launch_number(b);
+        int z = 0;
+        for (int k = 0; k < 4; ++k) z |= atomicExch(b.diagnostics + k, 0);
+        asm volatile("" ::"v"(z));  // cleared before the launch is published
+        atomicExch(reinterpret_cast<unsigned long long*>(b.build_scratch), launch);
+    }
+
+    // ---- start: unpack (one round trip) ---------------------------------------
+    const bool mine = tid < A;
+    const size_t g = (size_t)env * A + (mine ? tid : 0);
+    uint4 st = make_uint4(0u, 0u, 0u, 0u);
+    uint32_t hist[5] = {5u, 5u, 5u, 5u, 5u};
+    uint32_t info = 0;
+    if (mine) {
+        const uint16_t* h = b.histories + g * 5;
+#pragma unroll
+        for (int k = 0; k < 5; ++k) hist[k] = h[k];  // the kept history (a rejected raw row's too)
+        st = unpack_agent<kRows>(b, (int)g, raw_rows, cur_x, cur_y, goal_x, goal_y, info);
+        if (kRows && !(info & kInfoBadRow)) {
+            const uint16_t* row = reinterpret_cast<const uint16_t*>(raw_rows) + g * 13;
+#pragma unroll
+            for (int k = 0; k < 5; ++k) hist[k] = row[8 + k];
+        }
+    }
+    const uint32_t px = st.y & 0xFFFFu, py = st.y >> 16;
+    const bool valid = mine && px < (uint32_t)W && py < (uint32_t)H;
+    const bool reset = mine && (st.w >> 16) != 0;
+    lds_barrier();  // s_nlist and s_diag cleared
+    if (mine) {
+        s_rec[tid * kRecWords + 0] = valid ? st.y : kNoAgent;
+        s_rec[tid * kRecWords + 1] = st.z;
+        s_info[tid] = info;
+        if (reset) s_list[atomicAdd(s_nlist, 1)] = make_uint2((uint32_t)tid, st.x);
+    }
+    lds_barrier();
+
+    // ---- changed goals: BFS fields overlaying the token area -----------------
+    const int nlist = __builtin_amdgcn_readfirstlane(*s_nlist);
+    if (nlist > 0) {
+        if (wave < L.bfs_waves) {
+            uint16_t* s_dist = reinterpret_cast<uint16_t*>(smem) + (size_t)wave * cells;
+            for (int k = wave; k < nlist; k += L.bfs_waves) {
+                const uint2 it = s_list[k];
+                const uint32_t a = (uint32_t)__builtin_amdgcn_readfirstlane((int)it.x);
+                const uint32_t sx = (uint32_t)__builtin_amdgcn_readfirstlane((int)it.y);
+                const uint32_t pos = (uint32_t)__builtin_amdgcn_readfirstlane((int)s_rec[a * kRecWords]);
+                const uint32_t goal = (uint32_t)__builtin_amdgcn_readfirstlane((int)s_rec[a * kRecWords + 1]);
+                const uint32_t bits = refresh_field<H, R, true>(
+                    b, (size_t)env * A + a, sx & 0xFFFFu, (int)(goal & 0xFFFFu), (int)(goal >> 16),
+                    (int)(pos & 0xFFFFu), (int)(pos >> 16), s_dist);
+                if (lane == 0) s_info[a] |= bits;
+            }
+        }
+        // the refreshed fields are stored before any window load of this
+        // workgroup, and the LDS fields are free for the token area
+        __syncthreads();
+    }
+
+    // ---- second round trip: own cells' marks and the first windows ------------
+    uint32_t f_center = kUnreachable;
+    if (valid && !reset) f_center = b.cost_tiles[g * tcells + tile_offset<H>((int)px, (int)py)];
+
+    // Window segment of this lane: lane l < 33 loads segment (row i, tile
+    // column j) = l of an ego's 11 x 3 segments of 8 cells: rows ex - 5 + i,
+    // tile columns from that of column ey - 5 on (a third the window does not
+    // reach re-reads the second); lanes 33..63 repeat segments 0..30.  Cells
+    // off the map are the tiled field's unreachable border.  Offsets are
+    // 32-bit bytes from the env's first tiled field (the host checks that
+    // they fit).
+    const uint8_t* env_tiles = reinterpret_cast<const uint8_t*>(b.cost_tiles + (size_t)env * A * tcells);
+    const int g_seg = lane < kSegPerEgo ? lane : lane - kSegPerEgo;
+    const int g_i = g_seg / 3, g_j = g_seg - (g_seg / 3) * 3;
+    const int g_j2 = g_j < 1 ? g_j : 1;  // tile column when the window spans two
+    const uint32_t field_bytes = (uint32_t)tcells * 2u;
+    auto seg_load = [&](uint32_t pos, int e) -> uint4 {
+        const uint32_t p = pos == kNoAgent ? 0u : pos;
+        const int x8 = (int)(p & 0xFFFFu) + (8 - kRadius) + g_i;  // bordered row
+        const int y8 = (int)(p >> 16) + (8 - kRadius);             // bordered first column
+        const int tc = (y8 >> 3) + (((y8 & 7) >= 6) ? g_j : g_j2);
+        const uint32_t off = (uint32_t)e * field_bytes + ((uint32_t)(x8 >> 3) * TC + (uint32_t)tc) * 128u +
+                             (uint32_t)(x8 & 7) * 16u;
+        return *reinterpret_cast<const uint4*>(env_tiles + off);
+    };
+    const int npairs = (A + 1) >> 1;
+    auto ego_a = [&](int p) { return 2 * p; };
+    auto ego_b = [&](int p) { return (2 * p + 1) < A ? 2 * p + 1 : 2 * p; };
+    auto uniform_pos = [&](int e) {
+        return (uint32_t)__builtin_amdgcn_readfirstlane((int)s_rec[e * kRecWords]);
+    };
+    uint4 ga = make_uint4(0u, 0u, 0u, 0u), gb = ga;
+    auto stage = [&](int p) {
+        ga = seg_load(uniform_pos(ego_a(p)), ego_a(p));
+        gb = seg_load(uniform_pos(ego_b(p)), ego_b(p));
+    };
+    const bool has_pairs = wave < npairs;
+    if (has_pairs) stage(wave);
+
+    // ---- token area: map, slot templates, wavefront buffers ------------------
+    {
+        const int mwords = ((W + 2 * kRadius) * MH * 2 + 15) / 16;  // the map's 16-byte words
+        uint4* m4 = reinterpret_cast<uint4*>(s_map);
+        for (int k = tid; k < mwords; k += kThreads) m4[k] = make_uint4(~0u, ~0u, ~0u, ~0u);
+    }
+    if (lane < kSlotStride) my_slots[lane] = 0;
+    // the agent section and the tail start as padding (no slot in use)
+    for (int k = kCostTokens + lane; k < kContext; k += kWave) my_row[k] = kTokPad;
+    lds_barrier();
+    int d_over = 0, d_row = 0, d_dup = 0, d_bad = 0;
+    if (mine) {
+        const uint32_t gx = st.z & 0xFFFFu, gy = st.z >> 16;
+        b.active_mask[g] = (px != gx || py != gy) ? 1 : 0;
+        int* tp = s_tmpl + tid * kTmplWords;
+        tp[0] = (int)px;
+        tp[1] = (int)py;
+        tp[2] = (int)gx;
+        tp[3] = (int)gy;
+#pragma unroll
+        for (int k = 0; k < 5; ++k) tp[4 + k] = copy_token(hist[k] & 0xFFFFu, k);
+        const uint32_t inf = s_info[tid];  // refresh bits included
+        d_over = (int)(inf >> kInfoOverflowShift);
+        d_row = (inf & kInfoBadRow) ? 1 : 0;
+        d_bad = (inf & kInfoBadGoal) ? 1 : 0;
+        if (valid) {
+            const uint32_t prev = map16_min(s_map, (px + kRadius) * MH + py + kRadius, (uint32_t)tid);
+            if (prev != kNoAgent16) ++d_dup;  // lowest id keeps a shared cell
+        } else {
+            ++d_bad;  // position off the map (scatter, :336-339)
+        }
+        // greedy mask: from the refresh, or the mark of the agent's own cell
+        // in its kept field (the cross of five cells where that cell is
+        // unreachable)
+        uint32_t greedy = inf & kInfoGreedy;
+        if (!reset && valid)
+            greedy = f_center != kUnreachable ? f_center >> 12 : kept_greedy<H, false>(b, g, (int)px, (int)py);
+        tp[9] = copy_token(greedy, 5);
+    }
+    // wavefront sums, then one LDS add per wavefront and counter
+#pragma unroll
+    for (int m = 1; m < kWave; m <<= 1) {
+        d_over += __shfl_xor(d_over, m, kWave);
+        d_row += __shfl_xor(d_row, m, kWave);
+        d_dup += __shfl_xor(d_dup, m, kWave);
+        d_bad += __shfl_xor(d_bad, m, kWave);
+    }
+    if (lane == 0 && (d_over | d_row | d_dup | d_bad)) {
+        if (d_over) atomicAdd(&s_diag[0], d_over);
+        if (d_row) atomicAdd(&s_diag[1], d_row);
+        if (d_dup) atomicAdd(&s_diag[2], d_dup);
+        if (d_bad) atomicAdd(&s_diag[3], d_bad);
+    }
+    lds_barrier();
+    // the launch number, needed only at the end, is taken here, where its
+    // round trip overlaps the token work
+    if (tid == 0 && blockIdx.x != 0) launch = single_launch_number(b);
+
+    // ---- egos: lane constants ---------------------------------------------------
+    // cost / probe cells q0 = lane and q1 = lane + 64 (lanes 57..63 repeat cell
+    // 120, whose probe they leave out)
+    const bool own_q1 = lane + kWave < kCostTokens;
+    const int q0 = lane, q1 = own_q1 ? lane + kWave : kCostTokens - 1;
+    const int di0 = q0 / kDiam, dj0 = q0 % kDiam, di1 = q1 / kDiam, dj1 = q1 % kDiam;
+    const int win0 = di0 * kRegionCols + dj0, win1 = di1 * kRegionCols + dj1;
+    const int map0 = (di0 - kRadius) * MH + (dj0 - kRadius);
+    const int map1 = (di1 - kRadius) * MH + (dj1 - kRadius);
+    const uint32_t qd0 = (uint32_t)(abs(di0 - kRadius) + abs(dj0 - kRadius)) << 16;
+    const uint32_t qd1 = (uint32_t)(abs(di1 - kRadius) + abs(dj1 - kRadius)) << 16;
+    // agent-section passes: token 121 + t, t = lane (pass 0), lane + 64 (pass 1),
+    // lane + 128 (pass 2, lanes 0..1: slot 12's last two tokens)
+    const int t_slot0 = lane / kAgentTokens, t_slot1 = (lane + kWave) / kAgentTokens;
+    const int t_off0 = (lane % kAgentTokens) * 4;           // byte offset in a template
+    const int t_off1 = ((lane + kWave) % kAgentTokens) * 4;
+    const int t_off2 = ((lane & 1) + 8) * 4;
+    constexpr uint64_t kCoord0 = coord_lanes(0, false), kCoordY0 = coord_lanes(0, true);
+    constexpr uint64_t kCoord1 = coord_lanes(kWave, false), kCoordY1 = coord_lanes(kWave, true);
+    const bool coord0 = (kCoord0 >> lane) & 1, coordy0 = (kCoordY0 >> lane) & 1;
+    const bool coord1 = (kCoord1 >> lane) & 1, coordy1 = (kCoordY1 >> lane) & 1;
+    const uint8_t* tmpl_bytes = reinterpret_cast<const uint8_t*>(s_tmpl);
+    uint32_t* const my_keys = reinterpret_cast<uint32_t*>(my_row);  // [0, 124) before the cost tokens
+    uint32_t* const sink = my_slots + kSlotStride - 1;             // writes of lanes with nothing to write
+    int* const row_sink = reinterpret_cast<int*>(sink);
+    int prev_n = 0;  // slots of the row buffer's agent section written for the previous ego
+
+    // One agent-section token from slot o's template word w: coordinates
+    // relative to the ego (clip +-20, + 20), copied tokens as they are.
+    auto agent_token = [&](int w, bool coord, bool is_y, int ex, int ey) {
+        const int c = w - (is_y ? ey : ex);
+        const int t = (c < -kCostLimit ? -kCostLimit : (c > kCostLimit ? kCostLimit : c)) + kCostLimit;
+        return coord ? t : w;
+    };
+
+    auto produce = [&](uint32_t pos, int e, const uint16_t* win_base) {
+        v4i out = {kTokPad, kTokPad, kTokPad, kTokPad};
+        if (pos != kNoAgent) {
+            const int ex = (int)(pos & 0xFFFFu), ey = (int)(pos >> 16);
+            // region row = dx + 5, column = dy + 5 + ((ey + 3) & 7) (see seg_load)
+            const uint16_t* win = win_base + ((ey + (8 - kRadius)) & 7);
+            const uint32_t center = field_distance(win[kRadius * kRegionCols + kRadius], fmask);
+            const uint32_t v0 = win[win0];
+            const uint32_t v1 = win[win1];
+            const uint16_t* mrow = s_map + (ex + kRadius) * MH + (ey + kRadius);
+            const uint32_t id0 = mrow[map0];
+            const uint32_t id1 = mrow[map1];
+            const uint32_t centre_id = (uint32_t)__builtin_amdgcn_readlane((int)id0, kCentreCell);
+            // candidates other than the centre: compacted keys
+            const bool c0 = id0 != kNoAgent16 && lane != kCentreCell;
+            const bool c1 = own_q1 && id1 != kNoAgent16;
+            const uint64_t m0 = __ballot(c0);
+            const uint64_t m1 = __ballot(c1);
+            const int n0 = __popcll(m0);
+            const int others = n0 + __popcll(m1);
+            const uint32_t lo0 = (uint32_t)m0, hi0 = (uint32_t)(m0 >> 32);
+            const uint32_t lo1 = (uint32_t)m1, hi1 = (uint32_t)(m1 >> 32);
+            const int p0 = (int)__builtin_amdgcn_mbcnt_hi(hi0, __builtin_amdgcn_mbcnt_lo(lo0, 0u));
+            const int p1 = (int)__builtin_amdgcn_mbcnt_hi(hi1, __builtin_amdgcn_mbcnt_lo(lo1, (uint32_t)n0));
+            *(c0 ? my_keys + p0 : sink) = qd0 | id0;
+            *(c1 ? my_keys + p1 : sink) = qd1 | id1;
+            *(lane < 4 ? my_keys + others + lane : sink) = 0xFFFFFFFFu;  // pad for 4-wide reads
+            wave_sync();
+            const uint32_t mine_key = my_keys[lane];
+            int r = 1;  // slot 0 is the centre's
+            for (int j = 0; j < others; j += 4) {
+                const uint4 k4 = *reinterpret_cast<const uint4*>(my_keys + j);
+                r += (k4.x < mine_key) + (k4.y < mine_key) + (k4.z < mine_key) + (k4.w < mine_key);
+            }
+            *((lane < others && r < kVisible) ? my_slots + r : sink) = mine_key & 0xFFFFu;
+            my_slots[0] = centre_id;
+            const int nsel = others + 1 < kVisible ? others + 1 : kVisible;
+            wave_sync();
+            // cost tokens (over the keys)
+            const int cml = (int)center - kCostLimit;
+            my_row[q0] = cost_token_flat(v0, cml, fmask);
+            my_row[q1] = cost_token_flat(v1, cml, fmask);
+            // agent section: slots in use now or for the previous ego
+            const int span = (nsel > prev_n ? nsel : prev_n) * kAgentTokens;
+            {
+                const int o = (int)my_slots[t_slot0];
+                const int w = *reinterpret_cast<const int*>(tmpl_bytes + o * (kTmplWords * 4) + t_off0);
+                const int t = agent_token(w, coord0, coordy0, ex, ey);
+                my_row[kCostTokens + lane] = t_slot0 < nsel ? t : kTokPad;
+            }
+            if (span > kWave) {
+                const int o = (int)my_slots[t_slot1];
+                const int w = *reinterpret_cast<const int*>(tmpl_bytes + o * (kTmplWords * 4) + t_off1);
+                const int t = agent_token(w, coord1, coordy1, ex, ey);
+                *(lane + kWave < kVisible * kAgentTokens ? my_row + kCostTokens + kWave + lane : row_sink) =
+                    t_slot1 < nsel ? t : kTokPad;
+                if (span > 2 * kWave) {
+                    const int o2 = (int)my_slots[kVisible - 1];
+                    const int w2 = *reinterpret_cast<const int*>(tmpl_bytes + o2 * (kTmplWords * 4) + t_off2);
+                    *(lane < 2 ? my_row + kCostTokens + 2 * kWave + lane : row_sink) =
+                        nsel == kVisible ? w2 : kTokPad;
+                }
+            }
+            prev_n = nsel;
+            wave_sync();
+            out = reinterpret_cast<const v4i*>(my_row)[lane];
+            wave_sync();
+        }
+        __builtin_nontemporal_store(
+            out, reinterpret_cast<v4i*>(b.tokens + ((size_t)env * A + e) * kContext) + lane);
+    };
+
+    if (has_pairs) {
+        const uint16_t* win_a = reinterpret_cast<const uint16_t*>(my_win);
+        const uint16_t* win_b = reinterpret_cast<const uint16_t*>(my_win + kSegPerEgo);
+        // lanes 33..63 hold copies of segments 0..30 and store them to the
+        // same words
+        auto commit = [&]() {
+            asm volatile("" : "+v"(ga.x), "+v"(ga.y), "+v"(ga.z), "+v"(ga.w));
+            asm volatile("" : "+v"(gb.x), "+v"(gb.y), "+v"(gb.z), "+v"(gb.w));
+            my_win[g_seg] = ga;
+            my_win[kSegPerEgo + g_seg] = gb;
+            wave_sync();
+        };
+        commit();
+        for (int p = wave; p < npairs; p += kWaves) {
+            const int pn = p + kWaves;
+            const uint32_t pos_a = uniform_pos(ego_a(p)), pos_b = uniform_pos(ego_b(p));
+            stage(pn < npairs ? pn : p);
+            produce(pos_a, ego_a(p), win_a);
+            produce(pos_b, ego_b(p), win_b);
+            commit();
+        }
+    }
     // wavefront 0 always has pairs (npairs >= 1) and reaches this point
-    if (kFuse && tid == 0) publish_single_diagnostics(b, s_diag, launch);
+    if (tid == 0) publish_single_diagnostics(b, s_diag, launch);
 }
 
 // History roll (mapf_gpt_append_actions_kernel, mapf_gpt_cuda.cu:155-178): one
@@ -1128,32 +1435,35 @@ int launch_pass1(const jl_mapfgpt_t* b, const int16_t* rows, const int16_t* cx, 
     return launch_status();
 }
 
-// The whole build runs as one launch (tokens_kernel with kFuse) on maps of
-// at most kMarkedCells cells when an env fits one workgroup and the builder
-// has its build scratch.
+// The whole build runs as one launch (build_kernel) on maps of at most
+// kMarkedCells cells when an env fits one workgroup and the builder has its
+// build scratch.
 bool single_launch(const jl_mapfgpt_t* b) {
-    if (!b->build_scratch || !marked_fields(b->map_w, b->map_h) || b->n_agents > kTokThreads)
-        return false;
-    const TokLayout L = tok_layout(b->n_agents, b->map_w, b->map_h, true);
-    return L.dense && L.total <= 160 * 1024;
+    if (!b->build_scratch || !marked_fields(b->map_w, b->map_h) || b->n_agents > 1024) return false;
+    const int threads = build_threads(b->n_agents);
+    return build_layout(b->n_agents, b->map_w, b->map_h, threads / kWave).total <= 160 * 1024;
 }
 
-template <int H, int kFuse>
+template <int H, bool kRows>
 int launch_single(const jl_mapfgpt_t* b, const int16_t* rows, const int16_t* cx, const int16_t* cy,
                   const int16_t* gx, const int16_t* gy, hipStream_t stream) {
-    const TokLayout L = tok_layout(b->n_agents, b->map_w, H, true);
+    const int threads = build_threads(b->n_agents);
+    const size_t lds = build_layout(b->n_agents, b->map_w, H, threads / kWave).total;
+    const dim3 grid(b->n_envs);
+#define JL_LAUNCH_BUILD(R, T)                                                                      \
+    hipLaunchKernelGGL((build_kernel<H, kRows, R, T>), grid, dim3(T), lds, stream, *b, rows, cx, cy, \
+                       gx, gy)
     if (b->map_w <= 64) {
-        hipLaunchKernelGGL((tokens_kernel<H, true, kFuse, 1>), dim3(b->n_envs), dim3(kTokThreads),
-                           L.total, stream, *b, rows, cx, cy, gx, gy);
+        if (threads == 512) JL_LAUNCH_BUILD(1, 512); else JL_LAUNCH_BUILD(1, 1024);
     } else {
         // W > 64 with W * H <= kMarkedCells: H == 32 only
         if constexpr (H == 32) {
-            hipLaunchKernelGGL((tokens_kernel<H, true, kFuse, 2>), dim3(b->n_envs), dim3(kTokThreads),
-                               L.total, stream, *b, rows, cx, cy, gx, gy);
+            if (threads == 512) JL_LAUNCH_BUILD(2, 512); else JL_LAUNCH_BUILD(2, 1024);
         } else {
             return JL_ERR_PROFILE;
         }
     }
+#undef JL_LAUNCH_BUILD
     return launch_status();
 }
 
@@ -1171,7 +1481,7 @@ int build(const jl_mapfgpt_t* b, const int16_t* rows, const int16_t* cx, const i
                 rc = status(hipEventRecord((hipEvent_t)b->token_events[0], stream));
                 if (rc) return rc;
             }
-            rc = launch_single<H, kRows ? 1 : 2>(b, rows, cx, cy, gx, gy, stream);
+            rc = launch_single<H, kRows>(b, rows, cx, cy, gx, gy, stream);
             if (rc) return rc;
             if (b->token_events[1]) {
                 rc = status(hipEventRecord((hipEvent_t)b->token_events[1], stream));
@@ -1195,13 +1505,10 @@ int build(const jl_mapfgpt_t* b, const int16_t* rows, const int16_t* cx, const i
         }
         const int slice = ego_slice(b->n_agents);
         const dim3 grid2((unsigned)b->n_envs * ((b->n_agents + slice - 1) / slice));
-        const int16_t* none = nullptr;
         if (L.dense) {
-            hipLaunchKernelGGL((tokens_kernel<H, true, 0, 1>), grid2, dim3(kTokThreads), L.total, stream,
-                               *b, none, none, none, none, none);
+            hipLaunchKernelGGL((tokens_kernel<H, true>), grid2, dim3(kTokThreads), L.total, stream, *b);
         } else {
-            hipLaunchKernelGGL((tokens_kernel<H, false, 0, 1>), grid2, dim3(kTokThreads), L.total,
-                               stream, *b, none, none, none, none, none);
+            hipLaunchKernelGGL((tokens_kernel<H, false>), grid2, dim3(kTokThreads), L.total, stream, *b);
         }
         rc = launch_status();
         if (rc) return rc;

@@ -22,7 +22,7 @@ import types
 
 import torch
 
-from ._abi import BUILD_SCRATCH_WORDS, MagatDesc, MapfGPTDesc, SimDesc, check, load_library
+from ._abi import BUILD_SCRATCH_WORDS, MagatDesc, MapfGPTDesc, SimDesc, check, load_library, tiled_field_cells
 
 TASK_LIFELONG = 0
 TASK_STANDARD_MAPF = 1
@@ -271,10 +271,11 @@ class MapfGPTObservationBuilder(_Base):
             self.t_diagnostics = torch.zeros((4,), dtype=torch.int32, device=device)
             self.t_pyg_ptr = torch.arange(E + 1, dtype=torch.int64, device=device) * n_agents
             # build-private workspaces: per-agent greedy mask + diagnostic flags, and
-            # the distance fields in 8x8 tiles (the token pass reads its windows there)
+            # the distance fields in 8x8 tiles with a one-tile border of unreachable
+            # cells (the token pass reads its windows there); -1 is unreachable
             self._agent_info = torch.zeros((N,), dtype=torch.int32, device=device)
             self._cost_tiles = torch.full(
-                (E, n_agents, (W + 7) // 8 * 8 * H), -1, dtype=torch.int16, device=device
+                (E, n_agents, tiled_field_cells(W, H)), -1, dtype=torch.int16, device=device
             )
             # single-launch builds: number of the last launch whose diagnostics
             # were cleared (uint64) and workgroup arrival counters; zero at
