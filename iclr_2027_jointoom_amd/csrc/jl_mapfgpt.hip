@@ -874,11 +874,19 @@ constexpr int kTmplWords = 10;  // slot template: x, y, goal x, goal y, 5 histor
 // four 64x64 fields refresh at once in each workgroup
 constexpr size_t kBuildFieldRoom = 32768;
 constexpr int kCentreCell = kRadius * kDiam + kRadius;  // 60: the ego's own cell
+// Cost-token table: entry i in [0, 42] is the token of d - c = i - 21 (42
+// below -20, 0..40 between, 43 above +20); entry 43 is an unreachable cell's.
+constexpr int kLutEntries = 2 * kCostLimit + 4;
+constexpr int kLutUnreachable = 2 * kCostLimit + 3;
+__device__ __forceinline__ int cost_lut_entry(int i) {
+    return i == kLutUnreachable ? kTokUnreachable
+                                : (i == 0 ? kTokNegClip : (i > 2 * kCostLimit + 1 ? kTokPosClip : i - 1));
+}
 static_assert(kCentreCell < kWave, "the centre is a first-cell probe");
 
 struct BuildLayout {
     int bfs_waves;
-    size_t map_off, tmpl_off, wave_off, overlay;  // token area, overlaid by BFS fields
+    size_t map_off, tmpl_off, wave_off, lut_off, overlay;  // token area, overlaid by BFS fields
     size_t rec_off, info_off, list_off, nlist_off, diag_off, total;
 };
 
@@ -892,6 +900,8 @@ __host__ __device__ inline BuildLayout build_layout(int A, int W, int H, int wav
     off = align16(off + (size_t)A * kTmplWords * 4);
     L.wave_off = off;
     off = align16(off + (size_t)waves * kWaveBytes);
+    L.lut_off = off;
+    off = align16(off + (size_t)kLutEntries * 4);
     const size_t field = cells * 2;
     const size_t room = off > kBuildFieldRoom ? off : kBuildFieldRoom;
     const size_t fit = room / field;
@@ -966,6 +976,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(H <= 1
     const uint32_t fmask = field_mask(W, H);
     uint16_t* s_map = reinterpret_cast<uint16_t*>(smem + L.map_off);
     int* s_tmpl = reinterpret_cast<int*>(smem + L.tmpl_off);
+    int* s_lut = reinterpret_cast<int*>(smem + L.lut_off);
     uint32_t* s_rec = reinterpret_cast<uint32_t*>(smem + L.rec_off);
     uint32_t* s_info = reinterpret_cast<uint32_t*>(smem + L.info_off);
     uint2* s_list = reinterpret_cast<uint2*>(smem + L.list_off);
@@ -976,6 +987,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(H <= 1
     int* my_row = reinterpret_cast<int*>(my_lds + kWinBytes);
     uint32_t* my_slots = reinterpret_cast<uint32_t*>(my_lds + kWinBytes + kRowBytes);
 
+    // the start (round trips and staging) at the highest priority; the ego
+    // loop lowers it as each wavefront advances
+    __builtin_amdgcn_s_setprio(3);
     unsigned long long launch = 0;  // lane 0 of thread 0: this launch's number
     if (tid == 0) {
         *s_nlist = 0;
@@ -1087,6 +1101,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(H <= 1
         uint4* m4 = reinterpret_cast<uint4*>(s_map);
         for (int k = tid; k < mwords; k += kThreads) m4[k] = make_uint4(~0u, ~0u, ~0u, ~0u);
     }
+    if (tid < kLutEntries) s_lut[tid] = cost_lut_entry(tid);
     if (lane < kSlotStride) my_slots[lane] = 0;
     // the agent section and the tail start as padding (no slot in use)
     for (int k = kCostTokens + lane; k < kContext; k += kWave) my_row[k] = kTokPad;
@@ -1141,15 +1156,17 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(H <= 1
 
     // ---- egos: lane constants ---------------------------------------------------
     // cost / probe cells q0 = lane and q1 = lane + 64 (lanes 57..63 repeat cell
-    // 120, whose probe they leave out)
+    // 120, whose probe they leave out); LDS byte offsets per lane, so that each
+    // per-ego address is one add of a wavefront-uniform base
     const bool own_q1 = lane + kWave < kCostTokens;
     const int q0 = lane, q1 = own_q1 ? lane + kWave : kCostTokens - 1;
     const int di0 = q0 / kDiam, dj0 = q0 % kDiam, di1 = q1 / kDiam, dj1 = q1 % kDiam;
-    const int win0 = di0 * kRegionCols + dj0, win1 = di1 * kRegionCols + dj1;
-    const int map0 = (di0 - kRadius) * MH + (dj0 - kRadius);
-    const int map1 = (di1 - kRadius) * MH + (dj1 - kRadius);
+    const int winb0 = (di0 * kRegionCols + dj0) * 2, winb1 = (di1 * kRegionCols + dj1) * 2;
+    const int mapb0 = ((di0 - kRadius) * MH + (dj0 - kRadius)) * 2;
+    const int mapb1 = ((di1 - kRadius) * MH + (dj1 - kRadius)) * 2;
     const uint32_t qd0 = (uint32_t)(abs(di0 - kRadius) + abs(dj0 - kRadius)) << 16;
     const uint32_t qd1 = (uint32_t)(abs(di1 - kRadius) + abs(dj1 - kRadius)) << 16;
+    const bool not_centre = lane != kCentreCell;
     // agent-section passes: token 121 + t, t = lane (pass 0), lane + 64 (pass 1),
     // lane + 128 (pass 2, lanes 0..1: slot 12's last two tokens)
     const int t_slot0 = lane / kAgentTokens, t_slot1 = (lane + kWave) / kAgentTokens;
@@ -1161,75 +1178,87 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(H <= 1
     const bool coord0 = (kCoord0 >> lane) & 1, coordy0 = (kCoordY0 >> lane) & 1;
     const bool coord1 = (kCoord1 >> lane) & 1, coordy1 = (kCoordY1 >> lane) & 1;
     const uint8_t* tmpl_bytes = reinterpret_cast<const uint8_t*>(s_tmpl);
+    const uint8_t* map_bytes = reinterpret_cast<const uint8_t*>(s_map);
     uint32_t* const my_keys = reinterpret_cast<uint32_t*>(my_row);  // [0, 124) before the cost tokens
     uint32_t* const sink = my_slots + kSlotStride - 1;             // writes of lanes with nothing to write
     int* const row_sink = reinterpret_cast<int*>(sink);
+    v4i* const env_rows = reinterpret_cast<v4i*>(b.tokens + (size_t)env * A * kContext);
     int prev_n = 0;  // slots of the row buffer's agent section written for the previous ego
 
     // One agent-section token from slot o's template word w: coordinates
     // relative to the ego (clip +-20, + 20), copied tokens as they are.
-    auto agent_token = [&](int w, bool coord, bool is_y, int ex, int ey) {
-        const int c = w - (is_y ? ey : ex);
+    auto agent_token = [&](int w, bool coord, int sub) {
+        const int c = w - sub;
         const int t = (c < -kCostLimit ? -kCostLimit : (c > kCostLimit ? kCostLimit : c)) + kCostLimit;
         return coord ? t : w;
     };
+    // Cost token of a window value through the LDS table: index clamp(d - c +
+    // 21, 0, 42) (42 below -20, 43 above +20) or 43 for an unreachable cell.
+    auto cost_token_lut = [&](uint32_t v, int c_minus_21) {
+        const int t = (int)(v & fmask) - c_minus_21;
+        const int i = t < 0 ? 0 : (t > 2 * kCostLimit + 2 ? 2 * kCostLimit + 2 : t);
+        return s_lut[v == kUnreachable ? kLutUnreachable : i];
+    };
 
-    auto produce = [&](uint32_t pos, int e, const uint16_t* win_base) {
+    auto produce = [&](uint32_t pos, int e, const uint8_t* win_base) {
         v4i out = {kTokPad, kTokPad, kTokPad, kTokPad};
         if (pos != kNoAgent) {
             const int ex = (int)(pos & 0xFFFFu), ey = (int)(pos >> 16);
             // region row = dx + 5, column = dy + 5 + ((ey + 3) & 7) (see seg_load)
-            const uint16_t* win = win_base + ((ey + (8 - kRadius)) & 7);
-            const uint32_t center = field_distance(win[kRadius * kRegionCols + kRadius], fmask);
-            const uint32_t v0 = win[win0];
-            const uint32_t v1 = win[win1];
-            const uint16_t* mrow = s_map + (ex + kRadius) * MH + (ey + kRadius);
-            const uint32_t id0 = mrow[map0];
-            const uint32_t id1 = mrow[map1];
+            const uint8_t* win = win_base + ((ey + (8 - kRadius)) & 7) * 2;
+            const uint32_t craw = *reinterpret_cast<const uint16_t*>(win + (kRadius * kRegionCols + kRadius) * 2);
+            const uint32_t center = field_distance((uint32_t)__builtin_amdgcn_readfirstlane((int)craw), fmask);
+            const uint32_t v0 = *reinterpret_cast<const uint16_t*>(win + winb0);
+            const uint32_t v1 = *reinterpret_cast<const uint16_t*>(win + winb1);
+            const uint8_t* mrow = map_bytes + ((ex + kRadius) * MH + (ey + kRadius)) * 2;
+            const uint32_t id0 = *reinterpret_cast<const uint16_t*>(mrow + mapb0);
+            const uint32_t id1 = *reinterpret_cast<const uint16_t*>(mrow + mapb1);
             const uint32_t centre_id = (uint32_t)__builtin_amdgcn_readlane((int)id0, kCentreCell);
             // candidates other than the centre: compacted keys
-            const bool c0 = id0 != kNoAgent16 && lane != kCentreCell;
-            const bool c1 = own_q1 && id1 != kNoAgent16;
+            const bool c0 = (id0 != kNoAgent16) & not_centre;
+            const bool c1 = (id1 != kNoAgent16) & own_q1;
             const uint64_t m0 = __ballot(c0);
             const uint64_t m1 = __ballot(c1);
             const int n0 = __popcll(m0);
             const int others = n0 + __popcll(m1);
-            const uint32_t lo0 = (uint32_t)m0, hi0 = (uint32_t)(m0 >> 32);
-            const uint32_t lo1 = (uint32_t)m1, hi1 = (uint32_t)(m1 >> 32);
-            const int p0 = (int)__builtin_amdgcn_mbcnt_hi(hi0, __builtin_amdgcn_mbcnt_lo(lo0, 0u));
-            const int p1 = (int)__builtin_amdgcn_mbcnt_hi(hi1, __builtin_amdgcn_mbcnt_lo(lo1, (uint32_t)n0));
+            const uint32_t p0 = __builtin_amdgcn_mbcnt_hi((uint32_t)(m0 >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m0, 0u));
+            const uint32_t p1 =
+                __builtin_amdgcn_mbcnt_hi((uint32_t)(m1 >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m1, (uint32_t)n0));
             *(c0 ? my_keys + p0 : sink) = qd0 | id0;
             *(c1 ? my_keys + p1 : sink) = qd1 | id1;
             *(lane < 4 ? my_keys + others + lane : sink) = 0xFFFFFFFFu;  // pad for 4-wide reads
             wave_sync();
             const uint32_t mine_key = my_keys[lane];
             int r = 1;  // slot 0 is the centre's
+#pragma nounroll
             for (int j = 0; j < others; j += 4) {
                 const uint4 k4 = *reinterpret_cast<const uint4*>(my_keys + j);
-                r += (k4.x < mine_key) + (k4.y < mine_key) + (k4.z < mine_key) + (k4.w < mine_key);
+                r += (k4.x < mine_key) ? 1 : 0;
+                r += (k4.y < mine_key) ? 1 : 0;
+                r += (k4.z < mine_key) ? 1 : 0;
+                r += (k4.w < mine_key) ? 1 : 0;
             }
-            *((lane < others && r < kVisible) ? my_slots + r : sink) = mine_key & 0xFFFFu;
+            *(((lane < others) & (r < kVisible)) ? my_slots + r : sink) = mine_key & 0xFFFFu;
             my_slots[0] = centre_id;
             const int nsel = others + 1 < kVisible ? others + 1 : kVisible;
             wave_sync();
             // cost tokens (over the keys)
-            const int cml = (int)center - kCostLimit;
-            my_row[q0] = cost_token_flat(v0, cml, fmask);
-            my_row[q1] = cost_token_flat(v1, cml, fmask);
+            const int c21 = (int)center - (kCostLimit + 1);
+            my_row[q0] = cost_token_lut(v0, c21);
+            my_row[q1] = cost_token_lut(v1, c21);
             // agent section: slots in use now or for the previous ego
             const int span = (nsel > prev_n ? nsel : prev_n) * kAgentTokens;
             {
                 const int o = (int)my_slots[t_slot0];
                 const int w = *reinterpret_cast<const int*>(tmpl_bytes + o * (kTmplWords * 4) + t_off0);
-                const int t = agent_token(w, coord0, coordy0, ex, ey);
+                const int t = agent_token(w, coord0, coordy0 ? ey : ex);
                 my_row[kCostTokens + lane] = t_slot0 < nsel ? t : kTokPad;
             }
             if (span > kWave) {
                 const int o = (int)my_slots[t_slot1];
                 const int w = *reinterpret_cast<const int*>(tmpl_bytes + o * (kTmplWords * 4) + t_off1);
-                const int t = agent_token(w, coord1, coordy1, ex, ey);
-                *(lane + kWave < kVisible * kAgentTokens ? my_row + kCostTokens + kWave + lane : row_sink) =
-                    t_slot1 < nsel ? t : kTokPad;
+                const int t = agent_token(w, coord1, coordy1 ? ey : ex);
+                my_row[kCostTokens + kWave + lane] = t_slot1 < nsel ? t : kTokPad;
                 if (span > 2 * kWave) {
                     const int o2 = (int)my_slots[kVisible - 1];
                     const int w2 = *reinterpret_cast<const int*>(tmpl_bytes + o2 * (kTmplWords * 4) + t_off2);
@@ -1242,13 +1271,13 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(H <= 1
             out = reinterpret_cast<const v4i*>(my_row)[lane];
             wave_sync();
         }
-        __builtin_nontemporal_store(
-            out, reinterpret_cast<v4i*>(b.tokens + ((size_t)env * A + e) * kContext) + lane);
+        // streaming store: the row is not read again by this build
+        __builtin_nontemporal_store(out, env_rows + e * (kContext / 4) + lane);
     };
 
     if (has_pairs) {
-        const uint16_t* win_a = reinterpret_cast<const uint16_t*>(my_win);
-        const uint16_t* win_b = reinterpret_cast<const uint16_t*>(my_win + kSegPerEgo);
+        const uint8_t* win_a = reinterpret_cast<const uint8_t*>(my_win);
+        const uint8_t* win_b = reinterpret_cast<const uint8_t*>(my_win + kSegPerEgo);
         // lanes 33..63 hold copies of segments 0..30 and store them to the
         // same words
         auto commit = [&]() {
@@ -1259,7 +1288,19 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(H <= 1
             wave_sync();
         };
         commit();
-        for (int p = wave; p < npairs; p += kWaves) {
+        const int iters = (npairs - wave + kWaves - 1) / kWaves;
+        int it = 0;
+        for (int p = wave; p < npairs; p += kWaves, ++it) {
+            // The hardware issues the oldest wavefront first, which lets the
+            // first workgroup of a CU race ahead and leaves the last one alone
+            // at the end; wavefronts further along yield instead (priority 3
+            // for the first quarter of this wavefront's pairs, 0 for the last).
+            switch ((it * 4) / iters) {
+                case 0: __builtin_amdgcn_s_setprio(3); break;
+                case 1: __builtin_amdgcn_s_setprio(2); break;
+                case 2: __builtin_amdgcn_s_setprio(1); break;
+                default: __builtin_amdgcn_s_setprio(0); break;
+            }
             const int pn = p + kWaves;
             const uint32_t pos_a = uniform_pos(ego_a(p)), pos_b = uniform_pos(ego_b(p));
             stage(pn < npairs ? pn : p);
