@@ -14,6 +14,7 @@ from pathlib import Path
 _PKG_DIR = Path(__file__).resolve().parent
 LIBRARY_PATH = _PKG_DIR / "libjointloom.so"
 BUILD_SCRATCH_WORDS = 2080  # JL_BUILD_SCRATCH_WORDS of jointloom.h
+GAVE_UP_WORD = 2  # JL_BUILD_SCRATCH_GAVE_UP_WORD of jointloom.h
 
 
 def tiled_field_cells(map_w: int, map_h: int) -> int:

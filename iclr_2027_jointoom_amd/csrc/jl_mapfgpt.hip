@@ -491,11 +491,13 @@ __device__ __forceinline__ int copy_token(uint32_t v, int k) {
 
 // build_scratch of the single-launch build (JL_BUILD_SCRATCH_WORDS int32):
 // at byte 0 the uint64 number of the last launch whose diagnostics were
-// cleared; from byte 128, kArriveClasses uint64 arrival counters, one
-// 128-byte line each.  Workgroup g belongs to class g % kArriveClasses and
+// cleared; at byte 8 (word kGaveUpWord) a uint32 count of workgroups whose
+// wait for that number gave up (sticky: only the host clears it); from byte
+// 128, kArriveClasses uint64 arrival counters, one 128-byte line each.  Workgroup g belongs to class g % kArriveClasses and
 // adds 1 to its class's counter once, so every launch (n_envs workgroups,
 // the builder's fixed env count) adds the same per-class count.
 constexpr int kArriveClasses = 64;
+constexpr int kGaveUpWord = JL_BUILD_SCRATCH_GAVE_UP_WORD;
 constexpr int kArriveBaseWords = 32;
 constexpr int kArriveStrideWords = 32;
 static_assert(kArriveBaseWords + kArriveClasses * kArriveStrideWords == JL_BUILD_SCRATCH_WORDS,
@@ -526,15 +528,23 @@ __device__ __forceinline__ unsigned long long single_launch_number(const jl_mapf
 // counts to add (d, its env's sums) waits (bounded) for that number, then
 // adds.  Totals, the number and the arrival counters move only through
 // device-scope atomics, performed where every XCD sees them.  Workgroups
-// without counts, the usual case, touch neither.
+// without counts, the usual case, touch neither.  A wait that reaches its
+// bound (the number never came: the builder's arrival counters or launches
+// out of order) still adds its counts, which a clear may then have wiped or
+// not, and counts itself in the sticky kGaveUpWord for the host to report.
 __device__ __forceinline__ void publish_single_diagnostics(const jl_mapfgpt_t& b, const int* d,
                                                            unsigned long long launch) {
     if ((d[0] | d[1] | d[2] | d[3]) == 0) return;
     const unsigned long long* cleared = reinterpret_cast<const unsigned long long*>(b.build_scratch);
+    bool seen = false;
     for (int spin = 0; spin < kDiagSpinLimit; ++spin) {
-        if (__hip_atomic_load(cleared, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= launch) break;
+        if (__hip_atomic_load(cleared, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= launch) {
+            seen = true;
+            break;
+        }
         __builtin_amdgcn_s_sleep(2);
     }
+    if (!seen) atomicAdd(reinterpret_cast<unsigned int*>(b.build_scratch) + kGaveUpWord, 1u);
     for (int k = 0; k < 4; ++k)
         if (d[k]) atomicAdd(b.diagnostics + k, d[k]);
 }
@@ -1417,6 +1427,13 @@ int check_builder(const jl_mapfgpt_t* b) {
         !b->goal_cache || !b->tokens || !b->active_mask || !b->diagnostics || !b->agent_info ||
         !b->cost_tiles)
         return JL_ERR_ARG;
+    // buffers accessed 16 bytes at a time, and the build scratch's 64-bit
+    // atomics on 128-byte lines
+    const uintptr_t wide = reinterpret_cast<uintptr_t>(b->state_packed) |
+                           reinterpret_cast<uintptr_t>(b->cost_tiles) | reinterpret_cast<uintptr_t>(b->tokens) |
+                           reinterpret_cast<uintptr_t>(b->cost_to_go);
+    if (wide & 15u) return JL_ERR_ARG;
+    if (b->build_scratch && (reinterpret_cast<uintptr_t>(b->build_scratch) & 127u)) return JL_ERR_ARG;
     return JL_OK;
 }
 

@@ -22,7 +22,7 @@ import types
 
 import torch
 
-from ._abi import BUILD_SCRATCH_WORDS, MagatDesc, MapfGPTDesc, SimDesc, check, load_library, tiled_field_cells
+from ._abi import BUILD_SCRATCH_WORDS, GAVE_UP_WORD, MagatDesc, MapfGPTDesc, SimDesc, check, load_library, tiled_field_cells
 
 TASK_LIFELONG = 0
 TASK_STANDARD_MAPF = 1
@@ -303,6 +303,22 @@ class MapfGPTObservationBuilder(_Base):
             build_scratch=_ptr(self._build_scratch),
         )
         self._desc_ref = ctypes.byref(self._desc)
+        # stream of the last build: single-launch builds number themselves on
+        # the device and must run one after another
+        self._build_stream = None
+
+    def _order_builds(self) -> None:
+        """Orders this build after the previous one when they are issued from
+        different streams (single-launch builds derive their launch number
+        from arrival counters that assume builds do not overlap).  Builds
+        captured into a graph are ordered by the capture itself."""
+        if torch.cuda.is_current_stream_capturing():
+            return
+        cur = torch.cuda.current_stream(self._device)
+        last = self._build_stream
+        if last is not None and last != cur:
+            cur.wait_stream(last)
+        self._build_stream = cur
 
     def build_tokens(self, raw_rows: torch.Tensor) -> None:
         """mapf_gpt_builder.cpp:89-114."""
@@ -319,6 +335,7 @@ class MapfGPTObservationBuilder(_Base):
             raw_rows.device == self._device,
             "raw_rows and builder tensors must use the same CUDA device",
         )
+        self._order_builds()
         check(
             self._lib.jl_mapfgpt_build_rows(self._desc_ref, raw_rows.data_ptr(), _stream(self._device)),
             "MAPF-GPT cost-to-go generation",
@@ -331,6 +348,22 @@ class MapfGPTObservationBuilder(_Base):
         maps of at most 4096 cells and at most 1024 agents per env.  No
         counterpart in the reference."""
         return bool(self._lib.jl_mapfgpt_single_launch(self._desc_ref))
+
+    @property
+    def single_launch_waits_given_up(self) -> int:
+        """Workgroups of single-launch builds whose wait for their launch's
+        cleared diagnostics reached its bound (the counts they added may have
+        been cleared by that launch or not): 0 on a healthy builder.  Reads
+        device memory (synchronises the builder's device); sticky until
+        ``clear_single_launch_waits``.  No counterpart in the reference."""
+        if self._build_scratch is None:
+            return 0
+        return int(self._build_scratch[GAVE_UP_WORD].item())
+
+    def clear_single_launch_waits(self) -> None:
+        """Resets the count read by ``single_launch_waits_given_up``."""
+        if self._build_scratch is not None:
+            self._build_scratch[GAVE_UP_WORD].zero_()
 
     def _check_state(self, t: torch.Tensor, name: str) -> None:
         _require(t.is_cuda, f"{name} must be on a CUDA device")
@@ -346,6 +379,7 @@ class MapfGPTObservationBuilder(_Base):
         """mapf_gpt_builder.cpp:140-167."""
         for t, name in ((cur_x, "cur_x"), (cur_y, "cur_y"), (goal_x, "goal_x"), (goal_y, "goal_y")):
             self._check_state(t, name)
+        self._order_builds()
         check(
             self._lib.jl_mapfgpt_build_state(
                 self._desc_ref,

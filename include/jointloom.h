@@ -34,8 +34,11 @@ extern "C" {
 
 typedef void* jl_stream_t; /* hipStream_t */
 
-/* int32 words of a MAPF-GPT builder's build_scratch (8448 bytes). */
+/* int32 words of a MAPF-GPT builder's build_scratch (8320 bytes), and the
+ * word that counts single-launch diagnostics waits that gave up (sticky; the
+ * host reads and clears it). */
 #define JL_BUILD_SCRATCH_WORDS 2080
+#define JL_BUILD_SCRATCH_GAVE_UP_WORD 2
 
 enum {
     JL_OK = 0,
@@ -172,23 +175,33 @@ typedef struct jl_mapfgpt {
     int32_t* diagnostics;       /* [4] overflow, bad row/action, duplicate cell, bad goal/position */
     uint32_t* agent_info;       /* [N] workspace: greedy-move mask and diagnostic flags of
                                    each agent, written by the first pass of a build */
-    uint16_t* cost_tiles;       /* [E, A, ceil(W/8), H/8, 8, 8] workspace: the same fields as
-                                   cost_to_go in 8x8 tiles (one 128-byte line per tile); on
-                                   maps of at most 4096 cells bits 12-15 of a reachable cell
-                                   hold its greedy-move mask */
+    uint16_t* cost_tiles;       /* [E, A, ceil(W/8) + 2, H/8 + 2, 8, 8] workspace, 0xFFFF at
+                                   allocation: the same fields as cost_to_go in 8x8 tiles
+                                   (one 128-byte line per tile) inside a one-tile border of
+                                   unreachable cells that no kernel writes; on maps of at
+                                   most 4096 cells bits 12-15 of a reachable cell hold its
+                                   greedy-move mask */
     int32_t* build_scratch;     /* [JL_BUILD_SCRATCH_WORDS] workspace, zero at construction,
                                    128-byte aligned, used with this builder's n_envs only:
                                    the single-launch build of small maps keeps in it the
                                    uint64 number of the last launch whose diagnostics were
-                                   cleared and per-class workgroup arrival counters, from
-                                   which each launch derives its number on the device (so
-                                   builds captured into a graph keep one launch).  NULL =
+                                   cleared, the count of diagnostics waits that gave up
+                                   (word JL_BUILD_SCRATCH_GAVE_UP_WORD) and per-class
+                                   workgroup arrival counters, from which each launch
+                                   derives its number on the device (so builds captured
+                                   into a graph keep one launch).  That number assumes the
+                                   builds of one builder run one after another: issue them
+                                   in order on one stream (or order the streams).  NULL =
                                    two-launch builds only */
     void* token_events[2];      /* optional hipEvent_t pair recorded on the stream right
                                    before / after the token kernel (profiling); NULL = off */
 } jl_mapfgpt_t;
 
-/* cost_tiles holds what the builder last wrote into cost_to_go; the token
+/* state_packed, cost_to_go, cost_tiles and tokens must be 16-byte aligned
+ * (16-byte accesses) and build_scratch 128-byte aligned; the builds return
+ * JL_ERR_ARG otherwise.
+ *
+ * cost_tiles holds what the builder last wrote into cost_to_go; the token
  * pass reads the windows from it, so values written into cost_to_go by the
  * caller are not seen by later builds (cost_to_go is an output).
  *

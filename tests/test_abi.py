@@ -81,9 +81,32 @@ def test_host_side_argument_checks_return_before_device_work(lib):
     assert lib.jl_ring_upload_compact(ctypes.byref(u), None) == -1  # slot smaller than its layout
 
 
+def test_builder_rejects_misaligned_buffers(lib):
+    """Buffers the build accesses 16 bytes at a time, and the build scratch
+    (64-bit atomics on 128-byte lines), must be aligned: JL_ERR_ARG before
+    any device work."""
+    from iclr_2027_jointoom_amd._abi import MapfGPTDesc
+
+    def desc(**kw):
+        fields = dict(n_envs=1, n_agents=4, map_w=64, map_h=64, grid_bits=256, state_packed=256,
+                      histories=256, labels=256, cost_to_go=256, goal_cache=256, tokens=256,
+                      active_mask=256, diagnostics=256, agent_info=256, cost_tiles=256)
+        fields.update(kw)
+        return MapfGPTDesc(**fields)
+
+    for name in ("state_packed", "cost_to_go", "cost_tiles", "tokens"):
+        b = desc(**{name: 256 + 8})
+        assert lib.jl_mapfgpt_build_state(ctypes.byref(b), 1, 1, 1, 1, None) == -1, name
+        assert lib.jl_mapfgpt_build_rows(ctypes.byref(b), 1, None) == -1, name
+        assert lib.jl_mapfgpt_single_launch(ctypes.byref(b)) == 0, name
+    b = desc(build_scratch=256 + 64)
+    assert lib.jl_mapfgpt_build_state(ctypes.byref(b), 1, 1, 1, 1, None) == -1
+    assert lib.jl_mapfgpt_single_launch(ctypes.byref(desc(build_scratch=256))) == 1
+
+
 def test_ctypes_structs_match_the_c_layout(tmp_path):
-    from iclr_2027_jointoom_amd._abi import (BUILD_SCRATCH_WORDS, MagatDesc, MapfGPTDesc, RecordsDesc,
-                                             SimDesc, StageUploadDesc)
+    from iclr_2027_jointoom_amd._abi import (BUILD_SCRATCH_WORDS, GAVE_UP_WORD, MagatDesc, MapfGPTDesc,
+                                             RecordsDesc, SimDesc, StageUploadDesc)
 
     structs = {"jl_sim_t": SimDesc, "jl_mapfgpt_t": MapfGPTDesc, "jl_magat_t": MagatDesc,
                "jl_records_t": RecordsDesc, "jl_stage_upload_t": StageUploadDesc}
@@ -93,6 +116,7 @@ def test_ctypes_structs_match_the_c_layout(tmp_path):
         for field, _ in py._fields_:
             lines.append(f'printf("{cname} {field} %zu\\n", offsetof({cname}, {field}));')
     lines.append('printf("macro JL_BUILD_SCRATCH_WORDS %d\\n", JL_BUILD_SCRATCH_WORDS);')
+    lines.append('printf("macro JL_BUILD_SCRATCH_GAVE_UP_WORD %d\\n", JL_BUILD_SCRATCH_GAVE_UP_WORD);')
     lines += ["return 0; }"]
     src = tmp_path / "layout.c"
     src.write_text("\n".join(lines))
@@ -101,6 +125,7 @@ def test_ctypes_structs_match_the_c_layout(tmp_path):
     out = subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.split("\n")
     c = {(ln.split()[0], ln.split()[1]): int(ln.split()[2]) for ln in out if ln}
     assert c[("macro", "JL_BUILD_SCRATCH_WORDS")] == BUILD_SCRATCH_WORDS
+    assert c[("macro", "JL_BUILD_SCRATCH_GAVE_UP_WORD")] == GAVE_UP_WORD
     for cname, py in structs.items():
         assert c[(cname, "size")] == ctypes.sizeof(py), cname
         for field, _ in py._fields_:

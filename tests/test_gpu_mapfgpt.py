@@ -595,6 +595,7 @@ def test_c2_full_size_build(oracle):
         for name in ("tokens", "active_mask", "cost_to_go", "state_packed", "labels", "goal_cache", "diagnostics"):
             assert torch.equal(getattr(one, name), getattr(two, name)), (t, name)
         assert one.diagnostics.cpu().tolist() == [0, 0, 0, 0]
+        assert one.single_launch_waits_given_up == 0
         tok = one.tokens.view(E, A, 256)
         assert np.array_equal(tok[sample].cpu().numpy().reshape(-1, 256), ob.tokens), t
         assert bool((tok[:, :, 121] == 20).all() and (tok[:, :, 122] == 20).all()), t
@@ -643,3 +644,128 @@ def test_c5_full_size_build(oracle):
         ob.append(acts.cpu().numpy()[sample])
         sim.update_actions(acts)
         sim.step_sim_only()
+
+
+def _late_diagnostic_rows(rng, grids, A, goals, envs):
+    """Rows with a position off the map and two agents on one cell in each
+    of ``envs`` (diagnostics [3] and [2] from those envs' workgroups only)."""
+    E, W, H = grids.shape
+    rows = _rows_case(rng, grids, A, goals)
+    for e in envs:
+        rows[e * A + 1, 2] = W + 2             # position off the map
+        rows[e * A + 3, 2:4] = rows[e * A + 4, 2:4]  # two agents on one cell
+    return rows
+
+
+def test_single_launch_graph_replay_with_more_envs_than_arrival_classes():
+    """130 envs (more workgroups than the 64 arrival classes, so classes hold
+    two or three workgroups) with diagnostics only in envs 100..129: every
+    replay of a captured single-launch build equals the two-launch build,
+    diagnostics included, publishes the next launch number, and no
+    workgroup's diagnostics wait gives up."""
+    from iclr_2027_jointoom_amd import profile
+
+    W, H, A, E = 64, 64, 24, 130
+    rng = np.random.default_rng(130)
+    grids = (rng.random((E, W, H)) < 0.2).astype(np.int32)
+    ext = profile(W, H)
+    g = torch.from_numpy(grids).cuda()
+    one = ext.MapfGPTObservationBuilder(g, A)
+    two = ext.MapfGPTObservationBuilder(g, A)
+    two._desc.build_scratch = None
+    assert one.single_launch and not two.single_launch
+    goals = _rows_case(rng, grids, A)[:, 4:6].copy()
+    static = torch.from_numpy(_late_diagnostic_rows(rng, grids, A, goals, range(100, 130)).astype(np.int16)).cuda()
+    one.build_tokens(static)
+    two.build_tokens(static)  # the same goal caches before the replays
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    stream = torch.cuda.Stream()  # default priority
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.graph(graph, stream=stream):
+        one.build_tokens(static)
+    torch.cuda.current_stream().wait_stream(stream)
+    torch.cuda.synchronize()
+    launch = _published_launch(one)
+    for it in range(4):
+        rows = _late_diagnostic_rows(rng, grids, A, goals, range(100 + it, 130, 3))
+        static.copy_(torch.from_numpy(rows.astype(np.int16)))
+        graph.replay()
+        launch += 1
+        two.build_tokens(static)
+        torch.cuda.synchronize()
+        for name in ("tokens", "labels", "active_mask", "cost_to_go", "state_packed", "histories",
+                     "goal_cache", "diagnostics"):
+            assert torch.equal(getattr(one, name), getattr(two, name)), (it, name)
+        d = one.diagnostics.cpu().tolist()
+        assert d[2] > 0 and d[3] > 0, d
+        assert _published_launch(one) == launch, it
+    assert one.single_launch_waits_given_up == 0
+
+
+def test_single_launch_diagnostics_wait_gives_up_and_is_reported():
+    """The bounded wait's give-up path, forced from the host: one arrival
+    class's counter is advanced far ahead, so its workgroups derive a launch
+    number that workgroup 0 never publishes.  Those with counts wait out the
+    bound (milliseconds), add their counts anyway and are counted in the
+    sticky word the builder reports; every kernel exits and the outputs
+    equal the two-launch build's (the clear came first here)."""
+    from iclr_2027_jointoom_amd import profile
+
+    W, H, A, E = 32, 32, 16, 70
+    rng = np.random.default_rng(70)
+    grids = (rng.random((E, W, H)) < 0.2).astype(np.int32)
+    ext = profile(W, H)
+    g = torch.from_numpy(grids).cuda()
+    one = ext.MapfGPTObservationBuilder(g, A)
+    two = ext.MapfGPTObservationBuilder(g, A)
+    two._desc.build_scratch = None
+    goals = _rows_case(rng, grids, A)[:, 4:6].copy()
+    rows = torch.from_numpy(_late_diagnostic_rows(rng, grids, A, goals, [1, 65]).astype(np.int16)).cuda()
+    # class 1 (workgroups 1 and 65): uint64 arrival counter at word 32 + 1 * 32
+    counters = one._build_scratch.view(torch.int64)
+    counters[(32 + 32) // 2] = 1 << 40
+    one.build_tokens(rows)
+    two.build_tokens(rows)
+    torch.cuda.synchronize()
+    assert one.single_launch_waits_given_up == 2
+    for name in ("tokens", "labels", "active_mask", "state_packed", "diagnostics"):
+        assert torch.equal(getattr(one, name), getattr(two, name)), name
+    one.clear_single_launch_waits()
+    assert one.single_launch_waits_given_up == 0
+
+
+def test_builds_from_two_streams_are_ordered():
+    """A single-launch build issued from a second stream behind a long sleep,
+    followed at once by a build on the current stream: the builder orders the
+    second build after the first, so the outputs are the second build's (as
+    the two-launch build issued in that order on one stream gives) and the
+    launch numbers and diagnostics stay right."""
+    from iclr_2027_jointoom_amd import profile
+
+    W, H, A, E = 64, 64, 32, 6
+    rng = np.random.default_rng(6)
+    grids = (rng.random((E, W, H)) < 0.2).astype(np.int32)
+    ext = profile(W, H)
+    g = torch.from_numpy(grids).cuda()
+    one = ext.MapfGPTObservationBuilder(g, A)
+    two = ext.MapfGPTObservationBuilder(g, A)
+    two._desc.build_scratch = None
+    goals = _rows_case(rng, grids, A)[:, 4:6].copy()
+    side = torch.cuda.Stream()  # default priority
+    for it in range(3):
+        rows_a = torch.from_numpy(_late_diagnostic_rows(rng, grids, A, goals, [1]).astype(np.int16)).cuda()
+        rows_b = torch.from_numpy(_late_diagnostic_rows(rng, grids, A, goals, [4, 5]).astype(np.int16)).cuda()
+        torch.cuda.synchronize()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            torch.cuda._sleep(20_000_000)
+            one.build_tokens(rows_a)
+        one.build_tokens(rows_b)
+        two.build_tokens(rows_a)
+        two.build_tokens(rows_b)
+        torch.cuda.synchronize()
+        for name in ("tokens", "labels", "active_mask", "state_packed", "diagnostics"):
+            assert torch.equal(getattr(one, name), getattr(two, name)), (it, name)
+        assert _published_launch(one) == 2 * (it + 1)
+    assert one.single_launch_waits_given_up == 0
