@@ -8,7 +8,7 @@ from pathlib import Path
 PKG_DIR = Path(__file__).resolve().parent
 CSRC = PKG_DIR / "csrc"
 SOURCES = ["jl_sim.hip", "jl_mapfgpt.hip", "jl_energy.hip", "jl_magat.hip", "jl_records.hip",
-           "jl_costtracer.hip"]
+           "jl_costtracer.hip", "jl_stream.hip"]
 OUTPUT = PKG_DIR / "libjointloom.so"
 
 # Packed FP32 VALU forms are disabled for all device code.

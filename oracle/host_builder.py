@@ -100,12 +100,13 @@ def tokenize_env(grid, positions, goals, histories, costs, out):
 class CachedTokenBuilder:
     """Per-env goal cache + deque BFS + per-ego tokenizer (mapf_gpt backend)."""
 
-    def __init__(self, grids: np.ndarray, n_agents: int):
+    def __init__(self, grids: np.ndarray, n_agents: int, bfs=bfs_cost):
         self.grids = np.asarray(grids, dtype=np.uint8)
         self.A = int(n_agents)
         self.goals = [None] * len(self.grids)
         self.costs = [[None] * self.A for _ in range(len(self.grids))]
         self.rebuilds = 0
+        self.bfs = bfs
 
     def build(self, rows: np.ndarray):
         """rows: uint16 [E*A, 13] env-major.  Returns (tokens, labels, active)."""
@@ -121,7 +122,7 @@ class CachedTokenBuilder:
                 changed = np.any(self.goals[e] != goals, axis=1)
             changed |= blk[:, 7] != 0
             for a in np.flatnonzero(changed):
-                self.costs[e][a] = bfs_cost(self.grids[e], goals[a])
+                self.costs[e][a] = self.bfs(self.grids[e], goals[a])
                 self.rebuilds += 1
             self.goals[e] = goals
             positions = [(int(x), int(y)) for x, y in blk[:, 2:4]]
@@ -172,13 +173,24 @@ def resolve_step(grid, positions, goals, arrived, actions):
     return prop, new_arrived
 
 
+def _c_bfs(grid, goal):
+    """The C oracle's BFS (same fields as bfs_cost): fills a goal cache fast
+    outside the timed region on large maps."""
+    from oracle.oracle import bfs_u16
+
+    return bfs_u16(grid, goal)[0]
+
+
 def run_stage_worker(args):
-    """Worker body: `steps` resident steps (step + token build) of one stage."""
-    grids, starts, goals, actions, steps = args
+    """Worker body: `steps` resident steps (step + token build) of one stage.
+    An optional sixth item `fast_fill` fills the goal cache before timing with
+    the C BFS instead of the deque BFS (the same fields; untimed)."""
+    grids, starts, goals, actions, steps = args[:5]
+    fast_fill = len(args) > 5 and args[5]
     import time
 
     E, A = starts.shape[:2]
-    builder = CachedTokenBuilder(grids, A)
+    builder = CachedTokenBuilder(grids, A, bfs=_c_bfs if fast_fill else bfs_cost)
     pos = starts.astype(np.int64).copy()
     arrived = np.zeros((E, A), bool)
     hist = np.full((E, A, 5), 5, np.uint16)
@@ -193,6 +205,7 @@ def run_stage_worker(args):
         return r.reshape(E * A, 13)
 
     builder.build(rows_now())  # first build: every goal is fresh (untimed cache fill)
+    builder.bfs = bfs_cost
     t0 = time.perf_counter()
     for s in range(steps):
         tokens, _, active = builder.build(rows_now())
@@ -229,3 +242,53 @@ def run_magat_worker(args):
         m.nodes()
         m.edges()
     return time.perf_counter() - t0, E * A * steps
+
+
+def run_fresh_worker(args):
+    """Worker body: `builds` builds of one stage with every goal fresh (the
+    goal caches cleared first), timed; returns (seconds, agents built)."""
+    grids, starts, goals, builds = args
+    import time
+
+    E, A = starts.shape[:2]
+    rows = np.zeros((E, A, 13), np.uint16)
+    rows[..., 0] = np.arange(E)[:, None]
+    rows[..., 1] = np.arange(A)[None, :]
+    rows[..., 2:4] = starts
+    rows[..., 4:6] = goals
+    rows[..., 8:13] = 5
+    rows = rows.reshape(E * A, 13)
+    builder = CachedTokenBuilder(grids, A)
+    t0 = time.perf_counter()
+    for _ in range(builds):
+        builder.goals = [None] * E  # every goal fresh
+        builder.build(rows)
+    return time.perf_counter() - t0, E * A * builds
+
+
+def run_stage_build_worker(args):
+    """Worker body of the frozen-record consumer on the host: the cached
+    builder over `stages` stages of rows (positions change, goals fixed in the
+    episode; goal cache filled before timing with the C BFS), timed; returns
+    (seconds, agents built)."""
+    grids, positions, goals = args
+    import time
+
+    S, E, A = positions.shape[:3]
+    builder = CachedTokenBuilder(grids, A, bfs=_c_bfs)
+
+    def rows(s):
+        r = np.zeros((E, A, 13), np.uint16)
+        r[..., 0] = np.arange(E)[:, None]
+        r[..., 1] = np.arange(A)[None, :]
+        r[..., 2:4] = positions[s]
+        r[..., 4:6] = goals
+        r[..., 8:13] = 5
+        return r.reshape(E * A, 13)
+
+    builder.build(rows(0))  # untimed cache fill
+    builder.bfs = bfs_cost
+    t0 = time.perf_counter()
+    for s in range(1, S):
+        builder.build(rows(s))
+    return time.perf_counter() - t0, E * A * (S - 1)
