@@ -165,6 +165,7 @@ SIGNATURES = {
     ),
     "jl_seed_rng": (c_int32, [c_void_p, c_int64, ctypes.c_uint64, c_void_p]),
     "jl_mapfgpt_build_rows": (c_int32, [ctypes.POINTER(MapfGPTDesc), c_void_p, c_void_p]),
+    "jl_mapfgpt_build_rows_noalloc": (c_int32, [ctypes.POINTER(MapfGPTDesc), c_void_p, c_void_p]),
     "jl_mapfgpt_build_state": (
         c_int32,
         [ctypes.POINTER(MapfGPTDesc), c_void_p, c_void_p, c_void_p, c_void_p, c_void_p],

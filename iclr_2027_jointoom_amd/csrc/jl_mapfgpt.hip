@@ -26,6 +26,8 @@
 // top-13 search done serially by one lane per ego (:395-496) and every
 // window row read from the row-major field (one 128-byte line per row).
 
+#include <mutex>
+
 #include "jl_bfs.h"
 #include "jl_common.h"
 
@@ -1578,10 +1580,82 @@ int build(const jl_mapfgpt_t* b, const int16_t* rows, const int16_t* cx, const i
     return JL_OK;
 }
 
+// ---- builds that allocate nothing ------------------------------------------
+// jl_mapfgpt_build_rows_noalloc takes its build scratch from this array, one
+// copy per device held until the process ends, instead of the caller's
+// build_scratch.  Host code never passes the array's name to a kernel (on
+// the host it is only a stand-in for the device symbol): it passes the
+// device address that hipGetSymbolAddress returned for the current device.
+static __device__ __align__(256) int32_t scratch[JL_BUILD_SCRATCH_WORDS];
+
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mutex;
+int32_t* g_scratch_ptr[kMaxScratchDevices] = {};
+
+// Device address of `scratch` on the current device, looked up once per
+// device (with that device current) and kept.
+int current_scratch(int32_t** out) {
+    int dev = 0;
+    int rc = status(hipGetDevice(&dev));
+    if (rc) return rc;
+    if (dev < 0 || dev >= kMaxScratchDevices) return JL_ERR_ARG;
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (!g_scratch_ptr[dev]) {
+        void* ptr = nullptr;
+        rc = status(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)));
+        if (rc) return rc;
+        if (!ptr || (reinterpret_cast<uintptr_t>(ptr) & 127u)) return JL_ERR_ARG;
+        g_scratch_ptr[dev] = static_cast<int32_t*>(ptr);
+    }
+    *out = g_scratch_ptr[dev];
+    return JL_OK;
+}
+
+// Zero-fills a build scratch with vector stores (a kernel rather than a
+// memset node, so the clearing also holds in captured graphs).
+__global__ __launch_bounds__(256) void clear_scratch_kernel(int32_t* s) {
+    for (int i = threadIdx.x; i < JL_BUILD_SCRATCH_WORDS / 4; i += 256)
+        reinterpret_cast<int4*>(s)[i] = make_int4(0, 0, 0, 0);
+}
+static_assert(JL_BUILD_SCRATCH_WORDS % 4 == 0, "16-byte clearing");
+
 }  // namespace
 }  // namespace jl
 
 using namespace jl;
+
+extern "C" int jl_mapfgpt_build_rows_noalloc(const jl_mapfgpt_t* b, const int16_t* raw_rows,
+                                             jl_stream_t stream) {
+    if (!b || !raw_rows) return JL_ERR_ARG;
+    jl_mapfgpt_t local = *b;
+    local.build_scratch = nullptr;  // the caller's build scratch is not used
+    int rc = check_builder(&local);
+    if (rc) return rc;
+    hipStream_t st = (hipStream_t)stream;
+    if (st) {
+        // the scratch address is the current device's: the stream must be its
+        int dev = 0, stream_dev = 0;
+        rc = status(hipGetDevice(&dev));
+        if (rc) return rc;
+        rc = status(hipStreamGetDevice(st, &stream_dev));
+        if (rc) return rc;
+        if (stream_dev != dev) return JL_ERR_ARG;
+    }
+    int32_t* ptr = nullptr;
+    rc = current_scratch(&ptr);
+    if (rc) return rc;
+    local.build_scratch = ptr;
+    if (single_launch(&local)) {
+        // every call starts from zero counters (whatever the env count of the
+        // previous call on this device), so its launch number is 1
+        hipLaunchKernelGGL(clear_scratch_kernel, dim3(1), dim3(256), 0, st, ptr);
+        rc = launch_status();
+        if (rc) return rc;
+    } else {
+        local.build_scratch = nullptr;  // the two-launch build uses no scratch
+    }
+    return build<true>(&local, raw_rows, nullptr, nullptr, nullptr, nullptr, st);
+}
 
 extern "C" int jl_mapfgpt_build_rows(const jl_mapfgpt_t* b, const int16_t* raw_rows,
                                      jl_stream_t stream) {

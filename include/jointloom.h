@@ -212,6 +212,24 @@ typedef struct jl_mapfgpt {
 int jl_mapfgpt_build_rows(const jl_mapfgpt_t* b, const int16_t* raw_rows,
                           jl_stream_t stream);
 
+/* jl_mapfgpt_build_rows for callers that cannot allocate (code under graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc); it has no
+ * counterpart in the reference.  It allocates nothing: instead of
+ * b->build_scratch (ignored, may be NULL), it uses the library's own
+ * 8320-byte per-device build scratch (a static device array, JL_BUILD_-
+ * SCRATCH_WORDS words, that each device holds until the process ends).  One
+ * fixed size serves every builder that jl_mapfgpt_build_rows accepts; larger
+ * or malformed builders return JL_ERR_ARG / JL_ERR_PROFILE as there.  A
+ * single-launch build first clears that scratch with a small kernel on
+ * `stream` (two launches, no memset); a two-launch build does not use it.
+ * Outputs equal jl_mapfgpt_build_rows's bit for bit.  All calls on one
+ * device share its scratch: calls that overlap on one device (other streams,
+ * other threads) race and must be serialised by the caller.  The count of
+ * diagnostics waits that gave up is cleared with the scratch on every call
+ * and is not reported.  `stream` must belong to the current device. */
+int jl_mapfgpt_build_rows_noalloc(const jl_mapfgpt_t* b, const int16_t* raw_rows,
+                                  jl_stream_t stream);
+
 /* build_tokens_from_state(cur_x, cur_y, goal_x, goal_y int16 [E, A]).
  * Replaces MapfGPTObservationBuilder::build_tokens_from_state,
  * mapf_gpt_builder.cpp:140-167, and mapf_gpt_state_unpack_kernel :121-152. */

@@ -98,6 +98,7 @@ def test_builder_rejects_misaligned_buffers(lib):
         b = desc(**{name: 256 + 8})
         assert lib.jl_mapfgpt_build_state(ctypes.byref(b), 1, 1, 1, 1, None) == -1, name
         assert lib.jl_mapfgpt_build_rows(ctypes.byref(b), 1, None) == -1, name
+        assert lib.jl_mapfgpt_build_rows_noalloc(ctypes.byref(b), 1, None) == -1, name
         assert lib.jl_mapfgpt_single_launch(ctypes.byref(b)) == 0, name
     b = desc(build_scratch=256 + 64)
     assert lib.jl_mapfgpt_build_state(ctypes.byref(b), 1, 1, 1, 1, None) == -1
