@@ -4,7 +4,7 @@ Ports /root/reference/tests/expert/test_ring_fail_stop.py and the
 RingBuffer / DMAWorker cases of tests/expert/test_pipeline.py:170-320, and
 adds the stage protocol, the staged DMA data path (device calls replaced by
 mocks, as the reference's fail-stop test does), frozen-record round trips
-and forked record producers.
+and record producers started from a forkserver (their shutdown included).
 """
 import contextlib
 import multiprocessing as mp
@@ -301,3 +301,77 @@ def test_ring_stage_source_streams_frozen_records_in_order(tmp_path):
             src.next_rows()
     finally:
         src.close()
+
+
+def test_close_stops_blocked_producers_without_terminating_them(tmp_path):
+    """Producers waiting for a free slot (the consumer stopped reading) exit
+    by themselves when the source closes: exit code 0, no SIGTERM, well
+    within the grace period.  They are forkserver children, not forks of
+    the consumer."""
+    grids, stages = make_records(E=3, A=4, S=8)
+    save_records(tmp_path / "rec", backend="mapf_gpt", grids=grids, stages=stages, metadata={})
+    ring = RingBuffer(capacity=12, feature_dim=13, num_envs=3, agents_per_env=4)  # one stage slot
+    config = {"num_agents": 4, "num_steps": 8, "map_names": ["a", "b", "c"]}
+    src = RingStageSource(ring, "mapf_gpt", config, records=tmp_path / "rec", timeout=20, workers=2)
+    assert all(p._start_method == "forkserver" for p in src.processes)
+    src.start()
+    assert np.array_equal(src.next_rows(), stages[0])
+    time.sleep(0.2)  # the producers now wait for the slot of stage 2
+    assert all(p.is_alive() for p in src.processes)
+    started = time.monotonic()
+    src.close()
+    assert time.monotonic() - started < 3.0
+    assert [p.exitcode for p in src.processes] == [0, 0]
+
+
+def test_finished_producers_exit_and_a_failing_one_is_reported(tmp_path):
+    grids, stages = make_records(E=2, A=4, S=3)
+    save_records(tmp_path / "rec", backend="mapf_gpt", grids=grids, stages=stages, metadata={})
+    ring = RingBuffer(capacity=3 * 8, feature_dim=13, num_envs=2, agents_per_env=4)
+    src = RingStageSource(ring, "mapf_gpt", {"num_agents": 4, "num_steps": 3, "map_names": ["a", "b"]},
+                          records=tmp_path / "rec", timeout=20)
+    try:
+        src.start()
+        for p in src.processes:
+            p.join(10)
+        assert [p.exitcode for p in src.processes] == [0, 0]
+        src.check()  # finished producers are not failures
+        assert [np.array_equal(src.next_rows(), stages[s]) for s in range(3)] == [True] * 3
+    finally:
+        src.close()
+    # blocks of 3 rows into a ring of 4 agents per env: the producers raise
+    ring = RingBuffer(capacity=8, feature_dim=13, num_envs=2, agents_per_env=4)
+    src = RingStageSource(ring, "mapf_gpt", {"num_agents": 3, "num_steps": 3, "map_names": ["a", "b"]},
+                          records=tmp_path / "rec", timeout=20)
+    try:
+        src.start()
+        for p in src.processes:
+            p.join(10)
+        with pytest.raises(RuntimeError, match="expert process exited"):
+            src.check()
+    finally:
+        src.close()
+
+
+def test_ring_stage_source_without_records_is_not_built():
+    ring = RingBuffer(capacity=8, num_envs=2, agents_per_env=2)
+    with pytest.raises(NotImplementedError, match="live expert producers"):
+        RingStageSource(ring, "magat", {"num_agents": 2, "num_steps": 1, "map_names": ["a", "b"]})
+
+
+def test_stage_ready_counts_and_reserve_pointer_follow_the_env_words():
+    ring = RingBuffer(capacity=8, num_envs=2, agents_per_env=2)
+    assert list(ring.stage_ready_counts) == [0, 0] and ring.shared_reserve_ptr.value == 0
+    ring.reserve_and_write(env_block(1, fill=4))
+    assert list(ring.stage_ready_counts) == [1, 0] and ring.shared_reserve_ptr.value == 2
+    ring.write_stage_range(0, np.concatenate([env_block(0, fill=1)]))
+    assert list(ring.stage_ready_counts) == [2, 0] and ring.is_stage_ready(0)
+    # one producer writing both envs of the next stage with one reservation
+    both = np.concatenate([env_block(0, fill=7), env_block(1, fill=8)])
+    assert ring.write_stage_range(0, both) == ring._stage_row_bounds(1)
+    assert ring.is_stage_ready(1) and list(ring.env_write_seq) == [2, 2]
+    assert np.array_equal(ring.cpu_buffer[4:8, 2].numpy(), [7, 7, 8, 8])
+    with pytest.raises(ValueError, match="single env_id"):
+        ring.write_stage_range(0, np.concatenate([env_block(1), env_block(0)]))
+    ring.release_stage(0)
+    assert list(ring.stage_ready_counts) == [0, 2] and not ring.is_stage_ready(0)
