@@ -52,22 +52,25 @@ __device__ __forceinline__ uint32_t field_distance(uint32_t v, uint32_t mask) {
 }
 
 // The builder's tiled copies of the distance fields (cost_tiles): 8x8 tiles
-// of uint16 (128 bytes, one cache line each), row-major over a grid of
-// (ceil(W/8) + 2) x (H/8 + 2) tiles.  The outer ring of tiles is a border of
-// unreachable cells (set at allocation, never written), so a window of
-// radius 5 around any cell of the map reads whole tile rows without
-// clamping; tile (1, 1) holds cells (0..7, 0..7).  Rows past W inside the
-// last tile row of the map are unreachable as well.
+// of uint16 (128 bytes, one cache line each) over a grid of
+// TR = ceil(W/8) + 2 tile rows by H/8 + 2 tile columns, stored column-major:
+// the tiles of one 8-cell column strip are consecutive, so the strip's
+// 16-byte rows (8 cells each) follow one another for x = -8 .. 8 * TR - 9 and
+// a window's row segments lie at offsets linear in the row.  The outer ring
+// of tiles is a border of unreachable cells (set at allocation, never
+// written), so a window of radius 5 around any cell of the map reads whole
+// tile rows without clamping; tile (1, 1) holds cells (0..7, 0..7).  Rows
+// past W inside the last tile row of the map are unreachable as well.
 __host__ __device__ inline int tile_grid_rows(int W) { return (W + 7) / 8 + 2; }
 __host__ __device__ inline int tile_grid_cols(int H) { return H / 8 + 2; }
 __host__ __device__ inline size_t tiled_cells(int W, int H) {
     return (size_t)tile_grid_rows(W) * tile_grid_cols(H) * 64;
 }
+// Cells of one column strip (its TR tiles).
+__host__ __device__ inline uint32_t strip_cells(int W) { return (uint32_t)tile_grid_rows(W) * 64u; }
 // Offset of cell (x, y) in a tiled field, for -8 <= x < W + 8, -8 <= y < H + 8.
-template <int H>
-__device__ __forceinline__ uint32_t tile_offset(int x, int y) {
-    return ((uint32_t)((x >> 3) + 1) * (uint32_t)(H / 8 + 2) + (uint32_t)((y >> 3) + 1)) * 64u +
-           (uint32_t)((x & 7) * 8 + (y & 7));
+__device__ __forceinline__ uint32_t tile_offset(int x, int y, int W) {
+    return (uint32_t)((y >> 3) + 1) * strip_cells(W) + (uint32_t)(x + 8) * 8u + (uint32_t)(y & 7);
 }
 
 inline bool profile_ok(int w, int h) {

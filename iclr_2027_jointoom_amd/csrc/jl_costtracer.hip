@@ -64,7 +64,7 @@ __global__ __launch_bounds__(256) void reward_goals_kernel(jl_sim_t s, const uin
     const int b0 = best[i];
     const int k = cursor[i];
     const int xc = x < W ? x : W - 1, yc = y < H ? y : H - 1;
-    const int d = (int)field_distance(tiles[(size_t)i * tiled_cells(W, H) + tile_offset<H>(xc, yc)],
+    const int d = (int)field_distance(tiles[(size_t)i * tiled_cells(W, H) + tile_offset(xc, yc, W)],
                                       field_mask(W, H));
     rewards[i] = d < b0 ? 0.1f : 0.0f;
     int bn = min(b0, d);
@@ -126,8 +126,8 @@ __device__ __forceinline__ void observe_agents(const jl_sim_t& s, const jl_mapfg
         const uint32_t* ocp = s.grid_ocp + (size_t)(i / A) * words;
         c0[k] = (uint32_t)(xa * H + ya);
         c1[k] = (uint32_t)(xb * H + yb);
-        raw0[k] = f[tile_offset<H>(xa, ya)];  // marks stripped where the distance is taken
-        raw1[k] = f[tile_offset<H>(xb, yb)];
+        raw0[k] = f[tile_offset(xa, ya, W)];  // marks stripped where the distance is taken
+        raw1[k] = f[tile_offset(xb, yb, W)];
         w0[k] = ocp[c0[k] >> 5];
         w1[k] = ocp[c1[k] >> 5];
     }

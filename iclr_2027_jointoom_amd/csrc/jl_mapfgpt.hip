@@ -202,10 +202,10 @@ __device__ __forceinline__ uint32_t kept_greedy(const jl_mapfgpt_t& b, size_t i,
     const int W = b.map_w;
     const uint16_t* f = b.cost_tiles + i * tiled_cells(W, H);
     if (kMarked) {
-        const uint32_t c = f[tile_offset<H>(px, py)];
+        const uint32_t c = f[tile_offset(px, py, W)];
         if (c != kUnreachable) return c >> 12;
     }
-    return greedy_mask<H>([f](int x, int y) { return (uint32_t)f[tile_offset<H>(x, y)]; }, px, py, W);
+    return greedy_mask<H>([f, W](int x, int y) { return (uint32_t)f[tile_offset(x, y, W)]; }, px, py, W);
 }
 
 // Refresh of one agent's field (mapf_gpt_cost_to_go_kernel, :181-325) by the
@@ -258,7 +258,7 @@ __device__ uint32_t refresh_field(const jl_mapfgpt_t& b, size_t agent_index, uin
         const int t = c >> 3, r = c & 7;  // map tile, row inside the tile
         const int tr = t / (H / 8), tc = t - (t / (H / 8)) * (H / 8);
         const int x = tr * 8 + r, y0 = tc * 8;
-        const int dst = ((tr + 1) * (H / 8 + 2) + tc + 1) * 8 + r;
+        const int dst = (tc + 1) * (int)(strip_cells(W) / 8u) + x + 8;  // 16-byte row of strip tc + 1
         const bool in = x < W;  // rows past the map in the last tile row: unreachable
         uint4 v = kMarked ? marked_segment<H>(s_dist, W, in ? x : 0, y0) : lds4[((in ? x : 0) * H + y0) >> 3];
         v.x = in ? v.x : 0xFFFFFFFFu;
@@ -711,7 +711,7 @@ __global__ __launch_bounds__(kTokThreads) void tokens_kernel(jl_mapfgpt_t b) {
     const size_t tcells = tiled_cells(W, H);
     const uint8_t* env_tiles =
         reinterpret_cast<const uint8_t*>(b.cost_tiles + (size_t)env * A * tcells);
-    constexpr int TC = H / 8 + 2;  // tile grid columns
+    const uint32_t strip_bytes = strip_cells(W) * 2u;
     const int g_seg = lane < kSegPerEgo ? lane : lane - kSegPerEgo;
     const int g_i = g_seg / 3, g_j = g_seg - (g_seg / 3) * 3;
     auto seg_load = [&](uint32_t pos, int e, uint32_t& fill) -> uint4 {
@@ -722,8 +722,7 @@ __global__ __launch_bounds__(kTokThreads) void tokens_kernel(jl_mapfgpt_t b) {
         const int x = ex - kRadius + g_i;  // in [-5, W + 4]: the border covers it
         const int tcol = tyl + 1 + ((g_j == 2 && !third) ? 1 : g_j);
         fill = 0u;
-        const uint32_t off = (uint32_t)e * (uint32_t)tcells * 2u +
-                             ((uint32_t)((x >> 3) + 1) * TC + (uint32_t)tcol) * 128u + (uint32_t)(x & 7) * 16u;
+        const uint32_t off = (uint32_t)e * (uint32_t)tcells * 2u + (uint32_t)tcol * strip_bytes + (uint32_t)(x + 8) * 16u;
         return *reinterpret_cast<const uint4*>(env_tiles + off);
     };
 
@@ -895,6 +894,20 @@ __device__ __forceinline__ int cost_lut_entry(int i) {
                                 : (i == 0 ? kTokNegClip : (i > 2 * kCostLimit + 1 ? kTokPosClip : i - 1));
 }
 static_assert(kCentreCell < kWave, "the centre is a first-cell probe");
+// Visible-agent keys of the single-launch build, 16 bits: (Manhattan
+// distance << 10) | id, below 2^15 (distance <= 10, id < 1024), so a 16-bit
+// difference of two keys is negative exactly when the first is smaller.  The
+// pad of the compacted key list is above every key.
+constexpr uint32_t kKeyPad16 = 0x7FFFu;
+constexpr int kKeyDistShift = 10;
+typedef short v2s __attribute__((ext_vector_type(2)));
+
+// Per-agent record of the single-launch build: position word (kNoAgent off
+// the map), goal word, the byte offset of its window's first tile-row segment
+// from the env's first tiled field with bit 0 set when the window spans three
+// column strips, and the byte offset of its cell in the LDS agent map with
+// the window's first column inside its strip ((y + 3) & 7) in bits 16..18.
+constexpr int kBuildRecWords = 4;
 
 struct BuildLayout {
     int bfs_waves;
@@ -922,7 +935,7 @@ __host__ __device__ inline BuildLayout build_layout(int A, int W, int H, int wav
     L.overlay = align16(off > fields ? off : fields);
     off = L.overlay;
     L.rec_off = off;
-    off = align16(off + (size_t)A * kRecWords * 4);
+    off = align16(off + (size_t)A * kBuildRecWords * 4);
     L.info_off = off;
     off = align16(off + (size_t)A * 4);
     L.list_off = off;
@@ -1038,9 +1051,18 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(H <= 1
     const bool valid = mine && px < (uint32_t)W && py < (uint32_t)H;
     const bool reset = mine && (st.w >> 16) != 0;
     lds_barrier();  // s_nlist and s_diag cleared
+    const uint32_t strip_bytes = strip_cells(W) * 2u;
+    const uint32_t field_bytes = (uint32_t)tcells * 2u;
     if (mine) {
-        s_rec[tid * kRecWords + 0] = valid ? st.y : kNoAgent;
-        s_rec[tid * kRecWords + 1] = st.z;
+        const uint32_t ex = valid ? px : 0u, ey = valid ? py : 0u;  // windows of agents off the map: cell 0
+        const uint32_t y8 = ey + (8 - kRadius);                        // bordered first column
+        const uint32_t seg = (uint32_t)tid * field_bytes + (y8 >> 3) * strip_bytes + (ex + (8 - kRadius)) * 16u;
+        uint4 rec;
+        rec.x = valid ? st.y : kNoAgent;
+        rec.y = st.z;
+        rec.z = seg | ((y8 & 7u) >= 6u ? 1u : 0u);
+        rec.w = ((ex + kRadius) * MH + ey + kRadius) * 2u | ((y8 & 7u) << 16);
+        reinterpret_cast<uint4*>(s_rec)[tid] = rec;
         s_info[tid] = info;
         if (reset) s_list[atomicAdd(s_nlist, 1)] = make_uint2((uint32_t)tid, st.x);
     }
@@ -1055,8 +1077,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(H <= 1
                 const uint2 it = s_list[k];
                 const uint32_t a = (uint32_t)__builtin_amdgcn_readfirstlane((int)it.x);
                 const uint32_t sx = (uint32_t)__builtin_amdgcn_readfirstlane((int)it.y);
-                const uint32_t pos = (uint32_t)__builtin_amdgcn_readfirstlane((int)s_rec[a * kRecWords]);
-                const uint32_t goal = (uint32_t)__builtin_amdgcn_readfirstlane((int)s_rec[a * kRecWords + 1]);
+                const uint32_t pos = (uint32_t)__builtin_amdgcn_readfirstlane((int)s_rec[a * kBuildRecWords]);
+                const uint32_t goal = (uint32_t)__builtin_amdgcn_readfirstlane((int)s_rec[a * kBuildRecWords + 1]);
                 const uint32_t bits = refresh_field<H, R, true>(
                     b, (size_t)env * A + a, sx & 0xFFFFu, (int)(goal & 0xFFFFu), (int)(goal >> 16),
                     (int)(pos & 0xFFFFu), (int)(pos >> 16), s_dist);
@@ -1070,39 +1092,42 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(H <= 1
 
     // ---- second round trip: own cells' marks and the first windows ------------
     uint32_t f_center = kUnreachable;
-    if (valid && !reset) f_center = b.cost_tiles[g * tcells + tile_offset<H>((int)px, (int)py)];
+    if (valid && !reset) f_center = b.cost_tiles[g * tcells + tile_offset((int)px, (int)py, W)];
 
-    // Window segment of this lane: lane l < 33 loads segment (row i, tile
-    // column j) = l of an ego's 11 x 3 segments of 8 cells: rows ex - 5 + i,
-    // tile columns from that of column ey - 5 on (a third the window does not
-    // reach re-reads the second); lanes 33..63 repeat segments 0..30.  Cells
-    // off the map are the tiled field's unreachable border.  Offsets are
-    // 32-bit bytes from the env's first tiled field (the host checks that
-    // they fit).
+    // Window segment of this lane: lane l < 33 loads segment (row i, column
+    // strip j) = l of an ego's 11 x 3 segments of 8 cells: row ex - 5 + i of
+    // the strips from that of column ey - 5 on (a third strip the window does
+    // not reach re-reads the second); lanes 33..63 repeat segments 0..30.
+    // Cells off the map are the tiled field's unreachable border.  A strip's
+    // rows are consecutive 16-byte words, so a segment lies at the ego's
+    // record offset (32-bit bytes from the env's first tiled field; the host
+    // checks that they fit) plus a per-lane constant.
     const uint8_t* env_tiles = reinterpret_cast<const uint8_t*>(b.cost_tiles + (size_t)env * A * tcells);
     const int g_seg = lane < kSegPerEgo ? lane : lane - kSegPerEgo;
     const int g_i = g_seg / 3, g_j = g_seg - (g_seg / 3) * 3;
-    const int g_j2 = g_j < 1 ? g_j : 1;  // tile column when the window spans two
-    const uint32_t field_bytes = (uint32_t)tcells * 2u;
-    auto seg_load = [&](uint32_t pos, int e) -> uint4 {
-        const uint32_t p = pos == kNoAgent ? 0u : pos;
-        const int x8 = (int)(p & 0xFFFFu) + (8 - kRadius) + g_i;  // bordered row
-        const int y8 = (int)(p >> 16) + (8 - kRadius);             // bordered first column
-        const int tc = (y8 >> 3) + (((y8 & 7) >= 6) ? g_j : g_j2);
-        const uint32_t off = (uint32_t)e * field_bytes + ((uint32_t)(x8 >> 3) * TC + (uint32_t)tc) * 128u +
-                             (uint32_t)(x8 & 7) * 16u;
+    const uint32_t lane_seg3 = (uint32_t)g_i * 16u + (uint32_t)g_j * strip_bytes;
+    const uint32_t lane_seg2 = (uint32_t)g_i * 16u + (uint32_t)(g_j < 1 ? g_j : 1) * strip_bytes;
+    auto seg_load = [&](uint32_t seg) -> uint4 {
+        const uint32_t off = (seg & ~15u) + ((seg & 1u) ? lane_seg3 : lane_seg2);
         return *reinterpret_cast<const uint4*>(env_tiles + off);
     };
     const int npairs = (A + 1) >> 1;
     auto ego_a = [&](int p) { return 2 * p; };
     auto ego_b = [&](int p) { return (2 * p + 1) < A ? 2 * p + 1 : 2 * p; };
-    auto uniform_pos = [&](int e) {
-        return (uint32_t)__builtin_amdgcn_readfirstlane((int)s_rec[e * kRecWords]);
+    // an ego's record, wavefront-uniform
+    auto record = [&](int e) {
+        const uint4 r = reinterpret_cast<const uint4*>(s_rec)[e];
+        return make_uint4((uint32_t)__builtin_amdgcn_readfirstlane((int)r.x), 0u,
+                          (uint32_t)__builtin_amdgcn_readfirstlane((int)r.z),
+                          (uint32_t)__builtin_amdgcn_readfirstlane((int)r.w));
     };
     uint4 ga = make_uint4(0u, 0u, 0u, 0u), gb = ga;
+    uint4 rec_a = ga, rec_b = ga;  // records of the pair whose windows are staged
     auto stage = [&](int p) {
-        ga = seg_load(uniform_pos(ego_a(p)), ego_a(p));
-        gb = seg_load(uniform_pos(ego_b(p)), ego_b(p));
+        rec_a = record(ego_a(p));
+        rec_b = record(ego_b(p));
+        ga = seg_load(rec_a.z);
+        gb = seg_load(rec_b.z);
     };
     const bool has_pairs = wave < npairs;
     if (has_pairs) stage(wave);
@@ -1176,9 +1201,13 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(H <= 1
     const int winb0 = (di0 * kRegionCols + dj0) * 2, winb1 = (di1 * kRegionCols + dj1) * 2;
     const int mapb0 = ((di0 - kRadius) * MH + (dj0 - kRadius)) * 2;
     const int mapb1 = ((di1 - kRadius) * MH + (dj1 - kRadius)) * 2;
-    const uint32_t qd0 = (uint32_t)(abs(di0 - kRadius) + abs(dj0 - kRadius)) << 16;
-    const uint32_t qd1 = (uint32_t)(abs(di1 - kRadius) + abs(dj1 - kRadius)) << 16;
+    const uint32_t qd0 = (uint32_t)(abs(di0 - kRadius) + abs(dj0 - kRadius)) << kKeyDistShift;
+    const uint32_t qd1 = (uint32_t)(abs(di1 - kRadius) + abs(dj1 - kRadius)) << kKeyDistShift;
     const bool not_centre = lane != kCentreCell;
+    // probe lanes whose cell can hold a candidate: every q0 but the centre,
+    // q1 on lanes 0..56
+    constexpr uint64_t kProbe0 = ~(1ull << kCentreCell);
+    constexpr uint64_t kProbe1 = (1ull << (kCostTokens - kWave)) - 1;
     // agent-section passes: token 121 + t, t = lane (pass 0), lane + 64 (pass 1),
     // lane + 128 (pass 2, lanes 0..1: slot 12's last two tokens)
     const int t_slot0 = lane / kAgentTokens, t_slot1 = (lane + kWave) / kAgentTokens;
@@ -1189,19 +1218,25 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(H <= 1
     constexpr uint64_t kCoord1 = coord_lanes(kWave, false), kCoordY1 = coord_lanes(kWave, true);
     const bool coord0 = (kCoord0 >> lane) & 1, coordy0 = (kCoordY0 >> lane) & 1;
     const bool coord1 = (kCoord1 >> lane) & 1, coordy1 = (kCoordY1 >> lane) & 1;
-    const uint8_t* tmpl_bytes = reinterpret_cast<const uint8_t*>(s_tmpl);
+    // all ones on lanes of a y coordinate token (selects ey over ex)
+    const int ysel0 = coordy0 ? -1 : 0, ysel1 = coordy1 ? -1 : 0;
     const uint8_t* map_bytes = reinterpret_cast<const uint8_t*>(s_map);
-    uint32_t* const my_keys = reinterpret_cast<uint32_t*>(my_row);  // [0, 124) before the cost tokens
-    uint32_t* const sink = my_slots + kSlotStride - 1;             // writes of lanes with nothing to write
+    // template words through 32-bit LDS offsets
+    const uint32_t tmpl_base = (uint32_t)L.tmpl_off;
+
+    uint16_t* const my_keys16 = reinterpret_cast<uint16_t*>(my_row);  // before the cost tokens
+    uint32_t* const sink = my_slots + kSlotStride - 1;               // writes of lanes with nothing to write
     int* const row_sink = reinterpret_cast<int*>(sink);
     v4i* const env_rows = reinterpret_cast<v4i*>(b.tokens + (size_t)env * A * kContext);
     int prev_n = 0;  // slots of the row buffer's agent section written for the previous ego
 
-    // One agent-section token from slot o's template word w: coordinates
-    // relative to the ego (clip +-20, + 20), copied tokens as they are.
-    auto agent_token = [&](int w, bool coord, int sub) {
-        const int c = w - sub;
-        const int t = (c < -kCostLimit ? -kCostLimit : (c > kCostLimit ? kCostLimit : c)) + kCostLimit;
+    // One agent-section token from slot o's template word w: a coordinate
+    // relative to the ego, clip(w - e, -20, 20) + 20 with e = ex, or ey on
+    // lanes of a y field, computed as clamp(w + (20 - ex) + (ysel & (ex - ey)),
+    // 0, 40); copied tokens as they are.
+    auto agent_token = [&](int w, bool coord, int ysel, int x20, int dxy) {
+        const int c = w + x20 + (ysel & dxy);
+        const int t = c < 0 ? 0 : (c > 2 * kCostLimit ? 2 * kCostLimit : c);
         return coord ? t : w;
     };
     // Cost token of a window value through the LDS table: index clamp(d - c +
@@ -1212,45 +1247,47 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(H <= 1
         return s_lut[v == kUnreachable ? kLutUnreachable : i];
     };
 
-    auto produce = [&](uint32_t pos, int e, const uint8_t* win_base) {
+    auto produce = [&](const uint4 rec, int e, const uint8_t* win_base) {
         v4i out = {kTokPad, kTokPad, kTokPad, kTokPad};
+        const uint32_t pos = rec.x;
         if (pos != kNoAgent) {
             const int ex = (int)(pos & 0xFFFFu), ey = (int)(pos >> 16);
             // region row = dx + 5, column = dy + 5 + ((ey + 3) & 7) (see seg_load)
-            const uint8_t* win = win_base + ((ey + (8 - kRadius)) & 7) * 2;
+            const uint8_t* win = win_base + (rec.w >> 15);  // ((ey + 3) & 7) * 2
             const uint32_t craw = *reinterpret_cast<const uint16_t*>(win + (kRadius * kRegionCols + kRadius) * 2);
             const uint32_t center = field_distance((uint32_t)__builtin_amdgcn_readfirstlane((int)craw), fmask);
             const uint32_t v0 = *reinterpret_cast<const uint16_t*>(win + winb0);
             const uint32_t v1 = *reinterpret_cast<const uint16_t*>(win + winb1);
-            const uint8_t* mrow = map_bytes + ((ex + kRadius) * MH + (ey + kRadius)) * 2;
+            const uint8_t* mrow = map_bytes + (rec.w & 0xFFFFu);
             const uint32_t id0 = *reinterpret_cast<const uint16_t*>(mrow + mapb0);
             const uint32_t id1 = *reinterpret_cast<const uint16_t*>(mrow + mapb1);
             const uint32_t centre_id = (uint32_t)__builtin_amdgcn_readlane((int)id0, kCentreCell);
-            // candidates other than the centre: compacted keys
-            const bool c0 = (id0 != kNoAgent16) & not_centre;
-            const bool c1 = (id1 != kNoAgent16) & own_q1;
-            const uint64_t m0 = __ballot(c0);
-            const uint64_t m1 = __ballot(c1);
+            // candidates other than the centre: compacted 16-bit keys
+            const uint64_t m0 = __builtin_amdgcn_ballot_w64(id0 != kNoAgent16) & kProbe0;
+            const uint64_t m1 = __builtin_amdgcn_ballot_w64(id1 != kNoAgent16) & kProbe1;
             const int n0 = __popcll(m0);
             const int others = n0 + __popcll(m1);
             const uint32_t p0 = __builtin_amdgcn_mbcnt_hi((uint32_t)(m0 >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m0, 0u));
             const uint32_t p1 =
                 __builtin_amdgcn_mbcnt_hi((uint32_t)(m1 >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m1, (uint32_t)n0));
-            *(c0 ? my_keys + p0 : sink) = qd0 | id0;
-            *(c1 ? my_keys + p1 : sink) = qd1 | id1;
-            *(lane < 4 ? my_keys + others + lane : sink) = 0xFFFFFFFFu;  // pad for 4-wide reads
+            if ((id0 != kNoAgent16) & not_centre) my_keys16[p0] = (uint16_t)(qd0 | id0);
+            if ((id1 != kNoAgent16) & own_q1) my_keys16[p1] = (uint16_t)(qd1 | id1);
+            if (lane < 8) my_keys16[others + lane] = (uint16_t)kKeyPad16;  // pad to 8-key reads
             wave_sync();
-            const uint32_t mine_key = my_keys[lane];
-            int r = 1;  // slot 0 is the centre's
+            // rank = 1 + the number of smaller keys, 8 keys per read: the
+            // sign bits of the two 16-bit differences of each word
+            const uint32_t mk = my_keys16[lane];
+            const v2s mine2 = __builtin_bit_cast(v2s, mk | (mk << 16));
+            uint32_t r = 1;  // slot 0 is the centre's
 #pragma nounroll
-            for (int j = 0; j < others; j += 4) {
-                const uint4 k4 = *reinterpret_cast<const uint4*>(my_keys + j);
-                r += (k4.x < mine_key) ? 1 : 0;
-                r += (k4.y < mine_key) ? 1 : 0;
-                r += (k4.z < mine_key) ? 1 : 0;
-                r += (k4.w < mine_key) ? 1 : 0;
+            for (int j = 0; j < others; j += 8) {
+                const uint4 k8 = *reinterpret_cast<const uint4*>(my_keys16 + j);
+                r += __builtin_popcount(__builtin_bit_cast(uint32_t, __builtin_bit_cast(v2s, k8.x) - mine2) & 0x80008000u);
+                r += __builtin_popcount(__builtin_bit_cast(uint32_t, __builtin_bit_cast(v2s, k8.y) - mine2) & 0x80008000u);
+                r += __builtin_popcount(__builtin_bit_cast(uint32_t, __builtin_bit_cast(v2s, k8.z) - mine2) & 0x80008000u);
+                r += __builtin_popcount(__builtin_bit_cast(uint32_t, __builtin_bit_cast(v2s, k8.w) - mine2) & 0x80008000u);
             }
-            *(((lane < others) & (r < kVisible)) ? my_slots + r : sink) = mine_key & 0xFFFFu;
+            if ((lane < others) & (r < (uint32_t)kVisible)) my_slots[r] = mk & ((1u << kKeyDistShift) - 1u);
             my_slots[0] = centre_id;
             const int nsel = others + 1 < kVisible ? others + 1 : kVisible;
             wave_sync();
@@ -1260,20 +1297,23 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(H <= 1
             my_row[q1] = cost_token_lut(v1, c21);
             // agent section: slots in use now or for the previous ego
             const int span = (nsel > prev_n ? nsel : prev_n) * kAgentTokens;
+            const int x20 = kCostLimit - ex, dxy = ex - ey;
+            const int live = nsel * kAgentTokens;  // tokens of the slots in use
             {
-                const int o = (int)my_slots[t_slot0];
-                const int w = *reinterpret_cast<const int*>(tmpl_bytes + o * (kTmplWords * 4) + t_off0);
-                const int t = agent_token(w, coord0, coordy0 ? ey : ex);
-                my_row[kCostTokens + lane] = t_slot0 < nsel ? t : kTokPad;
+                const uint32_t o = my_slots[t_slot0];
+                const int w = *reinterpret_cast<const int*>(smem + (tmpl_base + __umul24(o, kTmplWords * 4) + t_off0));
+                const int t = agent_token(w, coord0, ysel0, x20, dxy);
+                my_row[kCostTokens + lane] = lane < live ? t : kTokPad;
             }
             if (span > kWave) {
-                const int o = (int)my_slots[t_slot1];
-                const int w = *reinterpret_cast<const int*>(tmpl_bytes + o * (kTmplWords * 4) + t_off1);
-                const int t = agent_token(w, coord1, coordy1 ? ey : ex);
-                my_row[kCostTokens + kWave + lane] = t_slot1 < nsel ? t : kTokPad;
+                const uint32_t o = my_slots[t_slot1];
+                const int w = *reinterpret_cast<const int*>(smem + (tmpl_base + __umul24(o, kTmplWords * 4) + t_off1));
+                const int t = agent_token(w, coord1, ysel1, x20, dxy);
+                my_row[kCostTokens + kWave + lane] = lane + kWave < live ? t : kTokPad;
                 if (span > 2 * kWave) {
-                    const int o2 = (int)my_slots[kVisible - 1];
-                    const int w2 = *reinterpret_cast<const int*>(tmpl_bytes + o2 * (kTmplWords * 4) + t_off2);
+                    const uint32_t o2 = my_slots[kVisible - 1];
+                    const int w2 =
+                        *reinterpret_cast<const int*>(smem + (tmpl_base + __umul24(o2, kTmplWords * 4) + t_off2));
                     *(lane < 2 ? my_row + kCostTokens + 2 * kWave + lane : row_sink) =
                         nsel == kVisible ? w2 : kTokPad;
                 }
@@ -1300,25 +1340,28 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(H <= 1
             wave_sync();
         };
         commit();
+        // The hardware issues the oldest wavefront first, which lets the first
+        // workgroup of a CU race ahead and leaves the last one alone at the
+        // end; wavefronts further along yield instead: priority 3 for the
+        // first quarter of this wavefront's pairs, 2, 1, then 0 for the last.
         const int iters = (npairs - wave + kWaves - 1) / kWaves;
-        int it = 0;
-        for (int p = wave; p < npairs; p += kWaves, ++it) {
-            // The hardware issues the oldest wavefront first, which lets the
-            // first workgroup of a CU race ahead and leaves the last one alone
-            // at the end; wavefronts further along yield instead (priority 3
-            // for the first quarter of this wavefront's pairs, 0 for the last).
-            switch ((it * 4) / iters) {
+        int p = wave, it = 0;
+        for (int quarter = 0; quarter < 4; ++quarter) {
+            switch (quarter) {
                 case 0: __builtin_amdgcn_s_setprio(3); break;
                 case 1: __builtin_amdgcn_s_setprio(2); break;
                 case 2: __builtin_amdgcn_s_setprio(1); break;
                 default: __builtin_amdgcn_s_setprio(0); break;
             }
-            const int pn = p + kWaves;
-            const uint32_t pos_a = uniform_pos(ego_a(p)), pos_b = uniform_pos(ego_b(p));
-            stage(pn < npairs ? pn : p);
-            produce(pos_a, ego_a(p), win_a);
-            produce(pos_b, ego_b(p), win_b);
-            commit();
+            const int it_end = ((quarter + 1) * iters + 3) / 4;  // the first pair of the next quarter
+            for (; it < it_end; ++it, p += kWaves) {
+                const uint4 cur_a = rec_a, cur_b = rec_b;
+                const int pn = p + kWaves;
+                stage(pn < npairs ? pn : p);
+                produce(cur_a, ego_a(p), win_a);
+                produce(cur_b, ego_b(p), win_b);
+                commit();
+            }
         }
     }
     // wavefront 0 always has pairs (npairs >= 1) and reaches this point

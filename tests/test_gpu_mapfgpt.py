@@ -769,3 +769,60 @@ def test_builds_from_two_streams_are_ordered():
             assert torch.equal(getattr(one, name), getattr(two, name)), (it, name)
         assert _published_launch(one) == 2 * (it + 1)
     assert one.single_launch_waits_given_up == 0
+
+
+def test_single_launch_builds_over_moves_teleports_goal_changes_and_two_launch_refresh(oracle):
+    """Single-launch builds over a run of one-cell moves (onto obstacles and off
+    the map edges included), agents standing on their goal, teleports, goal
+    changes and a two-launch refresh_distances between single-launch builds:
+    every output equals the two-launch build's and the oracle's, so kept
+    fields, their greedy marks and the windows of the tiled copies stay in
+    step with what the builds rewrite."""
+    from iclr_2027_jointoom_amd import profile
+
+    E, W, A = 3, 64, 48
+    rng = np.random.default_rng(77)
+    grids = (rng.random((E, W, W)) < 0.3).astype(np.int32)
+    ext = profile(W, W)
+    g = torch.from_numpy(grids).cuda()
+    one = ext.MapfGPTObservationBuilder(g, A)
+    two = ext.MapfGPTObservationBuilder(g, A)
+    two._desc.build_scratch = None
+    assert one.single_launch and not two.single_launch
+    ob = oracle.OracleMapfGPT(grids, A)
+    pos = np.zeros((E, A, 2), np.int64)
+    goal = np.zeros((E, A, 2), np.int64)
+    for e in range(E):
+        free = np.flatnonzero(grids[e].ravel() == 0)
+        pick = rng.choice(free, 2 * A, replace=False)
+        pos[e, :, 0], pos[e, :, 1] = pick[:A] // W, pick[:A] % W
+        goal[e, :, 0], goal[e, :, 1] = pick[A:] // W, pick[A:] % W
+    # a few agents start on their goal, on an obstacle, and on the map edges
+    goal[0, 0] = pos[0, 0]
+    pos[1, 1] = np.argwhere(grids[1] != 0)[0]
+    pos[2, 2] = (0, 5)
+    pos[2, 3] = (W - 1, W - 1)
+    moves = np.array([[0, 0], [-1, 0], [1, 0], [0, -1], [0, 1]])
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a).astype(np.int16)).cuda()
+    for t in range(8):
+        if t == 3:
+            pos[0, 5:9] = rng.integers(0, W, (4, 2))   # teleports
+        if t == 4:
+            goal[1, 10:14] = pos[1, 10:14]             # goals changed onto the agents' cells
+        if t == 6:
+            # fields rewritten by a two-launch pass between single-launch builds
+            goal[2, 20:30] = rng.integers(0, W, (10, 2))
+            state = [dev(pos[:, :, 0]), dev(pos[:, :, 1]), dev(goal[:, :, 0]), dev(goal[:, :, 1])]
+            one.refresh_distances(*state)
+            two.refresh_distances(*state)
+        state = [dev(pos[:, :, 0]), dev(pos[:, :, 1]), dev(goal[:, :, 0]), dev(goal[:, :, 1])]
+        one.build_tokens_from_state(*state)
+        two.build_tokens_from_state(*state)
+        ob.build_state(*(s.cpu().numpy() for s in state))
+        torch.cuda.synchronize()
+        for name in ("tokens", "active_mask", "cost_to_go", "state_packed", "labels", "goal_cache", "diagnostics"):
+            assert torch.equal(getattr(one, name), getattr(two, name)), (t, name)
+        assert np.array_equal(one.tokens.cpu().numpy(), ob.tokens), t
+        # one-cell moves, clipped to [-1, W] so that some agents leave the map
+        step = moves[rng.integers(0, 5, (E, A))]
+        pos = np.clip(pos + step, -1, W)
