@@ -172,6 +172,7 @@ SIGNATURES = {
     ),
     "jl_mapfgpt_append_actions": (c_int32, [ctypes.POINTER(MapfGPTDesc), c_void_p, c_void_p]),
     "jl_mapfgpt_reset_histories": (c_int32, [ctypes.POINTER(MapfGPTDesc), c_void_p]),
+    "jl_mapfgpt_cost_to_go": (c_int32, [ctypes.POINTER(MapfGPTDesc), c_void_p]),
     "jl_mapfgpt_agent_at_cell": (c_int32, [ctypes.POINTER(MapfGPTDesc), c_void_p]),
     "jl_energy_maps": (
         c_int32,

@@ -11,8 +11,9 @@
 //      mark when the reset flag is set.  It also clears `diagnostics`.
 //   1b. bfs: a grid sized to the CUs; each wavefront scans a range of info
 //      words and runs the bit-parallel BFS (jl_bfs.h) for the marked agents
-//      in its own LDS field, stores the field row-major (cost_to_go, the API
-//      tensor) and in 8x8 tiles (cost_tiles), and completes the info word.
+//      in its own LDS field, stores it in 8x8 tiles (cost_tiles; the API
+//      tensor cost_to_go is filled from them on request) and completes the
+//      info word.
 //   2. tokens: one 1024-thread workgroup per env (per 512 egos of a larger
 //      env).  Phase 1
 //      stages the env's agents (position, goal, the six ego-independent
@@ -211,9 +212,9 @@ __device__ __forceinline__ uint32_t kept_greedy(const jl_mapfgpt_t& b, size_t i,
 // Refresh of one agent's field (mapf_gpt_cost_to_go_kernel, :181-325) by the
 // calling wavefront (every lane, wavefront-uniform arguments): the
 // bit-parallel BFS (jl_bfs.h) from the goal (gx, gy) over env e's free cells
-// in the wavefront's LDS field s_dist (W * H uint16), then the field
-// row-major into cost_to_go (the API tensor) and in 8x8 tiles into
-// cost_tiles (with greedy marks when kMarked), 16-byte stores.  Returns the
+// in the wavefront's LDS field s_dist (W * H uint16), then the field in 8x8
+// tiles into cost_tiles (with greedy marks when kMarked), 16-byte stores; the
+// row-major cost_to_go is filled from the tiles on request.  Returns the
 // agent's info bits: the frontier overflow count, or kInfoBadGoal for a goal
 // off the map or on an obstacle (an all-unreachable field, :224-236), and the
 // greedy mask at its position (spx, spy) when that is on the map.
@@ -249,8 +250,6 @@ __device__ uint32_t refresh_field(const jl_mapfgpt_t& b, size_t agent_index, uin
     if ((uint32_t)spx < (uint32_t)W && (uint32_t)spy < (uint32_t)H)
         info |= greedy_mask<H>([s_dist](int x, int y) { return (uint32_t)s_dist[x * H + y]; }, spx, spy, W);
     const uint4* lds4 = reinterpret_cast<const uint4*>(s_dist);
-    uint4* out = reinterpret_cast<uint4*>(b.cost_to_go + agent_index * (size_t)cells);
-    for (int c = lane; c < cells / 8; c += kWave) out[c] = lds4[c];
     // the map's tiles (the border ring keeps its unreachable cells)
     uint4* tout = reinterpret_cast<uint4*>(b.cost_tiles + agent_index * tcells);
     const int map_tile_rows = (W + 7) / 8;
@@ -1440,6 +1439,34 @@ __global__ __launch_bounds__(256) void agent_at_cell_kernel(jl_mapfgpt_t b) {
         if (map[c] == 0x7FFFFFFF) map[c] = -1;
 }
 
+// cost_to_go on request: each thread turns one 16-byte strip row (8 cells)
+// of a tiled field into the same 8 cells of the row-major field, greedy
+// marks stripped.  Grid-stride over every field of the builder.
+template <int H>
+__global__ __launch_bounds__(256) void cost_to_go_kernel(jl_mapfgpt_t b) {
+    const int W = b.map_w;
+    const uint32_t fmask = field_mask(W, H);
+    const size_t fields = (size_t)b.n_envs * b.n_agents;
+    const size_t per_field = (size_t)W * (H / 8);  // 16-byte words of a row-major field
+    const size_t total = fields * per_field;
+    const uint32_t strip_words = strip_cells(W) / 8u;  // 16-byte rows of a strip
+    const size_t tcells = tiled_cells(W, H);
+    const v4i* tiles = reinterpret_cast<const v4i*>(b.cost_tiles);
+    v4i* out = reinterpret_cast<v4i*>(b.cost_to_go);
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (size_t)gridDim.x * blockDim.x) {
+        const size_t f = i / per_field;
+        const uint32_t w = (uint32_t)(i - f * per_field);
+        const uint32_t x = w / (H / 8), y8 = w - x * (H / 8);  // row, 8-cell group
+        v4i v = tiles[f * (tcells / 8) + (y8 + 1) * strip_words + x + 8];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const uint32_t u = (uint32_t)v[k], lo = u & 0xFFFFu, hi = u >> 16;
+            v[k] = (int)(field_distance(lo, fmask) | (field_distance(hi, fmask) << 16));
+        }
+        __builtin_nontemporal_store(v, out + i);
+    }
+}
+
 // Diagnostics of a refresh without tokens (refresh_distances): the BFS
 // overflow counts and bad goals pass 1 left in agent_info, summed the way the
 // token pass sums them (diagnostics[0] and [3]; the token pass's scatter
@@ -1468,9 +1495,8 @@ int check_builder(const jl_mapfgpt_t* b) {
     // the token pass addresses an env's tiled fields with 32-bit byte offsets
     if ((uint64_t)b->n_agents * tiled_cells(b->map_w, b->map_h) * 2u > 0xFFFFFFFFull)
         return JL_ERR_ARG;
-    if (!b->grid_bits || !b->state_packed || !b->histories || !b->labels || !b->cost_to_go ||
-        !b->goal_cache || !b->tokens || !b->active_mask || !b->diagnostics || !b->agent_info ||
-        !b->cost_tiles)
+    if (!b->grid_bits || !b->state_packed || !b->histories || !b->labels || !b->goal_cache || !b->tokens ||
+        !b->active_mask || !b->diagnostics || !b->agent_info || !b->cost_tiles)
         return JL_ERR_ARG;
     // buffers accessed 16 bytes at a time, and the build scratch's 64-bit
     // atomics on 128-byte lines
@@ -1759,6 +1785,20 @@ extern "C" int jl_mapfgpt_reset_histories(const jl_mapfgpt_t* b, jl_stream_t str
     const int blocks = (int)((n + 255) / 256 < 4096 ? (n + 255) / 256 : 4096);
     hipLaunchKernelGGL(fill_u16_kernel, dim3(blocks), dim3(256), 0, (hipStream_t)stream,
                        b->histories, n, (uint16_t)5);
+    return launch_status();
+}
+
+extern "C" int jl_mapfgpt_cost_to_go(const jl_mapfgpt_t* b, jl_stream_t stream) {
+    int rc = check_builder(b);
+    if (rc) return rc;
+    if (!b->cost_to_go) return JL_ERR_ARG;
+    const size_t words = (size_t)b->n_envs * b->n_agents * b->map_w * (b->map_h / 8);
+    size_t blocks = (words + 255) / 256;
+    const size_t cap = (size_t)device_cus() * 16;
+    if (blocks > cap) blocks = cap;
+    JL_DISPATCH_H(b->map_h, {
+        hipLaunchKernelGGL((cost_to_go_kernel<H>), dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, *b);
+    });
     return launch_status();
 }
 

@@ -429,7 +429,17 @@ class MapfGPTObservationBuilder(_Base):
     tokens = property(lambda self: self.t_tokens)
     active_mask = property(lambda self: self.t_active_mask)
     labels = property(lambda self: self.t_labels)
-    cost_to_go = property(lambda self: self.t_cost_to_go)
+    @property
+    def cost_to_go(self) -> torch.Tensor:
+        """Exact BFS distances [E, A, W, H] (-1 = unreachable), filled from the
+        tiled fields on every read, on the current stream, so that builds
+        replayed from captured graphs are seen as well (the reference writes
+        them on every refresh, mapf_gpt_cuda.cu:318-325)."""
+        check(
+            self._lib.jl_mapfgpt_cost_to_go(self._desc_ref, _stream(self._device)),
+            "MAPF-GPT cost-to-go copy",
+        )
+        return self.t_cost_to_go
     state_packed = property(lambda self: self.t_state_packed)
     histories = property(lambda self: self.t_histories)
     diagnostics = property(lambda self: self.t_diagnostics)
@@ -454,7 +464,7 @@ class MapfGPTObservationBuilder(_Base):
             "labels": self.t_labels,
             "tokens": self.t_tokens,
             "active_mask": self.t_active_mask,
-            "cost_to_go": self.t_cost_to_go,
+            "cost_to_go": self.cost_to_go,
             "agent_at_cell": self.t_agent_at_cell,
             "goal_cache": self.t_goal_cache,
             "diagnostics": self.t_diagnostics,

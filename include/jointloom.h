@@ -167,7 +167,9 @@ typedef struct jl_mapfgpt {
     uint16_t* state_packed;     /* [N, 8] */
     uint16_t* histories;        /* [N, 5] */
     int64_t* labels;            /* [N] */
-    uint16_t* cost_to_go;       /* [E, A, W, H] exact BFS distance, 0xFFFF unreachable */
+    uint16_t* cost_to_go;       /* [E, A, W, H] exact BFS distance, 0xFFFF unreachable,
+                                   filled on request (jl_mapfgpt_cost_to_go); may be
+                                   NULL for builds */
     int32_t* agent_at_cell;     /* [E, W, H] agent id or -1 (filled on request) */
     uint16_t* goal_cache;       /* [N, 2] goal of the last refresh (init 0xFFFF) */
     int32_t* tokens;            /* [N, 256] */
@@ -201,9 +203,10 @@ typedef struct jl_mapfgpt {
  * (16-byte accesses) and build_scratch 128-byte aligned; the builds return
  * JL_ERR_ARG otherwise.
  *
- * cost_tiles holds what the builder last wrote into cost_to_go; the token
- * pass reads the windows from it, so values written into cost_to_go by the
- * caller are not seen by later builds (cost_to_go is an output).
+ * cost_tiles holds the builder's fields; the token pass reads the windows
+ * from it, and jl_mapfgpt_cost_to_go copies it into cost_to_go, so values
+ * written into cost_to_go by the caller are not seen by later builds
+ * (cost_to_go is an output).
  *
  * build_tokens(raw_rows int16 [N, 13]): unpack + goal-cache refresh + BFS of
  * refreshed goals + tokens.  Replaces MapfGPTObservationBuilder::build_tokens,
@@ -265,6 +268,12 @@ int jl_mapfgpt_reset_histories(const jl_mapfgpt_t* b, jl_stream_t stream);
 /* Fill agent_at_cell from state_packed (the reference rewrites it on every
  * build, mapf_gpt_cuda.cu:328-347, 589-603; here it is filled on request). */
 int jl_mapfgpt_agent_at_cell(const jl_mapfgpt_t* b, jl_stream_t stream);
+
+/* Fill cost_to_go (row-major, plain distances) from the tiled fields the
+ * builds keep.  The reference writes cost_to_go on every refresh
+ * (mapf_gpt_cuda.cu:318-325); here refreshes write only the tiled copy and
+ * the row-major one is filled on request. */
+int jl_mapfgpt_cost_to_go(const jl_mapfgpt_t* b, jl_stream_t stream);
 
 /* ------------------------------------------------------------------------ */
 /* BFS distance fields                                                       */
