@@ -172,4 +172,293 @@ __device__ int wave_bfs(const uint64_t (&fr)[R][RowWords<H>::HW], int gx, int gy
     return overflow;
 }
 
+// Free-cell masks of map row x (0 for x >= W), for the group BFS.
+template <int H>
+__device__ __forceinline__ void load_free_row(const uint32_t* __restrict__ env_bits, int W, int x,
+                                              uint64_t (&fr)[RowWords<H>::HW]) {
+    constexpr int HW = RowWords<H>::HW;
+#pragma unroll
+    for (int k = 0; k < HW; ++k) {
+        uint64_t v = 0;
+        if (x < W) {
+            const uint32_t* row = env_bits + (size_t)x * (H / 32);
+            if (H == 32) {
+                v = (uint64_t)(~row[0]) & 0xFFFFFFFFull;
+            } else {
+                v = ~((uint64_t)row[2 * k] | ((uint64_t)row[2 * k + 1] << 32));
+            }
+            if (k == HW - 1) v &= RowWords<H>::kLastMask;
+        }
+        fr[k] = v;
+    }
+}
+
+// LDS words the group BFS needs besides the distance array (64-bit words):
+// the boundary rows [2 parities][R wavefronts][top, bottom][HW], then the
+// per-wavefront flags [2][R] and counts [R] (one word each).
+template <int H, int R>
+__host__ __device__ constexpr int group_bfs_words() {
+    return 2 * R * 2 * RowWords<H>::HW + 2 * R + R;
+}
+
+// wave_bfs over a workgroup of R wavefronts (R > 1; every wavefront of the
+// workgroup calls it with the same arguments and all lanes active):
+// wavefront w owns map rows x = 64 w + lane, each held as HW 64-bit masks
+// (fr: this lane's row).  A level is wave_bfs's on the wavefront's rows; the
+// frontier rows at a wavefront boundary (64 w - 1 and 64 w + 64) travel
+// through LDS, written at the end of the level before and read by this one,
+// in slots alternating with the level's parity, with one workgroup barrier
+// per level.  Each wavefront publishes with its boundary rows whether it
+// found a new cell, and every wavefront stops at the first level at which
+// none did.  The frontier overflow count needs the level's total over the
+// workgroup, taken (with a second barrier) only at levels where some row
+// holds more than kMaxFrontier / (64 R) new cells, as a level of more than
+// kMaxFrontier cells must have one.  Same result as wave_bfs with R rows per
+// lane.
+template <int H, int R, typename T, bool kCountOverflow>
+__device__ int group_bfs(const uint64_t (&fr)[RowWords<H>::HW], int gx, int gy, int cap, T* dist,
+                         uint64_t* s_words) {
+    constexpr int HW = RowWords<H>::HW;
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x / kWave));
+    const int x = wave * kWave + lane;
+    uint64_t* s_edge = s_words;                                      // [2][R][2][HW]
+    int* s_flag = reinterpret_cast<int*>(s_words + 2 * R * 2 * HW);  // [2][R], one word apart
+    int* s_count = s_flag + 2 * 2 * R;                               // [R]
+    uint64_t front[HW], vis[HW];
+#pragma unroll
+    for (int k = 0; k < HW; ++k) {
+        front[k] = 0;
+        vis[k] = 0;
+    }
+    if (x == gx) {
+#pragma unroll
+        for (int k = 0; k < HW; ++k) {
+            if (k == (gy >> 6)) {
+                front[k] = 1ull << (gy & 63);
+                vis[k] = front[k];
+            }
+        }
+    }
+    // boundary rows of slot `slot`: lane 0 stores the top row, lane 63 the bottom one
+    auto publish = [&](int slot, const uint64_t (&f)[HW], int flag) {
+        uint64_t* e = s_edge + (size_t)((slot * R + wave) * 2) * HW;
+        if (lane == 0) {
+#pragma unroll
+            for (int k = 0; k < HW; ++k) e[k] = f[k];
+            s_flag[2 * (slot * R + wave)] = flag;
+        }
+        if (lane == kWave - 1) {
+#pragma unroll
+            for (int k = 0; k < HW; ++k) e[HW + k] = f[k];
+        }
+    };
+    publish(1, front, 1);  // level 1 reads the start's rows from slot 1
+    __syncthreads();
+    constexpr int kBigRow = kMaxFrontier / (kWave * R);
+    int overflow = 0;
+    for (int level = 1; level <= cap; ++level) {
+        const int rd = level & 1, wr = rd ^ 1;
+        uint64_t nf[HW];
+        bool any_new = false;
+        int local = 0;
+#pragma unroll
+        for (int k = 0; k < HW; ++k) {
+            uint64_t up = from_lane_below(front[k]);
+            uint64_t down = from_lane_above(front[k]);
+            if (lane == 0 && wave > 0) up = s_edge[(size_t)((rd * R + wave - 1) * 2 + 1) * HW + k];
+            if (lane == kWave - 1 && wave + 1 < R) down = s_edge[(size_t)((rd * R + wave + 1) * 2) * HW + k];
+            uint64_t left = front[k] << 1;
+            uint64_t right = front[k] >> 1;
+            if (k > 0) left |= front[k - 1] >> 63;
+            if (k + 1 < HW) right |= front[k + 1] << 63;
+            const uint64_t n = (left | right | up | down) & fr[k] & ~vis[k];
+            nf[k] = n;
+            any_new |= (n != 0);
+            if (kCountOverflow) local += __popcll(n);
+        }
+        const bool wave_new = __any(any_new);
+        const bool big = kCountOverflow && __any(local > kBigRow);
+        publish(wr, nf, (wave_new ? 1 : 0) | (big ? 2 : 0));
+#pragma unroll
+        for (int k = 0; k < HW; ++k) {
+            vis[k] |= nf[k];
+            front[k] = nf[k];
+            uint64_t m = nf[k];
+            T* row_dist = dist + x * H + k * 64;
+            while (m) {
+                const int lo = __ffsll((unsigned long long)m) - 1;
+                const int hi = 63 - __clzll((long long)m);
+                row_dist[lo] = (T)level;
+                row_dist[hi] = (T)level;
+                m &= ~((1ull << lo) | (1ull << hi));
+            }
+        }
+        __syncthreads();
+        int flags = 0;
+#pragma unroll
+        for (int w = 0; w < R; ++w) flags |= s_flag[2 * (wr * R + w)];
+        flags = __builtin_amdgcn_readfirstlane(flags);
+        if (kCountOverflow && (flags & 2)) {
+#pragma unroll
+            for (int off = 32; off > 0; off >>= 1) local += __shfl_xor(local, off, kWave);
+            if (lane == 0) s_count[wave] = local;
+            __syncthreads();
+            int total = 0;
+#pragma unroll
+            for (int w = 0; w < R; ++w) total += s_count[w];
+            total = __builtin_amdgcn_readfirstlane(total);
+            if (total > kMaxFrontier) overflow += total - kMaxFrontier;
+            __syncthreads();  // s_count is rewritten at a later level
+        }
+        if (!(flags & 1)) break;
+    }
+    return overflow;
+}
+
+// Bit-planes of BFS levels: a reached cell's level (below 2^kLevelPlanes)
+// is held bit-sliced, plane b holding bit b of the levels of a row's cells.
+constexpr int kLevelPlanes = 16;
+
+// 8x8 bit-matrix transpose: bit c of byte b moves to bit b of byte c.
+__device__ __forceinline__ uint64_t transpose8x8(uint64_t x) {
+    uint64_t t = (x ^ (x >> 7)) & 0x00AA00AA00AA00AAull;
+    x = x ^ t ^ (t << 7);
+    t = (x ^ (x >> 14)) & 0x0000CCCC0000CCCCull;
+    x = x ^ t ^ (t << 14);
+    t = (x ^ (x >> 28)) & 0x00000000F0F0F0F0ull;
+    x = x ^ t ^ (t << 28);
+    return x;
+}
+
+// group_bfs keeping each reached cell's level in registers instead of an LDS
+// distance array: at level L the new frontier is ORed into the planes of
+// L's set bits, so no per-cell write happens during the search.  On return
+// vis holds the reached cells of this lane's row (the start included, at
+// level 0) and `top` the last level that reached a cell.  s_words as for
+// group_bfs.
+template <int H, int R, bool kCountOverflow>
+__device__ int group_bfs_planes(const uint64_t (&fr)[RowWords<H>::HW], int gx, int gy,
+                                uint64_t (&vis)[RowWords<H>::HW],
+                                uint64_t (&pl)[kLevelPlanes][RowWords<H>::HW], int& top, uint64_t* s_words) {
+    constexpr int HW = RowWords<H>::HW;
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x / kWave));
+    const int x = wave * kWave + lane;
+    uint64_t* s_edge = s_words;
+    int* s_flag = reinterpret_cast<int*>(s_words + 2 * R * 2 * HW);
+    int* s_count = s_flag + 2 * 2 * R;
+    uint64_t front[HW];
+#pragma unroll
+    for (int k = 0; k < HW; ++k) {
+        front[k] = 0;
+        vis[k] = 0;
+#pragma unroll
+        for (int b = 0; b < kLevelPlanes; ++b) pl[b][k] = 0;
+    }
+    if (x == gx) {
+#pragma unroll
+        for (int k = 0; k < HW; ++k) {
+            if (k == (gy >> 6)) {
+                front[k] = 1ull << (gy & 63);
+                vis[k] = front[k];
+            }
+        }
+    }
+    auto publish = [&](int slot, const uint64_t (&f)[HW], int flag) {
+        uint64_t* e = s_edge + (size_t)((slot * R + wave) * 2) * HW;
+        if (lane == 0) {
+#pragma unroll
+            for (int k = 0; k < HW; ++k) e[k] = f[k];
+            s_flag[2 * (slot * R + wave)] = flag;
+        }
+        if (lane == kWave - 1) {
+#pragma unroll
+            for (int k = 0; k < HW; ++k) e[HW + k] = f[k];
+        }
+    };
+    publish(1, front, 1);
+    __syncthreads();
+    constexpr int kBigRow = kMaxFrontier / (kWave * R);
+    constexpr int kCap = (1 << kLevelPlanes) - 2;  // levels stay below the unreachable value
+    int overflow = 0;
+    top = 0;
+    for (int level = 1; level <= kCap; ++level) {
+        const int rd = level & 1, wr = rd ^ 1;
+        uint64_t nf[HW];
+        bool any_new = false;
+        int local = 0;
+#pragma unroll
+        for (int k = 0; k < HW; ++k) {
+            uint64_t up = from_lane_below(front[k]);
+            uint64_t down = from_lane_above(front[k]);
+            if (lane == 0 && wave > 0) up = s_edge[(size_t)((rd * R + wave - 1) * 2 + 1) * HW + k];
+            if (lane == kWave - 1 && wave + 1 < R) down = s_edge[(size_t)((rd * R + wave + 1) * 2) * HW + k];
+            uint64_t left = front[k] << 1;
+            uint64_t right = front[k] >> 1;
+            if (k > 0) left |= front[k - 1] >> 63;
+            if (k + 1 < HW) right |= front[k + 1] << 63;
+            const uint64_t n = (left | right | up | down) & fr[k] & ~vis[k];
+            nf[k] = n;
+            any_new |= (n != 0);
+            if (kCountOverflow) local += __popcll(n);
+        }
+        const bool wave_new = __any(any_new);
+        const bool big = kCountOverflow && __any(local > kBigRow);
+        publish(wr, nf, (wave_new ? 1 : 0) | (big ? 2 : 0));
+#pragma unroll
+        for (int k = 0; k < HW; ++k) {
+            vis[k] |= nf[k];
+            front[k] = nf[k];
+        }
+#pragma unroll
+        for (int b = 0; b < kLevelPlanes; ++b) {
+            if ((level >> b) & 1) {
+#pragma unroll
+                for (int k = 0; k < HW; ++k) pl[b][k] |= nf[k];
+            }
+        }
+        __syncthreads();
+        int flags = 0;
+#pragma unroll
+        for (int w = 0; w < R; ++w) flags |= s_flag[2 * (wr * R + w)];
+        flags = __builtin_amdgcn_readfirstlane(flags);
+        if (kCountOverflow && (flags & 2)) {
+#pragma unroll
+            for (int off = 32; off > 0; off >>= 1) local += __shfl_xor(local, off, kWave);
+            if (lane == 0) s_count[wave] = local;
+            __syncthreads();
+            int total = 0;
+#pragma unroll
+            for (int w = 0; w < R; ++w) total += s_count[w];
+            total = __builtin_amdgcn_readfirstlane(total);
+            if (total > kMaxFrontier) overflow += total - kMaxFrontier;
+            __syncthreads();
+        }
+        if (!(flags & 1)) break;
+        top = level;
+    }
+    return overflow;
+}
+
+// Level of this lane's cell at column y from the planes (kUnreachable when
+// the cell was not reached).
+template <int H>
+__device__ __forceinline__ uint32_t plane_level(const uint64_t (&vis)[RowWords<H>::HW],
+                                                const uint64_t (&pl)[kLevelPlanes][RowWords<H>::HW], int y) {
+    constexpr int HW = RowWords<H>::HW;
+    uint32_t d = 0;
+    bool reached = false;
+#pragma unroll
+    for (int k = 0; k < HW; ++k) {
+        if (k == (y >> 6)) {
+            const int bit = y & 63;
+            reached = (vis[k] >> bit) & 1;
+#pragma unroll
+            for (int b = 0; b < kLevelPlanes; ++b) d |= (uint32_t)((pl[b][k] >> bit) & 1) << b;
+        }
+    }
+    return reached ? d : kUnreachable;
+}
+
 }  // namespace jl

@@ -270,6 +270,109 @@ __device__ uint32_t refresh_field(const jl_mapfgpt_t& b, size_t agent_index, uin
     return info;
 }
 
+// refresh_field (unmarked fields) by a workgroup of R wavefronts on maps of
+// more than 64 rows, without an LDS distance array: the group BFS with
+// bit-sliced levels (jl_bfs.h, wavefront w on rows 64 w .. 64 w + 63), then
+// every lane turns its row into 8-cell tile-row segments (one 8x8 bit
+// transpose per 8 planes and segment) and stores them into the tiled field.
+// The five cells of the greedy mask at (spx, spy) travel through s_gm.  Every
+// thread calls it with the same arguments.  Same tiles and info bits as
+// refresh_field.
+template <int H, int R>
+__device__ uint32_t refresh_field_group(const jl_mapfgpt_t& b, size_t agent_index, uint32_t e, int gx, int gy,
+                                        int spx, int spy, uint64_t* s_words, uint32_t* s_gm) {
+    constexpr int HW = RowWords<H>::HW;
+    const int W = b.map_w;
+    const int tid = threadIdx.x;
+    const int x = tid;  // this lane's map row
+    const int words = W * H / 32;
+    const size_t tcells = tiled_cells(W, H);
+    bool ok = e < (uint32_t)b.n_envs && (uint32_t)gx < (uint32_t)W && (uint32_t)gy < (uint32_t)H;
+    const uint32_t* env_bits = b.grid_bits + (size_t)(ok ? e : 0) * words;
+    if (ok && bit_at(env_bits, gx * H + gy)) ok = false;
+    uint64_t vis[HW], pl[kLevelPlanes][HW];
+    int top = 0, overflow = 0;
+#pragma unroll
+    for (int k = 0; k < HW; ++k) {
+        vis[k] = 0;
+#pragma unroll
+        for (int p = 0; p < kLevelPlanes; ++p) pl[p][k] = 0;
+    }
+    if (ok) {
+        uint64_t fr[HW];
+        load_free_row<H>(env_bits, W, x, fr);
+        if (W * H > kMaxFrontier + 1) {
+            overflow = group_bfs_planes<H, R, true>(fr, gx, gy, vis, pl, top, s_words);
+        } else {
+            overflow = group_bfs_planes<H, R, false>(fr, gx, gy, vis, pl, top, s_words);
+        }
+    }
+    // greedy mask at (spx, spy): the owners of the cell and of its four
+    // neighbours publish their levels (slots: cell, x - 1, x + 1, y - 1, y + 1)
+    const bool on_map = (uint32_t)spx < (uint32_t)W && (uint32_t)spy < (uint32_t)H;
+    if (on_map) {
+        if (x == spx) {
+            s_gm[0] = plane_level<H>(vis, pl, spy);
+            s_gm[3] = spy > 0 ? plane_level<H>(vis, pl, spy - 1) : kUnreachable;
+            s_gm[4] = spy + 1 < H ? plane_level<H>(vis, pl, spy + 1) : kUnreachable;
+        }
+        if (x == spx - 1) s_gm[1] = plane_level<H>(vis, pl, spy);
+        if (x == spx + 1 && x < W) s_gm[2] = plane_level<H>(vis, pl, spy);
+        // neighbours off the map have no owner
+        if (tid == 0 && spx == 0) s_gm[1] = kUnreachable;
+        if (tid == 0 && spx + 1 >= W) s_gm[2] = kUnreachable;
+    }
+    __syncthreads();
+    uint32_t info = ok ? (uint32_t)(overflow < 0xFFFFFF ? overflow : 0xFFFFFF) << kInfoOverflowShift
+                       : kInfoBadGoal;
+    if (on_map) {
+        const uint32_t c0 = s_gm[0];
+        const uint32_t n[4] = {s_gm[1], s_gm[2], s_gm[3], s_gm[4]};
+        uint32_t m = 0;
+#pragma unroll
+        for (int d = 0; d < 4; ++d)
+            if (n[d] != kUnreachable && c0 > n[d]) m |= 8u >> d;
+        info |= m;
+    }
+    // the map's tiles: this lane's row, 8 cells per segment (the border ring
+    // keeps its unreachable cells; rows past W hold no reached cell)
+    const int nplanes = top == 0 ? 0 : 32 - __clz(top);
+    uint4* tout = reinterpret_cast<uint4*>(b.cost_tiles + agent_index * tcells);
+    const int strip_words = (int)(strip_cells(W) / 8u);
+    if (x < (W + 7) / 8 * 8) {
+#pragma unroll
+        for (int k = 0; k < HW; ++k) {
+            const int groups = (H - k * 64) < 64 ? (H - k * 64) / 8 : 8;
+            for (int jj = 0; jj < groups; ++jj) {
+                const int sh = jj * 8;
+                uint64_t lo = 0, hi = 0;
+#pragma unroll
+                for (int p = 0; p < 8; ++p) lo |= ((pl[p][k] >> sh) & 0xFFull) << (8 * p);
+                lo = transpose8x8(lo);
+                if (nplanes > 8) {
+#pragma unroll
+                    for (int p = 0; p < 8; ++p) hi |= ((pl[8 + p][k] >> sh) & 0xFFull) << (8 * p);
+                    hi = transpose8x8(hi);
+                }
+                const uint32_t reached = (uint32_t)(vis[k] >> sh) & 0xFFu;
+                uint32_t w[4];
+#pragma unroll
+                for (int c = 0; c < 8; c += 2) {
+                    uint32_t d0 = (uint32_t)((lo >> (8 * c)) & 0xFF) | ((uint32_t)((hi >> (8 * c)) & 0xFF) << 8);
+                    uint32_t d1 = (uint32_t)((lo >> (8 * c + 8)) & 0xFF) | ((uint32_t)((hi >> (8 * c + 8)) & 0xFF) << 8);
+                    d0 = ((reached >> c) & 1) ? d0 : kUnreachable;
+                    d1 = ((reached >> (c + 1)) & 1) ? d1 : kUnreachable;
+                    w[c / 2] = d0 | (d1 << 16);
+                }
+                const int strip = k * 8 + jj;  // columns 8 strip .. 8 strip + 7
+                tout[(strip + 1) * strip_words + x + 8] = make_uint4(w[0], w[1], w[2], w[3]);
+            }
+        }
+    }
+    __syncthreads();  // s_words and s_gm are rewritten by the next refresh
+    return info;
+}
+
 // ---------------------------------------------------------------------------
 // Pass 1a (maps of more than kMarkedCells cells): unpack + goal-cache refresh
 // + agent info, one lane per agent, no LDS.  An agent whose field is kept
@@ -328,6 +431,36 @@ __global__ __launch_bounds__(kWave* kWaves) void bfs_kernel(jl_mapfgpt_t b, int 
                 b, agent_index, row.x & 0xFFFFu, (int)(row.z & 0xFFFFu), (int)(row.z >> 16),
                 (int)(row.y & 0xFFFFu), (int)(row.y >> 16), s_dist);
             if (lane == src) b.agent_info[agent_index] = (mine & ~(kInfoNeedsBfs | kInfoGreedy)) | bits;
+        }
+    }
+}
+
+// Pass 1b on maps of more than 64 rows: one field at a time per workgroup
+// of R wavefronts (refresh_field_group), workgroup g scanning agents
+// [g * per_group, (g + 1) * per_group).
+template <int H, int R>
+__global__ __launch_bounds__(kWave* R) void bfs_group_kernel(jl_mapfgpt_t b, int per_group) {
+    __shared__ uint64_t s_words[group_bfs_words<H, R>()];
+    __shared__ uint32_t s_gm[8];
+    const int N = b.n_envs * b.n_agents;
+    const int tid = threadIdx.x;
+    const int lane = tid & (kWave - 1);
+    const int begin = blockIdx.x * per_group;
+    const int end = (begin + per_group) < N ? (begin + per_group) : N;
+    for (int c0 = begin; c0 < end; c0 += kWave) {
+        // every wavefront reads the same 64 info words, so the ballots agree
+        const int i = c0 + lane;
+        const uint32_t mine = i < end ? b.agent_info[i] : 0u;
+        uint64_t todo = __ballot((mine & kInfoNeedsBfs) != 0);
+        while (todo) {
+            const int src = __ffsll((unsigned long long)todo) - 1;
+            todo &= todo - 1;
+            const size_t agent_index = (size_t)c0 + src;
+            const uint4 row = *reinterpret_cast<const uint4*>(b.state_packed + agent_index * 8);
+            const uint32_t bits = refresh_field_group<H, R>(
+                b, agent_index, row.x & 0xFFFFu, (int)(row.z & 0xFFFFu), (int)(row.z >> 16),
+                (int)(row.y & 0xFFFFu), (int)(row.y >> 16), s_words, s_gm);
+            if (tid == src) b.agent_info[agent_index] = (mine & ~(kInfoNeedsBfs | kInfoGreedy)) | bits;
         }
     }
 }
@@ -1542,6 +1675,17 @@ int launch_pass1(const jl_mapfgpt_t* b, const int16_t* rows, const int16_t* cx, 
                        dim3(kUnpackThreads), 0, stream, *b, rows, cx, cy, gx, gy);
     int rc = launch_status();
     if (rc) return rc;
+    if constexpr (R > 1) {
+        // one field per workgroup of R wavefronts, the levels in registers:
+        // two workgroups per CU
+        const int max_groups = (N + kWave - 1) / kWave;
+        int groups = device_cus() * 2;
+        if (groups > max_groups) groups = max_groups;
+        const int per_group = ((N + groups - 1) / groups + kWave - 1) / kWave * kWave;
+        hipLaunchKernelGGL((bfs_group_kernel<H, R>), dim3((N + per_group - 1) / per_group), dim3(kWave * R), 0,
+                           stream, *b, per_group);
+        return launch_status();
+    }
     const int waves = pass1_waves(b->map_w, H);
     const size_t lds = (size_t)waves * b->map_w * H * sizeof(uint16_t);
     const int per_cu = (int)(160 * 1024 / lds) < 8 ? (int)(160 * 1024 / lds) : 8;
