@@ -654,6 +654,8 @@ def run_gpu_magat(args) -> dict:
         if ev is not None:
             ev[1].record()
         sim.finalize_magat_plus_graph()
+        if ev is not None:
+            ev[2].record()
 
     print("[bench] warmup (the first step builds every energy field)", file=sys.stderr, flush=True)
     for s in range(args.warmup):
@@ -665,8 +667,7 @@ def run_gpu_magat(args) -> dict:
 
         graph = MagatStatefulGraph(sim)
     # all kernels run on torch's current stream, so torch events bracket the node pass
-    node_events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-                   for _ in range(args.steps)]
+    node_events = [tuple(torch.cuda.Event(enable_timing=True) for _ in range(3)) for _ in range(args.steps)]
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(args.steps):
@@ -684,7 +685,9 @@ def run_gpu_magat(args) -> dict:
         for i, ev in enumerate(node_events):
             one_step((args.warmup + i) % total_steps, ev)
         torch.cuda.synchronize()
-    node_ms = [a.elapsed_time(b) for a, b in node_events]
+    node_ms = [a.elapsed_time(b) for a, b, _ in node_events]
+    # the graph pass: env scan + edge writer (finalize_magat_plus_graph)
+    graph_ms = [b.elapsed_time(c) for _, b, c in node_events]
     N = E * A
     value = N * args.steps / wall
     node_s = float(np.mean(node_ms)) / 1000.0
@@ -705,6 +708,7 @@ def run_gpu_magat(args) -> dict:
             "avg_launch_us": node_s * 1e6,
         },
         "edges_per_step": int(sim.pyg_num_edges.item()),
+        "graph_us": float(np.mean(graph_ms)) * 1e3,
         "device": torch.cuda.get_device_name(0),
     }
 
@@ -739,6 +743,7 @@ def main_magat(args) -> int:
         "roofline": res["roofline"],
         "cpu_baseline": base,
         "edges_per_step": res["edges_per_step"],
+        "graph_us": res["graph_us"],
         "device": res["device"],
     }
     print(json.dumps(line), flush=True)

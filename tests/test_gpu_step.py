@@ -388,6 +388,11 @@ def test_c2_full_size_invariants():
                    torch.zeros((E, A), dtype=torch.uint8, device="cuda"), torch.zeros(E, dtype=torch.int32, device="cuda"))
     gt = g.bool()
     gen = torch.Generator(device="cuda").manual_seed(3)
+    index = torch.arange(A, device="cuda").expand(E, A)
+    # Action deltas: 0 stay, 1 x-1, 2 x+1, 3 y-1, 4 y+1.
+    DX = torch.tensor([0, -1, 1, 0, 0], device="cuda")
+    DY = torch.tensor([0, 0, 0, -1, 1], device="cuda")
+    swaps_seen = 0
     for _ in range(16):
         before = torch.stack([sim.cur_x, sim.cur_y], -1).long()
         acts = torch.randint(0, 5, (E, A), dtype=torch.uint8, device="cuda", generator=gen)
@@ -399,3 +404,104 @@ def test_c2_full_size_invariants():
         assert not bool((srt[:, 1:] == srt[:, :-1]).any()), "shared cell"
         assert not bool(gt[torch.arange(E, device="cuda")[:, None], after[..., 0], after[..., 1]].any())
         assert bool(((after - before).abs().sum(-1) <= 1).all())
+        # No swap: agent i entering the cell agent j left while j enters i's
+        # old cell.  who[e, c] = agent that stood on cell c before the step.
+        prev = before[..., 0] * W + before[..., 1]
+        who = torch.full((E, W * W), -1, dtype=torch.long, device="cuda").scatter_(1, prev, index)
+        j = who.gather(1, cells)
+        moved = (cells != prev) & (j >= 0)
+        swapped = moved & (cells.gather(1, j.clamp(min=0)) == prev)
+        assert not bool(swapped.any()), f"swap at {swapped.nonzero()[:4].tolist()}"
+        # The actions did ask for swaps: facing neighbours with opposite moves.
+        want = torch.stack([before[..., 0] + DX[acts.long()], before[..., 1] + DY[acts.long()]], -1)
+        wc = (want[..., 0].clamp(0, W - 1) * W + want[..., 1].clamp(0, W - 1))
+        jw = who.gather(1, wc)
+        swaps_seen += int(((jw >= 0) & (jw != index) & (wc != prev)
+                           & (wc.gather(1, jw.clamp(min=0)) == prev)).sum())
+    assert swaps_seen > 0, "no swap was requested; the invariant was not exercised"
+
+
+def test_c2_full_horizon_sampled_envs_match_oracle(oracle):
+    """C2 at full size over the whole 512-step horizon (and 4 steps past it):
+    three sampled envs compared with the oracle after every step."""
+    from iclr_2027_jointoom_amd.synthetic import make_batch
+
+    E, W, A, T = 1024, 64, 128, 512
+    sample = [0, 517, 1023]
+    grids, starts, goals = make_batch(2026, E, W, W, A)
+    ext = ext_for(W, W)
+    g = torch.from_numpy(grids.astype(np.int32)).cuda()
+    sim = ext.GridWorldSimulator(g, A, 0, E * W * W, 7, "standard_mapf", T)
+    sim.load_state(torch.from_numpy(starts).cuda(), torch.from_numpy(goals).cuda(),
+                   torch.zeros((E, A), dtype=torch.uint8, device="cuda"), torch.zeros(E, dtype=torch.int32, device="cuda"))
+    osim = oracle.OracleSim(grids[sample], A, task_mode=1, max_episode_steps=T)
+    osim.load_state(starts[sample], goals[sample])
+    rng = np.random.default_rng(512)
+    idx = torch.tensor(sample, device="cuda")
+    rows = (idx[:, None] * A + torch.arange(A, device="cuda")).reshape(-1)
+    for step in range(T + 4):
+        acts = rng.integers(0, 5, size=(E, A), dtype=np.uint8)
+        sim.update_actions(torch.from_numpy(acts).cuda())
+        sim.step_sim_only()
+        osim.step(acts[sample])
+        pairs = [
+            ("cur_x", sim.cur_x[idx], osim.cur_x.astype(np.int16)),
+            ("cur_y", sim.cur_y[idx], osim.cur_y.astype(np.int16)),
+            ("outcomes", sim.outcomes[idx], osim.outcomes),
+            ("arrived", sim.arrived[idx], osim.arrived),
+            ("terminated", sim.terminated[idx], osim.terminated),
+            ("truncated", sim.truncated[idx], osim.truncated),
+            ("step_counts", sim.step_counts[idx], osim.step_counts),
+            ("rewards", sim.rewards[idx], osim.rewards),
+            ("grid_ocp", sim.grid_ocp[idx], osim.grid_ocp.view(np.int32)),
+            ("state_packed", sim.state_packed[rows, 1:], osim.state_packed.view(np.int16)[:, 1:]),
+            ("goal_changed", sim.goal_changed_flags[idx], osim.goal_changed),
+        ]
+        for name, got, exp in pairs:
+            got = got.cpu().numpy()
+            assert np.array_equal(got, exp), f"step {step} {name} differs at {np.argwhere(got != exp)[:5].tolist()}"
+        env_col = sim.state_packed[rows, 0].cpu().numpy()
+        assert np.array_equal(env_col, np.repeat(np.array(sample, np.int16), A))
+    assert bool((osim.truncated | osim.terminated).all())
+    assert int(sim.step_counts.max()) <= T
+
+
+@pytest.mark.parametrize("W,H", [(32, 32), (7, 128), (64, 64), (256, 256)])
+def test_encode_map_matches_closed_form_on_gpu(W, H):
+    """jl_encode_map (grid_world_cuda.cu:112-183): bit (x*H + y) & 31 of word
+    (x*H + y) >> 5 is set iff grid[x, y] != 0, for any nonzero cell value."""
+    ext = ext_for(W, H)
+    gen = torch.Generator().manual_seed(W * 1000 + H)
+    E = 3
+    values = torch.randint(1, 7, (E, W, H), generator=gen, dtype=torch.int32)
+    grids = torch.where(torch.rand((E, W, H), generator=gen) < 0.3, values, torch.zeros_like(values))
+    grids[0] = 0
+    grids[1, 0, :] = 5
+    sim = ext.GridWorldSimulator(grids.cuda(), 2, 0, E * W * H, 7, "standard_mapf", 8)
+    torch.cuda.synchronize()
+    bits = sim.memory_tensors["grid_compressed"].cpu().numpy().view(np.uint32)
+    assert bits.shape == (E, W * H // 32)
+    cells = np.arange(W * H)
+    got = (bits[:, cells >> 5] >> (cells & 31).astype(np.uint32)) & 1
+    assert np.array_equal(got.reshape(E, W, H), (grids.numpy() != 0).astype(np.uint32))
+
+
+def test_decode_to_uint8_unpacks_rows():
+    """decode_to_uint8 (grid_world_cuda.cu:186-210): out[b, c, r, k] is bit k
+    of the packed row agents_obs[b, c, r]."""
+    ext = ext_for(32, 32)
+    E, A = 3, 5
+    sim = _sim(ext, num_envs=E, num_agents=A, task_mode="standard_mapf")
+    obs = sim.agents_obs
+    n, feats, d = obs.shape
+    assert n == E * A and feats >= 2
+    packed = torch.randint(0, 1 << 16, (n, feats, d), generator=torch.Generator().manual_seed(9), dtype=torch.int32)
+    packed[0] = 0xFFFF
+    packed[1] = 0
+    obs.copy_(torch.from_numpy(packed.numpy().astype(np.uint16).view(np.int16)).cuda())
+    out = sim.decode_to_uint8()
+    torch.cuda.synchronize()
+    assert out.shape == (n, 2, d, d) and out.dtype == torch.uint8
+    rows = packed[:, :2].numpy().astype(np.uint32)
+    want = (rows[..., None] >> np.arange(d, dtype=np.uint32)) & 1
+    assert np.array_equal(out.cpu().numpy(), want.astype(np.uint8))
