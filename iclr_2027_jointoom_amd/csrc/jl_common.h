@@ -30,6 +30,14 @@ constexpr int kPygArea = 169;
 constexpr int kPygFeatures = 4 * kPygArea;
 constexpr int kCommRadiusSq = 49;
 
+// Squared distance as the reference's 32-bit int arithmetic yields it for
+// any int16 positions: products and sum wrap modulo 2^32 (done in unsigned,
+// where the wrap is defined), so two agents near opposite int16 extremes can
+// test as neighbours there too (stateless_step.cu:513-520, :889).
+__device__ __forceinline__ int wrap_dist2(int dx, int dy) {
+    return (int)((uint32_t)dx * (uint32_t)dx + (uint32_t)dy * (uint32_t)dy);
+}
+
 // Scratch layout of jl_mapfgpt_t::scratch: diagnostics accumulated by a
 // build, then published by the last workgroup of the token kernel.
 constexpr int kScratchAccum = 0;     // [0..3]

@@ -9,16 +9,18 @@
 // 414-421, 438-478).  The clamped ctg value is one of 21 float constants k/10
 // (the IEEE quotients), so no division is evaluated on the device.
 // edges: per-env edge totals (from the node pass) -> one-workgroup scan ->
-// per (env, 64-source slice) writer: one wavefront per source tests the
-// others 64 at a time and the neighbours write their edges at consecutive
-// offsets, sorted by (source, destination id) (grid_world_cuda.cu:17-110,
-// stateless_step.cu:854-935).
+// per (env, 64-source slice) writer: each wavefront takes 16 consecutive
+// sources, tests the others 256 at a time and queues the neighbours in LDS;
+// they leave 64 edges per store, sorted by (source, destination id)
+// (grid_world_cuda.cu:17-110, stateless_step.cu:854-935).
 #include "jl_common.h"
 
 namespace jl {
 namespace {
 
 constexpr int kNodeThreads = 256;
+
+typedef short jl_v2s __attribute__((ext_vector_type(2)));  // (x, y) as packed int16
 
 // (float)k / 10.0f rounded to nearest even, k = -10..10.
 __device__ __constant__ float kTenths[21] = {-1.0f, -0.9f, -0.8f, -0.7f, -0.6f, -0.5f, -0.4f,
@@ -115,13 +117,13 @@ __host__ __device__ inline NodeLayout node_layout(int A, int W, int H) {
 }
 
 // Workgroup = (env, slice of kNodeEgos agents).  Every slice stages the env's
-// bitmaps and agents in LDS; the env's first slice also counts every agent's
-// neighbours within squared radius 49 (others split over its wavefronts) and
-// writes the env total for the scan.  Then one wavefront per agent row: lane
-// l holds patch cells l, l + 64, l + 128 of the 13x13 patch, loads its own
-// energy byte and stores the four channels (obstacle, agents, goal, ctg) of
-// its cells as dwords; the next agent's energy bytes are requested before
-// the current row is produced.
+// bitmaps and agents in LDS, issues the loads of its agents' energy windows,
+// counts its agents' neighbours within squared radius 49 while they are in
+// flight (others split over the wavefronts) and writes the slice total for
+// the scan.  Then one wavefront per agent row: lane l holds patch cells l,
+// l + 64, l + 128 of the 13x13 patch and writes the four channels (obstacle,
+// agents, goal, ctg) of its cells into an LDS row that leaves as 16-byte
+// stores.
 template <int H>
 __global__ __launch_bounds__(kNodeThreads) void nodes_kernel(jl_magat_t m) {
     extern __shared__ __align__(16) uint8_t smem[];
@@ -148,9 +150,12 @@ __global__ __launch_bounds__(kNodeThreads) void nodes_kernel(jl_magat_t m) {
         s_st[k] = m.grid_bits[(size_t)env * words + k];
         s_oc[k] = m.grid_ocp[(size_t)env * words + k];
     }
+    int wide = 0;  // a position outside [-8192, 8191]: counts in 32-bit arithmetic
     for (int a = tid; a < A; a += kNodeThreads) {
         const uint4 r = *reinterpret_cast<const uint4*>(m.states + (base + a) * 8);
         s_pos[a] = (int32_t)r.y;
+        const int x = (int16_t)(r.y & 0xFFFFu), y = (int16_t)(r.y >> 16);
+        wide |= (x < -8192 || x > 8191 || y < -8192 || y > 8191) ? 1 : 0;
         s_valid[a] = (r.x & 0xFFFFu) < (uint32_t)E ? 1 : 0;
         if (a >= e_begin && a < e_end) {
             s_part[a - e_begin] = 0;
@@ -158,25 +163,92 @@ __global__ __launch_bounds__(kNodeThreads) void nodes_kernel(jl_magat_t m) {
                                                         (int16_t)(r.z & 0xFFFFu), (int16_t)(r.z >> 16));
         }
     }
-    __syncthreads();
+    wide = __syncthreads_or(wide);
+
+    // Energy windows of the slice: item i = (agent i / 11, window row i % 11).
+    // The row's 11 bytes lie in two aligned 16-byte words of the field row,
+    // read with two vector loads at clamped addresses (a word off the map or
+    // off the row reads as 0), then shifted into place and stored as one
+    // 16-byte LDS word.  Every thread has at most kWinItems items (a slice of
+    // kNodeEgos agents); an item past the slice repeats item 0 (same bytes,
+    // same LDS address).  The loads are issued here and consumed after the
+    // neighbour count, which runs while they are in flight.
+    uint8_t* s_win = smem + L.win_off;
+    float* s_tenths = reinterpret_cast<float*>(smem + L.tenths_off);
+    if (tid < 21) s_tenths[tid] = kTenths[tid];
+    const uint8_t* env_energy = m.energy + base * cells;
+    const int nitems = (e_end - e_begin) * kDiam;
+    uint4 lo[kWinItems], hi[kWinItems];
+    int shift[kWinItems], dst[kWinItems];
+    bool ok_lo[kWinItems], ok_hi[kWinItems];
+#pragma unroll
+    for (int it = 0; it < kWinItems; ++it) {
+        const int i = tid + it * kNodeThreads < nitems ? tid + it * kNodeThreads : 0;
+        const int el = i / kDiam, r = i - el * kDiam;
+        const int a = e_begin + el;
+        const int32_t pos = s_pos[a];
+        const int x = (int16_t)(pos & 0xFFFF) + r - kRadius;
+        const int y0 = (int16_t)(pos >> 16) - kRadius;
+        const bool rok = s_valid[a] && x >= 0 && x < W;
+        const int c0 = y0 >> 4;  // word of column y0 (-1 for the columns left of the map)
+        ok_lo[it] = rok && c0 >= 0 && c0 < H / 16;
+        ok_hi[it] = rok && c0 + 1 >= 0 && c0 + 1 < H / 16;
+        const uint4* row4 =
+            reinterpret_cast<const uint4*>(env_energy + (size_t)a * cells + (size_t)(rok ? x : 0) * H);
+        lo[it] = row4[ok_lo[it] ? c0 : 0];
+        hi[it] = row4[ok_hi[it] ? c0 + 1 : 0];
+        shift[it] = y0 - c0 * 16;  // 0..15: byte of column y0 in lo
+        dst[it] = el * kWinStride + r * kWinRow;
+    }
 
     // Edge counts of the slice: others within squared radius 49, all rows of
-    // the env block (stateless_step.cu:511-520), lane = agent of the slice,
-    // the others split over the wavefronts.  Rows that are skipped keep their
-    // previous count, which the totals still include; each slice writes its
-    // total, and the scan adds the env's slices.
+    // the env block (stateless_step.cu:513-520), lane = agent of the slice,
+    // the others split over the wavefronts.  With every position in
+    // [-8192, 8191] the differences fit packed int16 and the test is the sign
+    // of one dot2 (the agent itself, at distance 0, is taken off after);
+    // otherwise 32-bit arithmetic with the reference's wrap.  Rows that are
+    // skipped keep their previous count, which the totals still include; each
+    // slice writes its total, and the scan adds the env's slices.
     {
         const int a = e_begin + lane;
         if (a < e_end) {
-            const int cx = (int16_t)(s_pos[a] & 0xFFFF), cy = (int16_t)(s_pos[a] >> 16);
+            const int32_t me_xy = s_pos[a];
             int count = 0;
-            for (int o = wave; o < A; o += nwaves) {
-                const int ox = (int16_t)(s_pos[o] & 0xFFFF), oy = (int16_t)(s_pos[o] >> 16);
-                const int dx = cx - ox, dy = cy - oy;
-                count += (o != a && dx * dx + dy * dy <= kCommRadiusSq) ? 1 : 0;
+            if (!wide) {
+                const jl_v2s me = __builtin_bit_cast(jl_v2s, me_xy);
+#pragma unroll 8
+                for (int o = wave; o < A; o += nwaves) {
+                    const jl_v2s d = me - __builtin_bit_cast(jl_v2s, s_pos[o]);
+                    count += (int)((uint32_t)__builtin_amdgcn_sdot2(d, d, -(kCommRadiusSq + 1), false) >> 31);
+                }
+                if (a % nwaves == wave) count -= 1;
+            } else {
+                const int cx = (int16_t)(me_xy & 0xFFFF), cy = (int16_t)(me_xy >> 16);
+                for (int o = wave; o < A; o += nwaves) {
+                    const int ox = (int16_t)(s_pos[o] & 0xFFFF), oy = (int16_t)(s_pos[o] >> 16);
+                    count += (o != a && wrap_dist2(cx - ox, cy - oy) <= kCommRadiusSq) ? 1 : 0;
+                }
             }
             if (count) atomicAdd(&s_part[lane], count);
         }
+    }
+#pragma unroll
+    for (int it = 0; it < kWinItems; ++it) {
+        // bytes shift .. shift + 11 of the 32 bytes lo:hi
+        const uint4 l = ok_lo[it] ? lo[it] : make_uint4(0u, 0u, 0u, 0u);
+        const uint4 h = ok_hi[it] ? hi[it] : make_uint4(0u, 0u, 0u, 0u);
+        const uint32_t w = (uint32_t)shift[it] >> 2, b = (uint32_t)shift[it] & 3u;
+        const uint32_t d[8] = {l.x, l.y, l.z, l.w, h.x, h.y, h.z, h.w};
+        uint32_t sel[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            sel[q] = w == 0 ? d[q] : (w == 1 ? d[q + 1] : (w == 2 ? d[q + 2] : d[q + 3]));
+        uint4 v;
+        v.x = __builtin_amdgcn_alignbyte(sel[1], sel[0], b);
+        v.y = __builtin_amdgcn_alignbyte(sel[2], sel[1], b);
+        v.z = __builtin_amdgcn_alignbyte(sel[3], sel[2], b);
+        v.w = 0u;
+        *reinterpret_cast<uint4*>(s_win + dst[it]) = v;
     }
     __syncthreads();
     if (wave == 0) {
@@ -193,62 +265,6 @@ __global__ __launch_bounds__(kNodeThreads) void nodes_kernel(jl_magat_t m) {
         for (int off = kWave / 2; off > 0; off >>= 1) count += __shfl_xor(count, off, kWave);
         if (lane == 0) m.env_edge_base[E + 1 + (size_t)env * parts + part] = count;
     }
-
-    // Energy windows of the slice: item i = (agent i / 11, window row i % 11).
-    // The row's 11 bytes lie in two aligned 16-byte words of the field row,
-    // read with two vector loads at clamped addresses (a word off the map or
-    // off the row reads as 0), then shifted into place and stored as one
-    // 16-byte LDS word.  Every thread has at most kWinItems items (a slice of
-    // kNodeEgos agents); an item past the slice repeats item 0 (same bytes,
-    // same LDS address), so all loads are issued before the first wait, and
-    // the row phase below reads LDS only, so its stores are never waited on.
-    uint8_t* s_win = smem + L.win_off;
-    float* s_tenths = reinterpret_cast<float*>(smem + L.tenths_off);
-    if (tid < 21) s_tenths[tid] = kTenths[tid];
-    {
-        const uint8_t* env_energy = m.energy + base * cells;
-        const int nitems = (e_end - e_begin) * kDiam;
-        uint4 lo[kWinItems], hi[kWinItems];
-        int shift[kWinItems], dst[kWinItems];
-#pragma unroll
-        for (int it = 0; it < kWinItems; ++it) {
-            const int i = tid + it * kNodeThreads < nitems ? tid + it * kNodeThreads : 0;
-            const int el = i / kDiam, r = i - el * kDiam;
-            const int a = e_begin + el;
-            const int32_t pos = s_pos[a];
-            const int x = (int16_t)(pos & 0xFFFF) + r - kRadius;
-            const int y0 = (int16_t)(pos >> 16) - kRadius;
-            const bool rok = s_valid[a] && x >= 0 && x < W;
-            const int c0 = y0 >> 4;  // word of column y0 (-1 for the columns left of the map)
-            const bool ok0 = rok && c0 >= 0 && c0 < H / 16;
-            const bool ok1 = rok && c0 + 1 >= 0 && c0 + 1 < H / 16;
-            const uint4* row4 =
-                reinterpret_cast<const uint4*>(env_energy + (size_t)a * cells + (size_t)(rok ? x : 0) * H);
-            const uint4 l = row4[ok0 ? c0 : 0], h = row4[ok1 ? c0 + 1 : 0];
-            lo[it] = ok0 ? l : make_uint4(0u, 0u, 0u, 0u);
-            hi[it] = ok1 ? h : make_uint4(0u, 0u, 0u, 0u);
-            shift[it] = y0 - c0 * 16;  // 0..15: byte of column y0 in lo
-            dst[it] = el * kWinStride + r * kWinRow;
-        }
-#pragma unroll
-        for (int it = 0; it < kWinItems; ++it) {
-            // bytes shift .. shift + 11 of the 32 bytes lo:hi
-            const uint32_t w = (uint32_t)shift[it] >> 2, b = (uint32_t)shift[it] & 3u;
-            const uint32_t d[8] = {lo[it].x, lo[it].y, lo[it].z, lo[it].w,
-                                   hi[it].x, hi[it].y, hi[it].z, hi[it].w};
-            uint32_t sel[4];
-#pragma unroll
-            for (int q = 0; q < 4; ++q)
-                sel[q] = w == 0 ? d[q] : (w == 1 ? d[q + 1] : (w == 2 ? d[q + 2] : d[q + 3]));
-            uint4 v;
-            v.x = __builtin_amdgcn_alignbyte(sel[1], sel[0], b);
-            v.y = __builtin_amdgcn_alignbyte(sel[2], sel[1], b);
-            v.z = __builtin_amdgcn_alignbyte(sel[3], sel[2], b);
-            v.w = 0u;
-            *reinterpret_cast<uint4*>(s_win + dst[it]) = v;
-        }
-    }
-    __syncthreads();
 
     // Rows: one wavefront per agent; lane l owns patch cells l, l + 64,
     // l + 128 (p < 169) of the 13x13 patch, whose rows and columns 1..11 are
@@ -353,32 +369,41 @@ __global__ __launch_bounds__(1024) void env_scan_kernel(jl_magat_t m) {
 
 constexpr int kEdgeThreads = 256;
 constexpr int kEdgeSources = 64;  // sources per edge workgroup
+constexpr int kEdgeWaves = kEdgeThreads / kWave;
+constexpr int kEdgeBlock = kEdgeSources / kEdgeWaves;  // consecutive sources per wavefront
 constexpr int kEdgeUnroll = 4;    // 64-candidate chunks tested per step
 constexpr int kEdgeSpan = kWave * kEdgeUnroll;
+constexpr int kEdgeRing = 512;    // pending edges per wavefront: >= (kWave - 1) + kEdgeSpan
+static_assert(kEdgeRing >= kWave - 1 + kEdgeSpan && (kEdgeRing & (kEdgeRing - 1)) == 0, "edge ring");
 
 // Edge workgroup LDS: positions padded to a multiple of kEdgeSpan with cells
-// far off every map (never within the radius), the env's counts, and one
-// neighbour list of up to A ids per wavefront.
+// far off every map (never within the radius), one ring of pending edges per
+// wavefront, then the env's counts.
 __host__ __device__ inline size_t edge_lds(int A) {
     const size_t padded = (size_t)(A + kEdgeSpan - 1) / kEdgeSpan * kEdgeSpan;
-    return padded * 4 + (size_t)A * 4 + (size_t)(kEdgeThreads / kWave) * A * 4;
+    return padded * 4 + (size_t)kEdgeWaves * kEdgeRing * 8 + (size_t)A * 4;
 }
 
 // Workgroup = (env, slice of kEdgeSources sources).  The env's positions and
 // counts are staged in LDS in one round trip; the slice's first edge offsets
 // are the env's scanned base plus the counts before the slice plus a scan
-// over the slice.  One wavefront per source tests the others kEdgeSpan at a
-// time (32-bit differences: positions are any int16), appends each chunk's
-// neighbours to its LDS list in lane (= id) order, then writes the source's
-// edges from consecutive lanes: edges are ordered by (source, destination
-// id), the reference's order (stateless_step.cu:854-935).
+// over the slice.  Wavefront w takes kEdgeBlock consecutive sources, so its
+// edges fill one contiguous range: each source tests the others kEdgeSpan at
+// a time (32-bit differences: positions are any int16) and queues its
+// neighbours, in id order, in the wavefront's LDS ring as (source, id,
+// output offset); whenever 64 are queued they leave with every lane storing
+// one edge (the neighbour count is about 9 at C4 density, so a store per
+// source would run with a seventh of the lanes).  Edges are ordered by
+// (source, destination id), the reference's order (stateless_step.cu:
+// 854-935); each sits at its source's first offset plus its rank.
 __global__ __launch_bounds__(kEdgeThreads) void edges_kernel(jl_magat_t m) {
     extern __shared__ __align__(16) int32_t s_xy[];  // (int16 x, int16 y) per agent, padded
-    __shared__ long long s_wave[kEdgeThreads / kWave];
+    __shared__ long long s_wave[kEdgeWaves];
     __shared__ long long s_first[kEdgeSources];
     const int A = m.n_agents;
     const int padded = (A + kEdgeSpan - 1) / kEdgeSpan * kEdgeSpan;
-    int32_t* s_cnt = s_xy + padded;
+    int2* s_ring = reinterpret_cast<int2*>(s_xy + padded);
+    int32_t* s_cnt = reinterpret_cast<int32_t*>(s_ring + kEdgeWaves * kEdgeRing);
     const int parts = (A + kEdgeSources - 1) / kEdgeSources;
     const int env = blockIdx.x / parts;
     const int part = blockIdx.x - env * parts;
@@ -386,8 +411,6 @@ __global__ __launch_bounds__(kEdgeThreads) void edges_kernel(jl_magat_t m) {
     const int s_end = (s_begin + kEdgeSources) < A ? (s_begin + kEdgeSources) : A;
     const int tid = threadIdx.x, lane = tid & (kWave - 1);
     const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);  // uniform per wavefront
-    constexpr int nwaves = kEdgeThreads / kWave;
-    int32_t* my_list = s_cnt + A + wave * A;
     const size_t base = (size_t)env * A;
     for (int a = tid; a < padded; a += kEdgeThreads) {
         int32_t xy = 0x40004000;  // padding: (16384, 16384)
@@ -409,7 +432,7 @@ __global__ __launch_bounds__(kEdgeThreads) void edges_kernel(jl_magat_t m) {
     __syncthreads();
     if (wave == 0) {
         long long first = env_base;
-        for (int k = 0; k < nwaves; ++k) first += s_wave[k];
+        for (int k = 0; k < kEdgeWaves; ++k) first += s_wave[k];
         const int a = s_begin + lane;
         const long long c = a < s_end ? s_cnt[a] : 0;
         long long incl = c;
@@ -425,44 +448,19 @@ __global__ __launch_bounds__(kEdgeThreads) void edges_kernel(jl_magat_t m) {
     __syncthreads();
     const long long cap = m.edge_capacity;
     int64_t* dst_index = m.edge_index + cap;
-    for (int a = s_begin + wave; a < s_end; a += nwaves) {
-        const long long first = s_first[a - s_begin];
-        const int32_t sxy = s_xy[a];
-        const int cx = (int16_t)(sxy & 0xFFFF), cy = sxy >> 16;
-        int n = 0;
-        for (int o0 = 0; o0 < padded; o0 += kEdgeSpan) {
-            const int32_t* row = s_xy + o0 + lane;
-            uint64_t bal[kEdgeUnroll];
-#pragma unroll
-            for (int u = 0; u < kEdgeUnroll; ++u) {
-                const int32_t oxy = row[u * kWave];
-                const int dx = cx - (int16_t)(oxy & 0xFFFF);
-                const int dy = cy - (oxy >> 16);
-                bal[u] = __ballot(dx * dx + dy * dy <= kCommRadiusSq);
-                // the source itself
-                const int self = a - (o0 + u * kWave);
-                if (self >= 0 && self < kWave) bal[u] &= ~(1ull << self);
-            }
-#pragma unroll
-            for (int u = 0; u < kEdgeUnroll; ++u) {
-                if (bal[u]) {
-                    if ((bal[u] >> lane) & 1ull)
-                        my_list[n + (int)__builtin_amdgcn_mbcnt_hi(
-                                        (uint32_t)(bal[u] >> 32),
-                                        __builtin_amdgcn_mbcnt_lo((uint32_t)bal[u], 0u))] =
-                            o0 + u * kWave + lane;
-                    n += __popcll(bal[u]);
-                }
-            }
-        }
+    const long long slice_first = s_first[0];
+    int2* ring = s_ring + wave * kEdgeRing;
+    // Stores `count` queued edges from ring position `from`, one per lane.
+    auto flush = [&](int from, int count) {
         wave_sync();
-        for (int i = lane; i < n; i += kWave) {
-            const int o = my_list[i];
-            const long long e = first + i;
+        if (lane < count) {
+            const int2 ent = ring[(from + lane) & (kEdgeRing - 1)];
+            const int o = ent.x & 0xFFFF, a = s_begin + (ent.x >> 16);
+            const long long e = slice_first + ent.y;
             if (e >= 0 && e < cap) {
-                const int32_t oxy = s_xy[o];
-                const int dx = cx - (int16_t)(oxy & 0xFFFF);
-                const int dy = cy - (oxy >> 16);
+                const int32_t sxy = s_xy[a], oxy = s_xy[o];
+                const int dx = (int16_t)(sxy & 0xFFFF) - (int16_t)(oxy & 0xFFFF);
+                const int dy = (sxy >> 16) - (oxy >> 16);
                 m.edge_index[e] = (int64_t)(base + a);
                 dst_index[e] = (int64_t)(base + o);
                 float* attr = m.edge_attr + e * 3;
@@ -471,7 +469,214 @@ __global__ __launch_bounds__(kEdgeThreads) void edges_kernel(jl_magat_t m) {
                 attr[2] = (float)((dx < 0 ? -dx : dx) + (dy < 0 ? -dy : dy));
             }
         }
-        wave_sync();  // the list is rewritten by the next source
+    };
+    const int a_begin = s_begin + wave * kEdgeBlock;
+    const int a_end = (a_begin + kEdgeBlock) < s_end ? (a_begin + kEdgeBlock) : s_end;
+    int head = 0, tail = 0;  // queued / stored edges of the wavefront (uniform)
+    for (int a = a_begin; a < a_end; ++a) {
+        const int sl = a - s_begin;
+        const int first_rel = (int)(s_first[sl] - slice_first);
+        const int32_t sxy = s_xy[a];
+        const int cx = (int16_t)(sxy & 0xFFFF), cy = sxy >> 16;
+        int n = 0;  // neighbours of a queued so far
+        for (int o0 = 0; o0 < padded; o0 += kEdgeSpan) {
+            const int32_t* row = s_xy + o0 + lane;
+            uint64_t bal[kEdgeUnroll];
+#pragma unroll
+            for (int u = 0; u < kEdgeUnroll; ++u) {
+                const int32_t oxy = row[u * kWave];
+                const int dx = cx - (int16_t)(oxy & 0xFFFF);
+                const int dy = cy - (oxy >> 16);
+                bal[u] = __ballot(wrap_dist2(dx, dy) <= kCommRadiusSq && o0 + u * kWave + lane < A);
+                // the source itself
+                const int self = a - (o0 + u * kWave);
+                if (self >= 0 && self < kWave) bal[u] &= ~(1ull << self);
+            }
+#pragma unroll
+            for (int u = 0; u < kEdgeUnroll; ++u) {
+                if (bal[u]) {
+                    if ((bal[u] >> lane) & 1ull) {
+                        const int rank = (int)__builtin_amdgcn_mbcnt_hi(
+                            (uint32_t)(bal[u] >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)bal[u], 0u));
+                        ring[(head + rank) & (kEdgeRing - 1)] =
+                            make_int2((sl << 16) | (o0 + u * kWave + lane), first_rel + n + rank);
+                    }
+                    const int c = __popcll(bal[u]);
+                    head += c;
+                    n += c;
+                }
+            }
+            while (head - tail >= kWave) {
+                flush(tail, kWave);
+                tail += kWave;
+            }
+        }
+    }
+    if (head > tail) flush(tail, head - tail);
+}
+
+constexpr int kMaskMaxAgents = 1024;  // mask writer: at most 16 64-id chunks per source
+
+// Mask writer LDS: per (64-id chunk, source of the slice) neighbour bits,
+// then the positions padded to whole chunks, then the env's counts.
+__host__ __device__ inline size_t edge_mask_lds(int A) {
+    const size_t chunks = (size_t)(A + kWave - 1) / kWave;
+    return chunks * kEdgeSources * 8 + chunks * kWave * 4 + (size_t)A * 4;
+}
+
+// Edge writer for envs of at most kMaskMaxAgents agents.  Workgroup = (env,
+// slice of kEdgeSources sources), as above.  Lane l of wavefront w tests
+// source s_begin + l against the ids of chunks w, w + 4, ... and keeps the
+// neighbour bits of each 64-id chunk in LDS (with positions in [-8192, 8191]
+// the differences and their squares fit packed int16 / one dot2 per pair;
+// other envs take 32-bit arithmetic).  Then every thread takes output
+// positions i = tid, tid + 256, ... of the slice's contiguous edge range:
+// source = the last one whose first offset is <= i, destination = the
+// (i - first)-th set bit of its mask, so consecutive lanes store consecutive
+// edges.  A position past a source's recomputed neighbours (a skipped row
+// whose stored count is stale) is left as it is.
+__global__ __launch_bounds__(kEdgeThreads) void edges_mask_kernel(jl_magat_t m) {
+    extern __shared__ __align__(16) uint64_t s_mask[];  // [chunk][source of the slice]
+    __shared__ long long s_wave[kEdgeWaves];
+    __shared__ long long s_slice_first;
+    __shared__ int s_rel[kEdgeSources + 1];  // first edge of each source, relative to the slice's
+    const int A = m.n_agents;
+    const int chunks = (A + kWave - 1) / kWave;
+    const int padded = chunks * kWave;
+    int32_t* s_xy = reinterpret_cast<int32_t*>(s_mask + (size_t)chunks * kEdgeSources);
+    int32_t* s_cnt = s_xy + padded;
+    const int parts = (A + kEdgeSources - 1) / kEdgeSources;
+    const int env = blockIdx.x / parts;
+    const int part = blockIdx.x - env * parts;
+    const int s_begin = part * kEdgeSources;
+    const int s_end = (s_begin + kEdgeSources) < A ? (s_begin + kEdgeSources) : A;
+    const int tid = threadIdx.x, lane = tid & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);  // uniform per wavefront
+    const size_t base = (size_t)env * A;
+    int wide = 0;
+    for (int a = tid; a < padded; a += kEdgeThreads) {
+        int32_t xy = 0x40004000;  // padding: (16384, 16384), never within the radius
+        if (a < A) {
+            const float2 p = reinterpret_cast<const float2*>(m.pyg_pos)[base + a];
+            const int x = (int16_t)p.x, y = (int16_t)p.y;
+            wide |= (x < -8192 || x > 8191 || y < -8192 || y > 8191) ? 1 : 0;
+            xy = (x & 0xFFFF) | (y << 16);
+            s_cnt[a] = m.edge_counts[base + a];
+        }
+        s_xy[a] = xy;
+    }
+    const long long env_base = m.env_edge_base[env];
+    wide = __syncthreads_or(wide);
+    long long before = 0;
+    for (int a = tid; a < s_begin; a += kEdgeThreads) before += s_cnt[a];
+    for (int off = kWave / 2; off > 0; off >>= 1) before += __shfl_xor(before, off, kWave);
+    if (lane == 0) s_wave[wave] = before;
+    __syncthreads();
+    if (wave == 0) {
+        long long first = env_base;
+        for (int k = 0; k < kEdgeWaves; ++k) first += s_wave[k];
+        const int a = s_begin + lane;
+        const int c = a < s_end ? s_cnt[a] : 0;
+        int incl = c;
+        for (int off = 1; off < kWave; off <<= 1) {
+            const int t = __shfl_up(incl, off, kWave);
+            if (lane >= off) incl += t;
+        }
+        if (a < s_end) m.edge_prefix[base + a] = first + incl - c;
+        s_rel[lane] = incl - c;
+        if (lane == kWave - 1) s_rel[kWave] = incl;
+        if (lane == 0) s_slice_first = first;
+    }
+    {
+        const int a = s_begin + lane;
+        const int32_t sxy = s_xy[a < s_end ? a : 0];
+        for (int c = wave; c < chunks; c += kEdgeWaves) {
+            const int32_t* row = s_xy + c * kWave;
+            uint64_t bits = 0;
+            if (!wide) {
+                // dx * dx + dy * dy - (49 + 1) is negative exactly for a neighbour:
+                // its sign bit is shifted in at bit 0 (alignbit), ids in
+                // descending order, so id j ends at bit j
+                const jl_v2s me = __builtin_bit_cast(jl_v2s, sxy);
+                uint32_t half[2] = {0u, 0u};
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+#pragma unroll
+                    for (int j = 31; j >= 0; --j) {
+                        const jl_v2s d = me - __builtin_bit_cast(jl_v2s, row[h * 32 + j]);
+                        const int t = __builtin_amdgcn_sdot2(d, d, -(kCommRadiusSq + 1), false);
+                        half[h] = __builtin_amdgcn_alignbit(half[h], (uint32_t)t, 31);
+                    }
+                }
+                bits = ((uint64_t)half[1] << 32) | half[0];
+            } else {
+                const int cx = (int16_t)(sxy & 0xFFFF), cy = sxy >> 16;
+                for (int j = 0; j < kWave; ++j) {
+                    const int32_t oxy = row[j];
+                    const int dx = cx - (int16_t)(oxy & 0xFFFF), dy = cy - (oxy >> 16);
+                    bits |= (uint64_t)(wrap_dist2(dx, dy) <= kCommRadiusSq) << j;
+                }
+            }
+            const int self = a - c * kWave;
+            if (self >= 0 && self < kWave) bits &= ~(1ull << self);
+            // padding ids (past A) are never neighbours, whatever 32-bit wrap gives
+            const int real = A - c * kWave;
+            if (real < kWave) bits &= (1ull << real) - 1ull;
+            s_mask[c * kEdgeSources + lane] = bits;
+        }
+    }
+    __syncthreads();
+    const long long cap = m.edge_capacity;
+    int64_t* dst_index = m.edge_index + cap;
+    const int nsrc = s_end - s_begin;
+    const int total = s_rel[nsrc];
+    const long long slice_first = s_slice_first;
+    for (int i = tid; i < total; i += kEdgeThreads) {
+        int sl = 0;  // the last source whose first edge is <= i
+#pragma unroll
+        for (int step = kEdgeSources / 2; step > 0; step >>= 1)
+            if (sl + step < nsrc && s_rel[sl + step] <= i) sl += step;
+        int k = i - s_rel[sl];
+        int c = 0;
+        uint64_t w = 0;
+        for (; c < chunks; ++c) {
+            w = s_mask[c * kEdgeSources + sl];
+            const int pc = __popcll(w);
+            if (k < pc) break;
+            k -= pc;
+        }
+        if (c == chunks) continue;
+        // the k-th set bit of w
+        uint32_t v = (uint32_t)w;
+        int bit = 0;
+        const int plo = __popc(v);
+        if (k >= plo) {
+            k -= plo;
+            v = (uint32_t)(w >> 32);
+            bit = 32;
+        }
+#pragma unroll
+        for (int half = 16; half > 0; half >>= 1) {
+            const int p = __popc(v & ((1u << half) - 1u));
+            if (k >= p) {
+                k -= p;
+                v >>= half;
+                bit += half;
+            }
+        }
+        const int a = s_begin + sl, o = c * kWave + bit;
+        const long long e = slice_first + i;
+        if (e < cap) {
+            const int32_t sxy = s_xy[a], oxy = s_xy[o];
+            const int dx = (int16_t)(sxy & 0xFFFF) - (int16_t)(oxy & 0xFFFF);
+            const int dy = (sxy >> 16) - (oxy >> 16);
+            m.edge_index[e] = (int64_t)(base + a);
+            dst_index[e] = (int64_t)(base + o);
+            float* attr = m.edge_attr + e * 3;
+            attr[0] = (float)dx;
+            attr[1] = (float)dy;
+            attr[2] = (float)((dx < 0 ? -dx : dx) + (dy < 0 ? -dy : dy));
+        }
     }
 }
 
@@ -523,6 +728,11 @@ extern "C" int jl_magat_edges(const jl_magat_t* m, jl_stream_t stream) {
     rc = launch_status();
     if (rc) return rc;
     const unsigned eparts = (unsigned)((m->n_agents + kEdgeSources - 1) / kEdgeSources);
+    if (m->n_agents <= kMaskMaxAgents) {
+        hipLaunchKernelGGL(edges_mask_kernel, dim3((unsigned)m->n_envs * eparts), dim3(kEdgeThreads),
+                           edge_mask_lds(m->n_agents), (hipStream_t)stream, *m);
+        return launch_status();
+    }
     const size_t elds = edge_lds(m->n_agents);
     if (elds > 160 * 1024) return JL_ERR_ARG;
     hipLaunchKernelGGL(edges_kernel, dim3((unsigned)m->n_envs * eparts), dim3(kEdgeThreads), elds,

@@ -51,6 +51,14 @@
 #define JLO_PYG_AREA 169
 #define JLO_COMM_RADIUS_SQ 49
 
+/* Squared distance in 32-bit int arithmetic as the reference computes it
+ * (stateless_step.cu:513-520, :889): for int16 positions near opposite
+ * extremes the products and sum wrap modulo 2^32; done in unsigned so the
+ * wrap is defined. */
+static inline int jlo_dist2(int dx, int dy) {
+    return (int)((uint32_t)dx * (uint32_t)dx + (uint32_t)dy * (uint32_t)dy);
+}
+
 static const int ACT_DX[5] = {0, -1, 1, 0, 0};
 static const int ACT_DY[5] = {0, 0, 0, -1, 1};
 
@@ -826,7 +834,7 @@ void jlo_magat_nodes(const jl_magat_t* m) {
                 if (o == a) continue;
                 const int dx = cx - (int16_t)rows[(size_t)o * 8 + 2];
                 const int dy = cy - (int16_t)rows[(size_t)o * 8 + 3];
-                if (dx * dx + dy * dy <= JLO_COMM_RADIUS_SQ) ++count;
+                if (jlo_dist2(dx, dy) <= JLO_COMM_RADIUS_SQ) ++count;
             }
             m->pyg_pos[g * 2] = (float)cx;
             m->pyg_pos[g * 2 + 1] = (float)cy;
@@ -861,7 +869,7 @@ void jlo_magat_edges(const jl_magat_t* m) {
                 const int ox = (int16_t)m->pyg_pos[((size_t)e * A + o) * 2];
                 const int oy = (int16_t)m->pyg_pos[((size_t)e * A + o) * 2 + 1];
                 const int dx = cx - ox, dy = cy - oy;
-                if (dx * dx + dy * dy > JLO_COMM_RADIUS_SQ) continue;
+                if (jlo_dist2(dx, dy) > JLO_COMM_RADIUS_SQ) continue;
                 m->edge_index[out] = node;
                 m->edge_index[cap + out] = (int64_t)e * A + o;
                 m->edge_attr[out * 3] = (float)dx;

@@ -69,7 +69,7 @@ def _oracle_stateless(oracle, grids, rows_reset, rows):
 
 @pytest.mark.parametrize(
     "E,W,A,density",
-    [(4, 64, 256, 0.3), (3, 32, 64, 0.2), (2, 128, 300, 0.2), (1, 256, 160, 0.2)],
+    [(4, 64, 256, 0.3), (3, 32, 64, 0.2), (2, 128, 300, 0.2), (1, 256, 160, 0.2), (1, 128, 1100, 0.1)],
 )
 def test_stateless_batches_match_oracle(oracle, E, W, A, density):
     """C4 shape on fewer envs (first case), plus the other map profiles."""
@@ -84,6 +84,32 @@ def test_stateless_batches_match_oracle(oracle, E, W, A, density):
     sim.refresh_compact_state_from_raw_batch(torch.from_numpy(rows).cuda())
     sim.materialize_pyg_inputs()
     _compare(sim, _oracle_stateless(oracle, grids, rows_reset, rows), f"E{E} W{W} A{A}")
+
+
+def test_far_off_map_positions_match_oracle(oracle):
+    """Positions far off the map: a cluster beyond +-8192 (the edge test then
+    runs in 32-bit arithmetic) and two agents at the int16 extremes, whose
+    squared distances to the others overflow int32 exactly as the
+    reference's int arithmetic does (stateless_step.cu:517, :889)."""
+    from iclr_2027_jointoom_amd.synthetic import make_batch
+
+    E, W, A = 2, 64, 40
+    grids, starts, goals = make_batch(31, E, W, W, A, density=0.2)
+    starts = starts.copy()
+    starts[1, :10, 0] = 9000 + np.arange(10) % 4
+    starts[1, :10, 1] = -9000 + np.arange(10) // 4
+    starts[1, 10] = (-32768, 32767)
+    starts[1, 11] = (-32766, 32765)
+    ext = ext_for(W, W)
+    sim = ext.StatelessGridWorldSimulator(torch.from_numpy(grids.astype(np.int32)).cuda(), A, 3)
+    rows_reset = _rows(E, A, starts, goals, 1)
+    rows = _rows(E, A, starts, goals, 0)
+    sim.update_energy_maps(torch.from_numpy(rows_reset).cuda(), len(rows_reset))
+    sim.refresh_compact_state_from_raw_batch(torch.from_numpy(rows).cuda())
+    sim.materialize_pyg_inputs()
+    m = _oracle_stateless(oracle, grids, rows_reset, rows)
+    assert m.edge_counts.reshape(E, A)[1, 10] > 0  # the overflow case is exercised
+    _compare(sim, m, "far")
 
 
 def test_partial_batch_and_invalid_rows_match_oracle(oracle):
