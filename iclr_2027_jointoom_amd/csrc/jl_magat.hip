@@ -9,10 +9,12 @@
 // 414-421, 438-478).  The clamped ctg value is one of 21 float constants k/10
 // (the IEEE quotients), so no division is evaluated on the device.
 // edges: per-env edge totals (from the node pass) -> one-workgroup scan ->
-// per (env, 64-source slice) writer: each wavefront takes 16 consecutive
-// sources, tests the others 256 at a time and queues the neighbours in LDS;
-// they leave 64 edges per store, sorted by (source, destination id)
-// (grid_world_cuda.cu:17-110, stateless_step.cu:854-935).
+// per (env, 64-source slice) writer: lane l of each wavefront tests source l
+// of the slice against 64 ids per step (packed int16 differences, one dot2
+// per pair) into per-source neighbour bitmasks in LDS; then every thread
+// stores one edge per output position, sorted by (source, destination id)
+// (grid_world_cuda.cu:17-110, stateless_step.cu:854-935).  Envs of more
+// than 1024 agents take a ballot writer with an LDS ring.
 #include "jl_common.h"
 
 namespace jl {
@@ -21,6 +23,7 @@ namespace {
 constexpr int kNodeThreads = 256;
 
 typedef short jl_v2s __attribute__((ext_vector_type(2)));  // (x, y) as packed int16
+typedef unsigned int jl_v4u __attribute__((ext_vector_type(4)));
 
 // (float)k / 10.0f rounded to nearest even, k = -10..10.
 __device__ __constant__ float kTenths[21] = {-1.0f, -0.9f, -0.8f, -0.7f, -0.6f, -0.5f, -0.4f,
@@ -195,8 +198,12 @@ __global__ __launch_bounds__(kNodeThreads) void nodes_kernel(jl_magat_t m) {
         ok_hi[it] = rok && c0 + 1 >= 0 && c0 + 1 < H / 16;
         const uint4* row4 =
             reinterpret_cast<const uint4*>(env_energy + (size_t)a * cells + (size_t)(rok ? x : 0) * H);
-        lo[it] = row4[ok_lo[it] ? c0 : 0];
-        hi[it] = row4[ok_hi[it] ? c0 + 1 : 0];
+        // read once per step: streamed past the caches the row stores fill
+        const jl_v4u* r4 = reinterpret_cast<const jl_v4u*>(row4);
+        const jl_v4u l4 = __builtin_nontemporal_load(r4 + (ok_lo[it] ? c0 : 0));
+        const jl_v4u h4 = __builtin_nontemporal_load(r4 + (ok_hi[it] ? c0 + 1 : 0));
+        lo[it] = make_uint4(l4.x, l4.y, l4.z, l4.w);
+        hi[it] = make_uint4(h4.x, h4.y, h4.z, h4.w);
         shift[it] = y0 - c0 * 16;  // 0..15: byte of column y0 in lo
         dst[it] = el * kWinStride + r * kWinRow;
     }
