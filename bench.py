@@ -54,9 +54,9 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 PEAK_HBM_BPS = 8.0e12
-# HBM bytes per token-kernel launch measured with rocprofv3 --pmc FETCH_SIZE /
+# HBM bytes per build launch measured with rocprofv3 --pmc FETCH_SIZE /
 # WRITE_SIZE on this workload, scaled by the copy calibration (file header).
-TRAFFIC_FILE = ROOT / "profiles" / "tokens_kernel_pmc_1024x128_64.txt"
+TRAFFIC_FILE = ROOT / "profiles" / "build_kernel_pmc_1024x128_64.txt"
 
 MAGAT_TRAFFIC_FILE = ROOT / "profiles" / "magat_nodes_pmc_512x256_64.txt"
 
@@ -390,7 +390,7 @@ def run_gpu(args) -> dict:
         "gpu_ms_per_step": gpu_ms / args.steps,
         "roofline": {
             "bound": "hbm",
-            "kernel": f"tokens_kernel<{W}>" + (" (single-launch build)" if single else ""),
+            "kernel": f"build_kernel<{W}> (single-launch build)" if single else f"tokens_kernel<{W}>",
             "achieved": achieved / 1e9,
             "peak": PEAK_HBM_BPS / 1e9,
             "unit": "GB/s",

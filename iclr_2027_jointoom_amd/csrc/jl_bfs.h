@@ -19,17 +19,18 @@
 namespace jl {
 
 // Value of lane - 1 (lane 0 reads 0) and of lane + 1 (lane 63 reads 0): DPP
-// wave_shr:1 / wave_shl:1 on both halves, no LDS round trip.  Every lane of
-// the wavefront must be active.
+// wave_shr:1 / wave_shl:1 on both halves, no LDS round trip; bound_ctrl
+// writes the 0 of the lane without a source.  Every lane of the wavefront
+// must be active.
 __device__ __forceinline__ uint64_t from_lane_below(uint64_t v) {
-    const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)v, 0x138, 0xF, 0xF, false);
-    const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(v >> 32), 0x138, 0xF, 0xF, false);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)v, 0x138, 0xF, 0xF, true);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(v >> 32), 0x138, 0xF, 0xF, true);
     return ((uint64_t)hi << 32) | lo;
 }
 
 __device__ __forceinline__ uint64_t from_lane_above(uint64_t v) {
-    const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)v, 0x130, 0xF, 0xF, false);
-    const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(v >> 32), 0x130, 0xF, 0xF, false);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)v, 0x130, 0xF, 0xF, true);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(v >> 32), 0x130, 0xF, 0xF, true);
     return ((uint64_t)hi << 32) | lo;
 }
 
@@ -170,6 +171,78 @@ __device__ int wave_bfs(const uint64_t (&fr)[R][RowWords<H>::HW], int gx, int gy
         }
     }
     return overflow;
+}
+
+// wave_bfs for one row per lane (R = 1) without the frontier overflow count
+// and without a level cap, in batches of 16 levels: the levels of a batch
+// are unrolled into straight-line code (expansion, then the new cells ORed
+// into the batch mask and into the planes of the level's 4 low bits, chosen
+// at compile time), and only after the batch are its cells' distances
+// L0 + (plane bits) written, one pass over the batch mask.  The search stops
+// after the first batch whose last level reached no cell (levels past the
+// last reach nothing, so the field is wave_bfs's).  The single wavefront's
+// search is a chain of dependent instructions; the batch keeps the writes
+// off that chain and lets the plane and mask updates fill its gaps.
+template <int H, typename T>
+__device__ void wave_bfs_batched(const uint64_t (&fr)[RowWords<H>::HW], int gx, int gy, T* dist) {
+    constexpr int HW = RowWords<H>::HW;
+    constexpr int kBatch = 16;
+    const int lane = threadIdx.x & (kWave - 1);
+    uint64_t front[HW], avail[HW];  // avail: free cells not reached yet
+#pragma unroll
+    for (int k = 0; k < HW; ++k) {
+        front[k] = 0;
+        avail[k] = fr[k];
+        if (lane == gx && k == (gy >> 6)) {
+            front[k] = 1ull << (gy & 63);
+            avail[k] &= ~front[k];
+        }
+    }
+    T* row_dist = dist + lane * H;
+    for (int L0 = 1;; L0 += kBatch) {
+        uint64_t bm[HW], p0[HW], p1[HW], p2[HW], p3[HW];
+#pragma unroll
+        for (int k = 0; k < HW; ++k) bm[k] = p0[k] = p1[k] = p2[k] = p3[k] = 0;
+#pragma unroll
+        for (int j = 0; j < kBatch; ++j) {
+            uint64_t nf[HW];
+#pragma unroll
+            for (int k = 0; k < HW; ++k) {
+                const uint64_t up = from_lane_below(front[k]);
+                const uint64_t down = from_lane_above(front[k]);
+                uint64_t left = front[k] << 1;
+                uint64_t right = front[k] >> 1;
+                if (k > 0) left |= front[k - 1] >> 63;
+                if (k + 1 < HW) right |= front[k + 1] << 63;
+                nf[k] = (left | right | up | down) & avail[k];
+            }
+#pragma unroll
+            for (int k = 0; k < HW; ++k) {
+                avail[k] &= ~nf[k];
+                front[k] = nf[k];
+                bm[k] |= nf[k];
+                if (j & 1) p0[k] |= nf[k];
+                if (j & 2) p1[k] |= nf[k];
+                if (j & 4) p2[k] |= nf[k];
+                if (j & 8) p3[k] |= nf[k];
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < HW; ++k) {
+            uint64_t m = bm[k];
+            while (m) {
+                const int c = __ffsll((unsigned long long)m) - 1;
+                const uint32_t j = (uint32_t)((p0[k] >> c) & 1u) | (uint32_t)((p1[k] >> c) & 1u) << 1 |
+                                   (uint32_t)((p2[k] >> c) & 1u) << 2 | (uint32_t)((p3[k] >> c) & 1u) << 3;
+                row_dist[k * 64 + c] = (T)(L0 + (int)j);
+                m &= m - 1;
+            }
+        }
+        bool more = false;
+#pragma unroll
+        for (int k = 0; k < HW; ++k) more |= front[k] != 0;
+        if (!__any(more)) break;
+    }
 }
 
 // Free-cell masks of map row x (0 for x >= W), for the group BFS.

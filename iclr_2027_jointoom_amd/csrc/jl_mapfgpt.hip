@@ -218,42 +218,17 @@ __device__ __forceinline__ uint32_t kept_greedy(const jl_mapfgpt_t& b, size_t i,
 // agent's info bits: the frontier overflow count, or kInfoBadGoal for a goal
 // off the map or on an obstacle (an all-unreachable field, :224-236), and the
 // greedy mask at its position (spx, spy) when that is on the map.
-template <int H, int R, bool kMarked>
-__device__ uint32_t refresh_field(const jl_mapfgpt_t& b, size_t agent_index, uint32_t e, int gx,
-                                  int gy, int spx, int spy, uint16_t* s_dist) {
-    constexpr int HW = RowWords<H>::HW;
+// The map's tiles of the LDS field s_dist (W * H uint16, with greedy marks
+// when kMarked) into agent agent_index's tiled field, 16-byte row segments
+// first, first + stride, ... (the border ring keeps its unreachable cells).
+template <int H, bool kMarked>
+__device__ void store_field_tiles(const jl_mapfgpt_t& b, size_t agent_index, const uint16_t* s_dist,
+                                  int first, int stride) {
     const int W = b.map_w;
-    const int lane = threadIdx.x & (kWave - 1);
-    const int cells = W * H;
-    const int words = cells / 32;
-    const size_t tcells = tiled_cells(W, H);
-    for (int c = lane; c < cells; c += kWave) s_dist[c] = kUnreachable;
-    wave_sync();
-    bool ok = e < (uint32_t)b.n_envs && (uint32_t)gx < (uint32_t)W && (uint32_t)gy < (uint32_t)H;
-    const uint32_t* env_bits = b.grid_bits + (size_t)(ok ? e : 0) * words;
-    if (ok && bit_at(env_bits, gx * H + gy)) ok = false;
-    int overflow = 0;
-    if (ok) {
-        uint64_t fr[R][HW];
-        load_free_rows<H, R>(env_bits, W, fr);
-        if (lane == 0) s_dist[gx * H + gy] = 0;
-        wave_sync();
-        if (W * H > kMaxFrontier + 1) {
-            overflow = wave_bfs<H, R, uint16_t, true>(fr, gx, gy, 0x7FFFFFFF, s_dist);
-        } else {
-            overflow = wave_bfs<H, R, uint16_t, false>(fr, gx, gy, 0x7FFFFFFF, s_dist);
-        }
-    }
-    wave_sync();
-    uint32_t info = ok ? (uint32_t)(overflow < 0xFFFFFF ? overflow : 0xFFFFFF) << kInfoOverflowShift
-                       : kInfoBadGoal;
-    if ((uint32_t)spx < (uint32_t)W && (uint32_t)spy < (uint32_t)H)
-        info |= greedy_mask<H>([s_dist](int x, int y) { return (uint32_t)s_dist[x * H + y]; }, spx, spy, W);
     const uint4* lds4 = reinterpret_cast<const uint4*>(s_dist);
-    // the map's tiles (the border ring keeps its unreachable cells)
-    uint4* tout = reinterpret_cast<uint4*>(b.cost_tiles + agent_index * tcells);
+    uint4* tout = reinterpret_cast<uint4*>(b.cost_tiles + agent_index * tiled_cells(W, H));
     const int map_tile_rows = (W + 7) / 8;
-    for (int c = lane; c < map_tile_rows * H; c += kWave) {
+    for (int c = first; c < map_tile_rows * H; c += stride) {
         const int t = c >> 3, r = c & 7;  // map tile, row inside the tile
         const int tr = t / (H / 8), tc = t - (t / (H / 8)) * (H / 8);
         const int x = tr * 8 + r, y0 = tc * 8;
@@ -266,7 +241,50 @@ __device__ uint32_t refresh_field(const jl_mapfgpt_t& b, size_t agent_index, uin
         v.w = in ? v.w : 0xFFFFFFFFu;
         tout[dst] = v;
     }
-    wave_sync();  // the LDS field is rewritten by the next refresh
+}
+
+template <int H, int R, bool kMarked, bool kTiles = true>
+__device__ uint32_t refresh_field(const jl_mapfgpt_t& b, size_t agent_index, uint32_t e, int gx,
+                                  int gy, int spx, int spy, uint16_t* s_dist) {
+    constexpr int HW = RowWords<H>::HW;
+    const int W = b.map_w;
+    const int lane = threadIdx.x & (kWave - 1);
+    const int cells = W * H;
+    const int words = cells / 32;
+    {
+        // W * H is a multiple of 8 cells (H >= 32): 16-byte stores
+        const uint32_t u2 = (uint32_t)kUnreachable * 0x10001u;
+        uint4* d4 = reinterpret_cast<uint4*>(s_dist);
+        for (int c = lane; c < cells / 8; c += kWave) d4[c] = make_uint4(u2, u2, u2, u2);
+    }
+    wave_sync();
+    bool ok = e < (uint32_t)b.n_envs && (uint32_t)gx < (uint32_t)W && (uint32_t)gy < (uint32_t)H;
+    const uint32_t* env_bits = b.grid_bits + (size_t)(ok ? e : 0) * words;
+    if (ok && bit_at(env_bits, gx * H + gy)) ok = false;
+    int overflow = 0;
+    if (ok) {
+        uint64_t fr[R][HW];
+        load_free_rows<H, R>(env_bits, W, fr);
+        if (lane == 0) s_dist[gx * H + gy] = 0;
+        wave_sync();
+        if (W * H > kMaxFrontier + 1) {
+            overflow = wave_bfs<H, R, uint16_t, true>(fr, gx, gy, 0x7FFFFFFF, s_dist);
+        } else if constexpr (R == 1) {
+            // no level of a map this small can overflow the frontier
+            wave_bfs_batched<H, uint16_t>(fr[0], gx, gy, s_dist);
+        } else {
+            overflow = wave_bfs<H, R, uint16_t, false>(fr, gx, gy, 0x7FFFFFFF, s_dist);
+        }
+    }
+    wave_sync();
+    uint32_t info = ok ? (uint32_t)(overflow < 0xFFFFFF ? overflow : 0xFFFFFF) << kInfoOverflowShift
+                       : kInfoBadGoal;
+    if ((uint32_t)spx < (uint32_t)W && (uint32_t)spy < (uint32_t)H)
+        info |= greedy_mask<H>([s_dist](int x, int y) { return (uint32_t)s_dist[x * H + y]; }, spx, spy, W);
+    if (kTiles) {
+        store_field_tiles<H, kMarked>(b, agent_index, s_dist, lane, kWave);
+        wave_sync();  // the LDS field is rewritten by the next refresh
+    }
     return info;
 }
 
@@ -1120,7 +1138,6 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(H <= 1
     const int16_t* __restrict__ goal_y) {
     constexpr int kWaves = kThreads / kWave;
     constexpr int MH = H + 2 * kRadius;  // map columns
-    constexpr int TC = H / 8 + 2;        // tile grid columns of a tiled field
     extern __shared__ __align__(16) uint8_t smem[];
     const int A = b.n_agents, W = b.map_w;
     const int env = blockIdx.x;
@@ -1202,23 +1219,31 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(H <= 1
 
     // ---- changed goals: BFS fields overlaying the token area -----------------
     const int nlist = __builtin_amdgcn_readfirstlane(*s_nlist);
-    if (nlist > 0) {
-        if (wave < L.bfs_waves) {
+    // rounds of up to bfs_waves fields: each wavefront searches one into its
+    // LDS field, then the whole workgroup stores the round's tiles
+    for (int r0 = 0; r0 < nlist; r0 += L.bfs_waves) {
+        if (wave < L.bfs_waves && r0 + wave < nlist) {
             uint16_t* s_dist = reinterpret_cast<uint16_t*>(smem) + (size_t)wave * cells;
-            for (int k = wave; k < nlist; k += L.bfs_waves) {
-                const uint2 it = s_list[k];
-                const uint32_t a = (uint32_t)__builtin_amdgcn_readfirstlane((int)it.x);
-                const uint32_t sx = (uint32_t)__builtin_amdgcn_readfirstlane((int)it.y);
-                const uint32_t pos = (uint32_t)__builtin_amdgcn_readfirstlane((int)s_rec[a * kBuildRecWords]);
-                const uint32_t goal = (uint32_t)__builtin_amdgcn_readfirstlane((int)s_rec[a * kBuildRecWords + 1]);
-                const uint32_t bits = refresh_field<H, R, true>(
-                    b, (size_t)env * A + a, sx & 0xFFFFu, (int)(goal & 0xFFFFu), (int)(goal >> 16),
-                    (int)(pos & 0xFFFFu), (int)(pos >> 16), s_dist);
-                if (lane == 0) s_info[a] |= bits;
-            }
+            const uint2 it = s_list[r0 + wave];
+            const uint32_t a = (uint32_t)__builtin_amdgcn_readfirstlane((int)it.x);
+            const uint32_t sx = (uint32_t)__builtin_amdgcn_readfirstlane((int)it.y);
+            const uint32_t pos = (uint32_t)__builtin_amdgcn_readfirstlane((int)s_rec[a * kBuildRecWords]);
+            const uint32_t goal = (uint32_t)__builtin_amdgcn_readfirstlane((int)s_rec[a * kBuildRecWords + 1]);
+            const uint32_t bits = refresh_field<H, R, true, false>(
+                b, (size_t)env * A + a, sx & 0xFFFFu, (int)(goal & 0xFFFFu), (int)(goal >> 16),
+                (int)(pos & 0xFFFFu), (int)(pos >> 16), s_dist);
+            if (lane == 0) s_info[a] |= bits;
+        }
+        __syncthreads();
+        const int nround = (nlist - r0) < L.bfs_waves ? (nlist - r0) : L.bfs_waves;
+        for (int f = 0; f < nround; ++f) {
+            const uint32_t a = s_list[r0 + f].x;
+            store_field_tiles<H, true>(b, (size_t)env * A + a, reinterpret_cast<uint16_t*>(smem) + (size_t)f * cells,
+                                       tid, kThreads);
         }
         // the refreshed fields are stored before any window load of this
-        // workgroup, and the LDS fields are free for the token area
+        // workgroup, and the LDS fields are free for the next round or the
+        // token area
         __syncthreads();
     }
 
