@@ -107,21 +107,35 @@ def cpu_baseline(args) -> dict:
     }
 
 
+# hipEventDisableSystemFence (hip_runtime_api.h): a timing event recorded
+# without a system-scope release.  A default event writes back and
+# invalidates the caches where it is recorded, which slowed the resident
+# loop by about 7 us per step with two events around every build.
+HIP_EVENT_DISABLE_SYSTEM_FENCE = 0x20000000
+# the timed loops bracket the hot kernel with events on every EVENT_EVERY-th step only
+EVENT_EVERY = 4
+
+
 class HipEvents:
-    """hipEvent_t pairs from the process's HIP runtime (torch's libamdhip64)."""
+    """hipEvent_t handles from the process's HIP runtime (torch's libamdhip64),
+    timing-only: created with hipEventDisableSystemFence."""
 
     def __init__(self):
         self.rt = ctypes.CDLL("libamdhip64.so.7")
-        self.rt.hipEventCreate.argtypes = [ctypes.POINTER(ctypes.c_void_p)]
+        self.rt.hipEventCreateWithFlags.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_uint]
+        self.rt.hipEventRecord.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
         self.rt.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p, ctypes.c_void_p]
         self.rt.hipEventDestroy.argtypes = [ctypes.c_void_p]
 
     def create(self) -> int:
         ev = ctypes.c_void_p()
-        rc = self.rt.hipEventCreate(ctypes.byref(ev))
+        rc = self.rt.hipEventCreateWithFlags(ctypes.byref(ev), HIP_EVENT_DISABLE_SYSTEM_FENCE)
         if rc != 0:
-            raise RuntimeError(f"hipEventCreate failed ({rc})")
+            raise RuntimeError(f"hipEventCreateWithFlags failed ({rc})")
         return ev.value
+
+    def event(self) -> "HipTimingEvent":
+        return HipTimingEvent(self)
 
     def elapsed_ms(self, a: int, b: int) -> float:
         ms = ctypes.c_float()
@@ -129,6 +143,25 @@ class HipEvents:
         if rc != 0:
             raise RuntimeError(f"hipEventElapsedTime failed ({rc})")
         return float(ms.value)
+
+
+class HipTimingEvent:
+    """A fence-less timing event with torch.cuda.Event's record / elapsed_time."""
+
+    def __init__(self, hip: HipEvents):
+        self.hip = hip
+        self.ev = hip.create()
+
+    def record(self, stream=None) -> None:
+        import torch
+
+        s = stream if stream is not None else torch.cuda.current_stream()
+        rc = self.hip.rt.hipEventRecord(ctypes.c_void_p(self.ev), ctypes.c_void_p(s.cuda_stream))
+        if rc != 0:
+            raise RuntimeError(f"hipEventRecord failed ({rc})")
+
+    def elapsed_time(self, other: "HipTimingEvent") -> float:
+        return self.hip.elapsed_ms(self.ev, other.ev)
 
 
 def measured_traffic(path: Path = TRAFFIC_FILE) -> int | None:
@@ -346,7 +379,10 @@ def run_gpu(args) -> dict:
     if any(diag):
         raise RuntimeError(f"builder diagnostics non-zero after warmup: {diag}")
 
-    tok_events = [(hip.create(), hip.create()) for _ in range(args.steps)]
+    # every EVENT_EVERY-th timed step carries the event pair around its
+    # build: each event is a packet of its own that the command processor
+    # takes about 1.7 us to pass between the kernels
+    tok_events = [(hip.create(), hip.create()) for _ in range(0, args.steps, EVENT_EVERY)]
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
@@ -354,7 +390,10 @@ def run_gpu(args) -> dict:
     start.record()
     for i in range(args.steps):
         if graph is None:
-            builder._desc.token_events[0], builder._desc.token_events[1] = tok_events[i]
+            if i % EVENT_EVERY == 0:
+                builder._desc.token_events[0], builder._desc.token_events[1] = tok_events[i // EVENT_EVERY]
+            else:
+                builder._desc.token_events[0] = builder._desc.token_events[1] = None
         one_step(args.warmup + i)
     end.record()
     torch.cuda.synchronize()
@@ -364,7 +403,7 @@ def run_gpu(args) -> dict:
     if graph is not None:
         # events cannot be recorded inside the graph: time the token kernel on
         # eager steps after the timed region
-        n_ev = min(args.steps, 20)
+        n_ev = min(len(tok_events), 20)
         tok_events = tok_events[:n_ev]
         for i in range(n_ev):
             builder._desc.token_events[0], builder._desc.token_events[1] = tok_events[i]
@@ -399,6 +438,7 @@ def run_gpu(args) -> dict:
             "traffic": measured_traffic() if (E, A, W, args.map_kind) == (1024, 128, 64, "iid") else None,
             "bytes_per_launch": tok_bytes,
             "avg_launch_us": tok_avg_s * 1e6,
+            "timed_launches": len(tok_ms),  # HIP events on every EVENT_EVERY-th timed step
         },
         "first_build_ms": first_build_ms,
         "goals_reassigned": int(sim.goal_cursors.sum().item()) if args.task_mode == "lifelong" else None,
@@ -666,13 +706,14 @@ def run_gpu_magat(args) -> dict:
         from iclr_2027_jointoom_amd.graphs import MagatStatefulGraph
 
         graph = MagatStatefulGraph(sim)
-    # all kernels run on torch's current stream, so torch events bracket the node pass
-    node_events = [tuple(torch.cuda.Event(enable_timing=True) for _ in range(3)) for _ in range(args.steps)]
+    # all kernels run on torch's current stream, so events recorded there bracket the node pass
+    hip = HipEvents()
+    node_events = [tuple(hip.event() for _ in range(3)) for _ in range(0, args.steps, EVENT_EVERY)]
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(args.steps):
         if graph is None:
-            one_step(args.warmup + i, node_events[i])
+            one_step(args.warmup + i, node_events[i // EVENT_EVERY] if i % EVENT_EVERY == 0 else None)
         else:
             graph.actions.copy_(actions[args.warmup + i])
             graph.replay()
@@ -681,7 +722,7 @@ def run_gpu_magat(args) -> dict:
     if graph is not None:
         # events cannot be recorded inside the graph: time the node pass on
         # eager steps after the timed region
-        node_events = node_events[: min(args.steps, 20)]
+        node_events = node_events[:20]
         for i, ev in enumerate(node_events):
             one_step((args.warmup + i) % total_steps, ev)
         torch.cuda.synchronize()
@@ -706,6 +747,7 @@ def run_gpu_magat(args) -> dict:
             "traffic": measured_traffic(MAGAT_TRAFFIC_FILE) if (E, A, W) == (512, 256, 64) else None,
             "bytes_per_launch": node_bytes,
             "avg_launch_us": node_s * 1e6,
+            "timed_launches": len(node_ms),  # HIP events on every EVENT_EVERY-th timed step
         },
         "edges_per_step": int(sim.pyg_num_edges.item()),
         "graph_us": float(np.mean(graph_ms)) * 1e3,
@@ -814,15 +856,15 @@ def run_gpu_ring(args) -> dict:
         out = {}
         for fmt, path in archives.items():
             builder = ext.MapfGPTObservationBuilder(g, A)
-            tok_events = [(hip.create(), hip.create()) for _ in range(args.steps)]
+            tok_events = [(hip.create(), hip.create()) for _ in range(0, args.steps, EVENT_EVERY)]
 
             class _Build:
                 n = 0
 
                 def train_step(self, b, raw):
                     i = self.n - args.warmup
-                    if 0 <= i < len(tok_events):
-                        b._desc.token_events[0], b._desc.token_events[1] = tok_events[i]
+                    if 0 <= i < args.steps and i % EVENT_EVERY == 0:
+                        b._desc.token_events[0], b._desc.token_events[1] = tok_events[i // EVENT_EVERY]
                     else:
                         b._desc.token_events[0] = b._desc.token_events[1] = None
                     b.build_tokens(raw)
@@ -1102,13 +1144,13 @@ def run_gpu_costtracer(args) -> dict:
     torch.cuda.synchronize()
     if any(builder.diagnostics.cpu().tolist()):
         raise RuntimeError(f"builder diagnostics non-zero: {builder.diagnostics.cpu().tolist()}")
-    obs_events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-                  for _ in range(args.steps)]
+    hip = HipEvents()
+    obs_events = [(hip.event(), hip.event()) for _ in range(0, args.steps, EVENT_EVERY)]
     hits0 = int(cursor.sum().item())
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(args.steps):
-        one_step(args.warmup + i, obs_events[i])
+        one_step(args.warmup + i, obs_events[i // EVENT_EVERY] if i % EVENT_EVERY == 0 else None)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     obs_s = float(np.mean([a.elapsed_time(b) for a, b in obs_events])) / 1000.0
@@ -1127,6 +1169,7 @@ def run_gpu_costtracer(args) -> dict:
             "traffic": None,
             "bytes_per_launch": nbytes,
             "avg_launch_us": obs_s * 1e6,
+            "timed_launches": len(obs_events),  # HIP events on every EVENT_EVERY-th timed step
         },
         "goal_hits_in_timed_steps": int(cursor.sum().item()) - hits0,
         "resets": int(episodes.sum().item()),

@@ -826,3 +826,58 @@ def test_single_launch_builds_over_moves_teleports_goal_changes_and_two_launch_r
         # one-cell moves, clipped to [-1, W] so that some agents leave the map
         step = moves[rng.integers(0, 5, (E, A))]
         pos = np.clip(pos + step, -1, W)
+
+
+def test_token_events_time_the_token_kernel_and_change_no_output():
+    """token_events (a hipEvent_t pair in the descriptor) are recorded right
+    before and after the token kernel, on the single-launch and the
+    two-launch build alike: the builds with and without them agree bit for
+    bit, and the pair spans a positive time no longer than the whole build
+    bracketed from the host."""
+    import ctypes
+
+    from iclr_2027_jointoom_amd import profile
+
+    rt = ctypes.CDLL("libamdhip64.so.7")
+    rt.hipEventCreateWithFlags.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_uint]
+    rt.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p, ctypes.c_void_p]
+    rt.hipEventDestroy.argtypes = [ctypes.c_void_p]
+
+    def event():
+        ev = ctypes.c_void_p()
+        assert rt.hipEventCreateWithFlags(ctypes.byref(ev), 0x20000000) == 0  # timing only, no system fence
+        return ev.value
+
+    rng = np.random.default_rng(11)
+    E, W, A = 4, 64, 128
+    grids = (rng.random((E, W, W)) < 0.2).astype(np.int32)
+    ext = profile(W, W)
+    g = torch.from_numpy(grids).cuda()
+    rows = torch.from_numpy(_rows_case(rng, grids, A).astype(np.int16)).cuda()
+    for single in (True, False):
+        timed = ext.MapfGPTObservationBuilder(g, A)
+        plain = ext.MapfGPTObservationBuilder(g, A)
+        if not single:
+            timed._desc.build_scratch = None
+            plain._desc.build_scratch = None
+        assert timed.single_launch == single
+        evs = (event(), event())
+        timed._desc.token_events[0], timed._desc.token_events[1] = evs
+        try:
+            for _ in range(2):
+                host0, host1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                host0.record()
+                timed.build_tokens(rows)
+                host1.record()
+                plain.build_tokens(rows)
+                torch.cuda.synchronize()
+                ms = ctypes.c_float()
+                assert rt.hipEventElapsedTime(ctypes.byref(ms), evs[0], evs[1]) == 0
+                assert 0.0 < ms.value <= host0.elapsed_time(host1), (single, ms.value)
+                for name in ("tokens", "labels", "active_mask", "cost_to_go", "state_packed", "histories",
+                             "diagnostics"):
+                    assert torch.equal(getattr(timed, name), getattr(plain, name)), (single, name)
+        finally:
+            timed._desc.token_events[0] = timed._desc.token_events[1] = None
+            for ev in evs:
+                rt.hipEventDestroy(ev)
