@@ -182,6 +182,9 @@ SIGNATURES = {
     "jl_energy_maps_flagged": (
         c_int32, [ctypes.POINTER(SimDesc), c_void_p, c_int32, c_void_p, c_void_p, c_void_p]
     ),
+    "jl_goal_changed_refresh": (
+        c_int32, [ctypes.POINTER(SimDesc), c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]
+    ),
     "jl_magat_occupancy": (c_int32, [ctypes.POINTER(MagatDesc), c_void_p]),
     "jl_magat_nodes": (c_int32, [ctypes.POINTER(MagatDesc), c_void_p]),
     "jl_magat_edges": (c_int32, [ctypes.POINTER(MagatDesc), c_void_p]),

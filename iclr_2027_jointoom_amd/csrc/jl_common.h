@@ -89,6 +89,20 @@ inline int status(hipError_t e) { return e == hipSuccess ? JL_OK : (int)e; }
 
 inline int launch_status() { return status(hipGetLastError()); }
 
+// Sum of the four bytes of a word.
+__device__ __forceinline__ uint32_t byte_sum(uint32_t w) {
+    return (w & 0xFFu) + ((w >> 8) & 0xFFu) + ((w >> 16) & 0xFFu) + (w >> 24);
+}
+
+// Compute units of the current device (grids of looping kernels are sized to them).
+inline int device_cus() {
+    int dev = 0, cus = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return 256;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+        return 256;
+    return cus > 0 ? cus : 256;
+}
+
 // Map-profile dispatch on the column count H (a compile-time divisor).
 #define JL_DISPATCH_H(h, ...)                                   \
     switch (h) {                                               \

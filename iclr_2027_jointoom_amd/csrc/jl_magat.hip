@@ -376,12 +376,42 @@ __global__ __launch_bounds__(1024) void env_scan_kernel(jl_magat_t m) {
 
 constexpr int kEdgeThreads = 256;
 constexpr int kEdgeSources = 64;  // sources per edge workgroup
+static_assert(kEdgeSources == kNodeEgos, "an edge slice is a node slice: the node pass's slice totals");
+// Edge launches of at most this many slices sum the node pass's slice totals
+// before their own (at most 32 loads per thread) instead of reading bases
+// from env_scan_kernel, one launch less.
+constexpr int kSummedSlices = 8192;
 constexpr int kEdgeWaves = kEdgeThreads / kWave;
 constexpr int kEdgeBlock = kEdgeSources / kEdgeWaves;  // consecutive sources per wavefront
 constexpr int kEdgeUnroll = 4;    // 64-candidate chunks tested per step
 constexpr int kEdgeSpan = kWave * kEdgeUnroll;
 constexpr int kEdgeRing = 512;    // pending edges per wavefront: >= (kWave - 1) + kEdgeSpan
 static_assert(kEdgeRing >= kWave - 1 + kEdgeSpan && (kEdgeRing & (kEdgeRing - 1)) == 0, "edge ring");
+
+// This thread's share of the node pass's edge totals of the slices before
+// `slice` (slices in (env, part) order, the order of the edge list); zero
+// when the bases come from env_scan_kernel.
+template <bool kSummed>
+__device__ __forceinline__ long long slice_totals_before(const jl_magat_t& m, int slice) {
+    long long before = 0;
+    if constexpr (kSummed) {
+        const int64_t* totals = m.env_edge_base + m.n_envs + 1;
+#pragma unroll 8
+        for (int j = threadIdx.x; j < slice; j += kEdgeThreads) before += totals[j];
+    }
+    return before;
+}
+
+// The last slice's end is the edge count: num_edges and the closing prefix
+// (what env_scan_kernel writes when it runs).
+__device__ __forceinline__ void write_edge_total(const jl_magat_t& m, int slice, long long total) {
+    const int parts = (m.n_agents + kEdgeSources - 1) / kEdgeSources;
+    if (slice == m.n_envs * parts - 1) {
+        m.env_edge_base[m.n_envs] = total;
+        m.num_edges[0] = total;
+        m.edge_prefix[(size_t)m.n_envs * m.n_agents] = total;
+    }
+}
 
 // Edge workgroup LDS: positions padded to a multiple of kEdgeSpan with cells
 // far off every map (never within the radius), one ring of pending edges per
@@ -403,6 +433,7 @@ __host__ __device__ inline size_t edge_lds(int A) {
 // source would run with a seventh of the lanes).  Edges are ordered by
 // (source, destination id), the reference's order (stateless_step.cu:
 // 854-935); each sits at its source's first offset plus its rank.
+template <bool kSummed>
 __global__ __launch_bounds__(kEdgeThreads) void edges_kernel(jl_magat_t m) {
     extern __shared__ __align__(16) int32_t s_xy[];  // (int16 x, int16 y) per agent, padded
     __shared__ long long s_wave[kEdgeWaves];
@@ -419,6 +450,7 @@ __global__ __launch_bounds__(kEdgeThreads) void edges_kernel(jl_magat_t m) {
     const int tid = threadIdx.x, lane = tid & (kWave - 1);
     const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);  // uniform per wavefront
     const size_t base = (size_t)env * A;
+    long long before = slice_totals_before<kSummed>(m, env * parts + part);
     for (int a = tid; a < padded; a += kEdgeThreads) {
         int32_t xy = 0x40004000;  // padding: (16384, 16384)
         if (a < A) {
@@ -429,11 +461,11 @@ __global__ __launch_bounds__(kEdgeThreads) void edges_kernel(jl_magat_t m) {
         }
         s_xy[a] = xy;
     }
-    const long long env_base = m.env_edge_base[env];
+    const long long env_base = kSummed ? 0 : m.env_edge_base[env];
     __syncthreads();
-    // counts of the agents before the slice
-    long long before = 0;
-    for (int a = tid; a < s_begin; a += kEdgeThreads) before += s_cnt[a];
+    // counts of the env's agents before the slice (bases from env_scan_kernel)
+    if constexpr (!kSummed)
+        for (int a = tid; a < s_begin; a += kEdgeThreads) before += s_cnt[a];
     for (int off = kWave / 2; off > 0; off >>= 1) before += __shfl_xor(before, off, kWave);
     if (lane == 0) s_wave[wave] = before;
     __syncthreads();
@@ -451,6 +483,7 @@ __global__ __launch_bounds__(kEdgeThreads) void edges_kernel(jl_magat_t m) {
             s_first[lane] = first + incl - c;
             m.edge_prefix[base + a] = first + incl - c;
         }
+        if (kSummed && lane == kWave - 1) write_edge_total(m, env * parts + part, first + incl);
     }
     __syncthreads();
     const long long cap = m.edge_capacity;
@@ -532,20 +565,27 @@ __host__ __device__ inline size_t edge_mask_lds(int A) {
 }
 
 // Edge writer for envs of at most kMaskMaxAgents agents.  Workgroup = (env,
-// slice of kEdgeSources sources), as above.  Lane l of wavefront w tests
-// source s_begin + l against the ids of chunks w, w + 4, ... and keeps the
-// neighbour bits of each 64-id chunk in LDS (with positions in [-8192, 8191]
-// the differences and their squares fit packed int16 / one dot2 per pair;
-// other envs take 32-bit arithmetic).  Then every thread takes output
-// positions i = tid, tid + 256, ... of the slice's contiguous edge range:
-// source = the last one whose first offset is <= i, destination = the
-// (i - first)-th set bit of its mask, so consecutive lanes store consecutive
-// edges.  A position past a source's recomputed neighbours (a skipped row
-// whose stored count is stale) is left as it is.
+// slice of kEdgeSources sources), as above.  The env's positions and counts
+// are loaded first, then (kSummed) this thread's share of the node pass's
+// slice totals before the slice, which stay in flight, in registers, until
+// the masks are built: the barriers in between order LDS only.  Lane l of
+// wavefront w tests source s_begin + l against the ids of chunks w, w + 4,
+// ... and keeps the neighbour bits of each 64-id chunk in LDS (with
+// positions in [-8192, 8191] the differences and their squares fit packed
+// int16 / one dot2 per pair; other envs take 32-bit arithmetic).  Then every
+// thread takes output positions i = tid, tid + 256, ... of the slice's
+// contiguous edge range: source = the last one whose first offset is <= i,
+// destination = the (i - first)-th set bit of its mask, so consecutive lanes
+// store consecutive edges.  A position past a source's recomputed neighbours
+// (a skipped row whose stored count is stale) is left as it is.
+constexpr int kMaskStage = kMaskMaxAgents / kEdgeThreads;  // staged agents per thread
+constexpr int kMaskTotals = 8;  // slice totals per thread held in registers (2,048 slices)
+
+template <bool kSummed>
 __global__ __launch_bounds__(kEdgeThreads) void edges_mask_kernel(jl_magat_t m) {
     extern __shared__ __align__(16) uint64_t s_mask[];  // [chunk][source of the slice]
     __shared__ long long s_wave[kEdgeWaves];
-    __shared__ long long s_slice_first;
+    __shared__ int s_wide[kEdgeWaves];
     __shared__ int s_rel[kEdgeSources + 1];  // first edge of each source, relative to the slice's
     const int A = m.n_agents;
     const int chunks = (A + kWave - 1) / kWave;
@@ -555,33 +595,58 @@ __global__ __launch_bounds__(kEdgeThreads) void edges_mask_kernel(jl_magat_t m) 
     const int parts = (A + kEdgeSources - 1) / kEdgeSources;
     const int env = blockIdx.x / parts;
     const int part = blockIdx.x - env * parts;
+    const int slice = blockIdx.x;
     const int s_begin = part * kEdgeSources;
     const int s_end = (s_begin + kEdgeSources) < A ? (s_begin + kEdgeSources) : A;
     const int tid = threadIdx.x, lane = tid & (kWave - 1);
     const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);  // uniform per wavefront
     const size_t base = (size_t)env * A;
-    int wide = 0;
-    for (int a = tid; a < padded; a += kEdgeThreads) {
-        int32_t xy = 0x40004000;  // padding: (16384, 16384), never within the radius
+    // the env's positions and counts, then the slice totals (in that order:
+    // loads complete in issue order, and the totals are needed last)
+    float2 pos[kMaskStage];
+    int32_t cnt[kMaskStage];
+#pragma unroll
+    for (int k = 0; k < kMaskStage; ++k) {
+        const int a = tid + k * kEdgeThreads;
         if (a < A) {
-            const float2 p = reinterpret_cast<const float2*>(m.pyg_pos)[base + a];
-            const int x = (int16_t)p.x, y = (int16_t)p.y;
-            wide |= (x < -8192 || x > 8191 || y < -8192 || y > 8191) ? 1 : 0;
-            xy = (x & 0xFFFF) | (y << 16);
-            s_cnt[a] = m.edge_counts[base + a];
+            pos[k] = reinterpret_cast<const float2*>(m.pyg_pos)[base + a];
+            cnt[k] = m.edge_counts[base + a];
         }
-        s_xy[a] = xy;
     }
-    const long long env_base = m.env_edge_base[env];
-    wide = __syncthreads_or(wide);
-    long long before = 0;
-    for (int a = tid; a < s_begin; a += kEdgeThreads) before += s_cnt[a];
-    for (int off = kWave / 2; off > 0; off >>= 1) before += __shfl_xor(before, off, kWave);
-    if (lane == 0) s_wave[wave] = before;
-    __syncthreads();
+    long long tot[kMaskTotals];
+    if constexpr (kSummed) {
+        const int64_t* totals = m.env_edge_base + m.n_envs + 1;
+#pragma unroll
+        for (int k = 0; k < kMaskTotals; ++k) {
+            const int j = tid + k * kEdgeThreads;
+            tot[k] = j < slice ? totals[j] : 0;
+        }
+    }
+    int wide = 0;
+#pragma unroll
+    for (int k = 0; k < kMaskStage; ++k) {
+        const int a = tid + k * kEdgeThreads;
+        if (a < padded) {
+            int32_t xy = 0x40004000;  // padding: (16384, 16384), never within the radius
+            if (a < A) {
+                const int x = (int16_t)pos[k].x, y = (int16_t)pos[k].y;
+                wide |= (x < -8192 || x > 8191 || y < -8192 || y > 8191) ? 1 : 0;
+                xy = (x & 0xFFFF) | (y << 16);
+                s_cnt[a] = cnt[k];
+            }
+            s_xy[a] = xy;
+        }
+    }
+    const long long env_base = kSummed ? 0 : m.env_edge_base[env];
+    if (lane == 0) s_wide[wave] = 0;
+    wave_sync();
+    if (wide) s_wide[wave] = 1;
+    lds_barrier();
+    wide = 0;
+#pragma unroll
+    for (int k = 0; k < kEdgeWaves; ++k) wide |= s_wide[k];
     if (wave == 0) {
-        long long first = env_base;
-        for (int k = 0; k < kEdgeWaves; ++k) first += s_wave[k];
+        // offsets of the slice's sources relative to its first edge
         const int a = s_begin + lane;
         const int c = a < s_end ? s_cnt[a] : 0;
         int incl = c;
@@ -589,10 +654,8 @@ __global__ __launch_bounds__(kEdgeThreads) void edges_mask_kernel(jl_magat_t m) 
             const int t = __shfl_up(incl, off, kWave);
             if (lane >= off) incl += t;
         }
-        if (a < s_end) m.edge_prefix[base + a] = first + incl - c;
         s_rel[lane] = incl - c;
         if (lane == kWave - 1) s_rel[kWave] = incl;
-        if (lane == 0) s_slice_first = first;
     }
     {
         const int a = s_begin + lane;
@@ -632,12 +695,32 @@ __global__ __launch_bounds__(kEdgeThreads) void edges_mask_kernel(jl_magat_t m) 
             s_mask[c * kEdgeSources + lane] = bits;
         }
     }
-    __syncthreads();
-    const long long cap = m.edge_capacity;
-    int64_t* dst_index = m.edge_index + cap;
+    // the slice's first edge: totals of the slices before it (kSummed), or
+    // the env's scanned base plus the counts of its agents before the slice
+    long long before = 0;
+    if constexpr (kSummed) {
+#pragma unroll
+        for (int k = 0; k < kMaskTotals; ++k) before += tot[k];
+        const int64_t* totals = m.env_edge_base + m.n_envs + 1;
+        for (int j = tid + kMaskTotals * kEdgeThreads; j < slice; j += kEdgeThreads) before += totals[j];
+    } else {
+        for (int a = tid; a < s_begin; a += kEdgeThreads) before += s_cnt[a];
+    }
+    for (int off = kWave / 2; off > 0; off >>= 1) before += __shfl_xor(before, off, kWave);
+    if (lane == 0) s_wave[wave] = before;
+    lds_barrier();
+    long long slice_first = env_base;
+#pragma unroll
+    for (int k = 0; k < kEdgeWaves; ++k) slice_first += s_wave[k];
     const int nsrc = s_end - s_begin;
     const int total = s_rel[nsrc];
-    const long long slice_first = s_slice_first;
+    if (wave == 0) {
+        const int a = s_begin + lane;
+        if (a < s_end) m.edge_prefix[base + a] = slice_first + s_rel[lane];
+        if (kSummed && lane == 0) write_edge_total(m, slice, slice_first + total);
+    }
+    const long long cap = m.edge_capacity;
+    int64_t* dst_index = m.edge_index + cap;
     for (int i = tid; i < total; i += kEdgeThreads) {
         int sl = 0;  // the last source whose first edge is <= i
 #pragma unroll
@@ -677,8 +760,9 @@ __global__ __launch_bounds__(kEdgeThreads) void edges_mask_kernel(jl_magat_t m) 
             const int32_t sxy = s_xy[a], oxy = s_xy[o];
             const int dx = (int16_t)(sxy & 0xFFFF) - (int16_t)(oxy & 0xFFFF);
             const int dy = (sxy >> 16) - (oxy >> 16);
-            m.edge_index[e] = (int64_t)(base + a);
-            dst_index[e] = (int64_t)(base + o);
+            // index rows leave as whole lines (consecutive lanes, consecutive edges)
+            __builtin_nontemporal_store((int64_t)(base + a), &m.edge_index[e]);
+            __builtin_nontemporal_store((int64_t)(base + o), &dst_index[e]);
             float* attr = m.edge_attr + e * 3;
             attr[0] = (float)dx;
             attr[1] = (float)dy;
@@ -731,18 +815,29 @@ extern "C" int jl_magat_edges(const jl_magat_t* m, jl_stream_t stream) {
         return JL_ERR_ARG;
     if (m->edge_capacity < (int64_t)m->n_envs * m->n_agents * (m->n_agents - 1))
         return JL_ERR_CAPACITY;
-    hipLaunchKernelGGL(env_scan_kernel, dim3(1), dim3(1024), 0, (hipStream_t)stream, *m);
-    rc = launch_status();
-    if (rc) return rc;
     const unsigned eparts = (unsigned)((m->n_agents + kEdgeSources - 1) / kEdgeSources);
-    if (m->n_agents <= kMaskMaxAgents) {
-        hipLaunchKernelGGL(edges_mask_kernel, dim3((unsigned)m->n_envs * eparts), dim3(kEdgeThreads),
-                           edge_mask_lds(m->n_agents), (hipStream_t)stream, *m);
-        return launch_status();
-    }
+    const size_t slices = (size_t)m->n_envs * eparts;
+    const bool summed = slices <= (size_t)kSummedSlices;
     const size_t elds = edge_lds(m->n_agents);
-    if (elds > 160 * 1024) return JL_ERR_ARG;
-    hipLaunchKernelGGL(edges_kernel, dim3((unsigned)m->n_envs * eparts), dim3(kEdgeThreads), elds,
-                       (hipStream_t)stream, *m);
+    if (m->n_agents > kMaskMaxAgents && elds > 160 * 1024) return JL_ERR_ARG;
+    if (!summed) {
+        hipLaunchKernelGGL(env_scan_kernel, dim3(1), dim3(1024), 0, (hipStream_t)stream, *m);
+        rc = launch_status();
+        if (rc) return rc;
+    }
+    const dim3 grid((unsigned)slices), block(kEdgeThreads);
+    if (m->n_agents <= kMaskMaxAgents) {
+        if (summed) {
+            hipLaunchKernelGGL(edges_mask_kernel<true>, grid, block, edge_mask_lds(m->n_agents),
+                               (hipStream_t)stream, *m);
+        } else {
+            hipLaunchKernelGGL(edges_mask_kernel<false>, grid, block, edge_mask_lds(m->n_agents),
+                               (hipStream_t)stream, *m);
+        }
+    } else if (summed) {
+        hipLaunchKernelGGL(edges_kernel<true>, grid, block, elds, (hipStream_t)stream, *m);
+    } else {
+        hipLaunchKernelGGL(edges_kernel<false>, grid, block, elds, (hipStream_t)stream, *m);
+    }
     return launch_status();
 }

@@ -1674,15 +1674,6 @@ inline int pass1_waves(int W, int H) {
     return field <= 16384 ? 4 : (field <= 32768 ? 2 : 1);
 }
 
-// Compute units of the current device (the BFS grid is sized to them).
-inline int device_cus() {
-    int dev = 0, cus = 0;
-    if (hipGetDevice(&dev) != hipSuccess) return 256;
-    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
-        return 256;
-    return cus > 0 ? cus : 256;
-}
-
 template <int H, int R, bool kRows>
 int launch_pass1(const jl_mapfgpt_t* b, const int16_t* rows, const int16_t* cx, const int16_t* cy,
                  const int16_t* gx, const int16_t* gy, hipStream_t stream) {

@@ -781,42 +781,40 @@ __global__ __launch_bounds__(256) void copy_actions_kernel(uint8_t* __restrict__
 // Inclusive int64 prefix sum of the goal_changed values and its last value
 // (the int64 cast, cumsum and count of GridWorldSimulator::
 // update_derived_state, grid_world_simulator.cpp:709-717).  Workgroup w
-// scans values [w * kScanChunk, (w + 1) * kScanChunk): it sums every value
-// before its range itself (16 bytes per load, from the L2), so workgroups
-// never wait for each other, scans its own range through LDS and writes the
-// prefixes with consecutive lanes on consecutive values.
-constexpr int kScanThreads = 1024;  // at 4096 values per workgroup, a thread's share of the
-                                    // values before its chunk (<= 8 x 16 bytes per 128 K
-                                    // values) is one batch of loads
-constexpr int kScanPer = 4;                             // values per thread
-constexpr int kScanChunk = kScanThreads * kScanPer;     // values per workgroup
+// scans values [w * chunk, (w + 1) * chunk), chunk = kScanThreads * PER: it
+// sums every value before its range itself (16 bytes per load, from the L2),
+// so workgroups never wait for each other, scans its own range (through LDS
+// when a thread holds more than one value) and writes the prefixes with
+// consecutive lanes on consecutive values.  PER grows with N only past 128
+// workgroups of one value per thread, so that small batches spread over as
+// many CUs as the chunks allow.
+constexpr int kScanThreads = 1024;
+constexpr int kScanWorkgroups = 128;  // PER = 1 up to this many workgroups, then 2, then 4
 
-__device__ __forceinline__ uint32_t byte_sum(uint32_t w) {
-    return (w & 0xFFu) + ((w >> 8) & 0xFFu) + ((w >> 16) & 0xFFu) + (w >> 24);
-}
-
+template <int PER>
 __global__ __launch_bounds__(kScanThreads) void goal_changed_scan_kernel(jl_sim_t s, int64_t* prefix,
                                                                          int64_t* count,
                                                                          uint16_t* changed) {
+    constexpr int kChunk = kScanThreads * PER;
     __shared__ int64_t s_wave[kScanThreads / kWave];
-    __shared__ int64_t s_out[kScanChunk];
+    __shared__ int64_t s_out[PER > 1 ? kChunk : 1];
     const int tid = threadIdx.x, lane = tid & (kWave - 1);
     const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);  // uniform per wavefront
     const int64_t N = (int64_t)s.n_envs * s.n_agents;
-    const int64_t c0 = (int64_t)blockIdx.x * kScanChunk;
+    const int64_t c0 = (int64_t)blockIdx.x * kChunk;
     const uint8_t* f = s.goal_changed;
-    // this thread's kScanPer consecutive values, loaded first so that they
-    // travel with the loads of the values before the chunk
-    const int64_t e0 = c0 + (int64_t)tid * kScanPer;
-    uint32_t v[kScanPer];
+    // this thread's PER consecutive values, loaded first so that they travel
+    // with the loads of the values before the chunk
+    const int64_t e0 = c0 + (int64_t)tid * PER;
+    uint32_t v[PER];
 #pragma unroll
-    for (int j = 0; j < kScanPer; ++j) v[j] = e0 + j < N ? f[e0 + j] : 0u;
+    for (int j = 0; j < PER; ++j) v[j] = e0 + j < N ? f[e0 + j] : 0u;
     // the changed-row buffer is cleared before the energy pass packs into it
     // (the reference zero-fills it, grid_world_simulator.cpp:724-733)
     if (changed) {
         const uint4 zero = make_uint4(0, 0, 0, 0);
 #pragma unroll
-        for (int j = 0; j < kScanPer; ++j) {
+        for (int j = 0; j < PER; ++j) {
             const int64_t e = c0 + tid + j * kScanThreads;
             if (e < N) reinterpret_cast<uint4*>(changed)[e] = zero;
         }
@@ -837,30 +835,37 @@ __global__ __launch_bounds__(kScanThreads) void goal_changed_scan_kernel(jl_sim_
     int64_t base = 0;
     for (int k = 0; k < kScanThreads / kWave; ++k) base += s_wave[k];
     __syncthreads();
-    // this thread's values, scanned across the workgroup
+    // this thread's values, scanned across the workgroup: a wavefront's sum
+    // is at most 64 * PER * 255, so 32 bits hold it
     uint32_t local = 0;
 #pragma unroll
-    for (int j = 0; j < kScanPer; ++j) local += v[j];
-    int64_t incl = local;
+    for (int j = 0; j < PER; ++j) local += v[j];
+    uint32_t incl = local;
     for (int off = 1; off < kWave; off <<= 1) {
-        const int64_t t = __shfl_up(incl, off, kWave);
+        const uint32_t t = __shfl_up(incl, off, kWave);
         if (lane >= off) incl += t;
     }
     if (lane == kWave - 1) s_wave[wave] = incl;
     __syncthreads();
-    int64_t run = base + incl - local;
+    int64_t run = base + (int64_t)(incl - local);
     for (int k = 0; k < wave; ++k) run += s_wave[k];
+    if constexpr (PER == 1) {
+        run += v[0];
+        if (e0 < N) prefix[e0] = run;
+        if (e0 == N - 1) count[0] = run;
+    } else {
 #pragma unroll
-    for (int j = 0; j < kScanPer; ++j) {
-        run += v[j];
-        s_out[tid * kScanPer + j] = run;
-    }
-    __syncthreads();
+        for (int j = 0; j < PER; ++j) {
+            run += v[j];
+            s_out[tid * PER + j] = run;
+        }
+        __syncthreads();
 #pragma unroll
-    for (int j = 0; j < kScanPer; ++j) {
-        const int64_t e = c0 + tid + j * kScanThreads;
-        if (e < N) prefix[e] = s_out[tid + j * kScanThreads];
-        if (e == N - 1) count[0] = s_out[tid + j * kScanThreads];
+        for (int j = 0; j < PER; ++j) {
+            const int64_t e = c0 + tid + j * kScanThreads;
+            if (e < N) prefix[e] = s_out[tid + j * kScanThreads];
+            if (e == N - 1) count[0] = s_out[tid + j * kScanThreads];
+        }
     }
 }
 
@@ -958,8 +963,19 @@ extern "C" int jl_goal_changed_scan(const jl_sim_t* s, int64_t* prefix, int64_t*
     if (rc) return rc;
     if (!prefix || !count) return JL_ERR_ARG;
     const int64_t N = (int64_t)s->n_envs * s->n_agents;
-    hipLaunchKernelGGL(goal_changed_scan_kernel, dim3((unsigned)((N + kScanChunk - 1) / kScanChunk)),
-                       dim3(kScanThreads), 0, (hipStream_t)stream, *s, prefix, count, changed_states);
+    const int64_t one = (int64_t)kScanThreads * kScanWorkgroups;
+    if (N <= one) {
+        hipLaunchKernelGGL(goal_changed_scan_kernel<1>, dim3((unsigned)((N + kScanThreads - 1) / kScanThreads)),
+                           dim3(kScanThreads), 0, (hipStream_t)stream, *s, prefix, count, changed_states);
+    } else if (N <= 2 * one) {
+        hipLaunchKernelGGL(goal_changed_scan_kernel<2>,
+                           dim3((unsigned)((N + 2 * kScanThreads - 1) / (2 * kScanThreads))), dim3(kScanThreads), 0,
+                           (hipStream_t)stream, *s, prefix, count, changed_states);
+    } else {
+        hipLaunchKernelGGL(goal_changed_scan_kernel<4>,
+                           dim3((unsigned)((N + 4 * kScanThreads - 1) / (4 * kScanThreads))), dim3(kScanThreads), 0,
+                           (hipStream_t)stream, *s, prefix, count, changed_states);
+    }
     return launch_status();
 }
 

@@ -681,14 +681,27 @@ class GridWorldSimulator(_Base, _PygModeMixin, _PygStorage):
 
     def update_derived_state(self) -> None:
         """Energy fields of changed goals (grid_world_simulator.cpp:707-753), no host sync."""
-        full = self.current_step == 1
-        # after the first step the changed-row buffer is cleared, then packed
+        if self.current_step != 1:
+            # the changed-row buffer is cleared, then packed; the fields of
+            # the changed goals are refreshed
+            check(
+                self._lib.jl_goal_changed_refresh(
+                    self._sim_ref,
+                    self.t_energy_maps.data_ptr(),
+                    self.t_goal_changed_prefix.data_ptr(),
+                    self.t_goal_changed_count.data_ptr(),
+                    self.t_changed_state_packed.data_ptr(),
+                    _stream(self._device),
+                ),
+                "Incremental energy map kernel",
+            )
+            return
         check(
             self._lib.jl_goal_changed_scan(
                 self._sim_ref,
                 self.t_goal_changed_prefix.data_ptr(),
                 self.t_goal_changed_count.data_ptr(),
-                None if full else self.t_changed_state_packed.data_ptr(),
+                None,
                 _stream(self._device),
             ),
             "Goal-changed scan",
@@ -697,7 +710,7 @@ class GridWorldSimulator(_Base, _PygModeMixin, _PygStorage):
             self._lib.jl_energy_maps_flagged(
                 self._sim_ref,
                 self.t_energy_maps.data_ptr(),
-                1 if full else 0,
+                1,
                 self.t_goal_changed_prefix.data_ptr(),
                 self.t_changed_state_packed.data_ptr(),
                 _stream(self._device),

@@ -294,12 +294,23 @@ int jl_energy_maps(const uint32_t* grid_bits, uint8_t* energy,
  * arrays.  Unless `all_agents`, each changed agent's state row (reset_flag 1)
  * is also written to changed_states[changed_prefix[g] - 1], where
  * changed_prefix is the inclusive int64 prefix sum of the flags
- * (pack_changed_agent_state_kernel, 128_agents_map_step.cu:469-511).
+ * (pack_changed_agent_state_kernel, 128_agents_map_step.cu:469-511); when
+ * its last value is 0 (no flag set) the launch returns at once.
  * Replaces GridWorldSimulator::update_derived_state,
  * grid_world_simulator.cpp:707-753, without its host synchronisation. */
 int jl_energy_maps_flagged(const jl_sim_t* sim, uint8_t* energy,
                            int32_t all_agents, const int64_t* changed_prefix,
                            uint16_t* changed_states, jl_stream_t stream);
+
+/* The incremental half of GridWorldSimulator::update_derived_state
+ * (grid_world_simulator.cpp:707-753) in one call: jl_goal_changed_scan and
+ * jl_energy_maps_flagged (all_agents 0) with the same outputs (prefix, count,
+ * changed_states cleared and packed, energy fields of the changed agents),
+ * as one launch for at most 131,072 agents on maps of at most 4,096 cells
+ * and 64 rows, as the two launches otherwise.  changed_states may be NULL
+ * (nothing packed). */
+int jl_goal_changed_refresh(const jl_sim_t* sim, uint8_t* energy, int64_t* prefix, int64_t* count,
+                            uint16_t* changed_states, jl_stream_t stream);
 
 /* ------------------------------------------------------------------------ */
 /* MAGAT builder (StatelessGridWorldContext, grid_world_cuda.h:99-117)        */
