@@ -190,6 +190,27 @@ def copy_calibration() -> None:
     print(f"copied 3 x {n} bytes", flush=True)
 
 
+def fetch_probe() -> None:
+    """Three launches of jl_hbm_stream kind 10 over 256 MiB: one isolated
+    16-byte read per 256-byte block (1,048,576 reads), the reference reading
+    for the bytes the L2 fetches per read under the FETCH_SIZE counter."""
+    import torch
+
+    from iclr_2027_jointoom_amd._abi import check, load_library
+
+    lib = load_library()
+    n = 256 << 20
+    a = torch.ones(n // 4, dtype=torch.int32, device="cuda")
+    sink = torch.zeros(1 << 16, dtype=torch.int32, device="cuda")
+    stream = torch.cuda.current_stream().cuda_stream
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    torch.cuda.synchronize()
+    for _ in range(3):
+        check(lib.jl_hbm_stream(10, a.data_ptr(), None, n, sink.data_ptr(), cus * 4, stream), "fetch probe")
+    torch.cuda.synchronize()
+    print(f"3 x {n // 256} isolated 16-byte reads", flush=True)
+
+
 def achievable_bandwidth(reps: int = 10) -> dict:
     """HBM bandwidth a plain streaming kernel of this library reaches on the
     device (jl_hbm_stream: 16-byte non-temporal loads, non-temporal or plain
@@ -1229,6 +1250,8 @@ def main() -> int:
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--copy-calibration", action="store_true",
                    help="only run 3 device copies of 256 MiB (PMC byte-counter calibration)")
+    p.add_argument("--fetch-probe", action="store_true",
+                   help="only run 3 x 1,048,576 isolated 16-byte reads (HBM fetch granularity under FETCH_SIZE)")
     p.add_argument("--graph", action="store_true",
                    help="replay each step from a captured HIP graph (iclr_2027_jointoom_amd/graphs.py)")
     p.add_argument("--workload", choices=("resident", "magat", "c5", "ring", "costtracer", "fresh"),
@@ -1278,6 +1301,9 @@ def main() -> int:
             args.cpu_steps = 2000  # ~2 s per worker of the C restatement
     if args.copy_calibration:
         copy_calibration()
+        return 0
+    if args.fetch_probe:
+        fetch_probe()
         return 0
     if args.gpus != 1:
         print(

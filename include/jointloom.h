@@ -467,7 +467,9 @@ int jl_decode_to_uint8(const uint16_t* obs, uint8_t* out, int64_t n_batch,
  * with each workgroup streaming one contiguous chunk instead (5 read, 6 and
  * 7 write and copy non-temporal, 8 and 9 write and copy plain).  The
  * bandwidth a plain streaming kernel reaches on the device, the "achievable"
- * figure beside the published peak. */
+ * figure beside the published peak.  Kind 10 reads one 16-byte word at the
+ * start of every 256-byte block of `src` (bytes a multiple of 256), for the
+ * HBM fetch granularity under the FETCH_SIZE counter. */
 int jl_hbm_stream(int32_t kind, const void* src, void* dst, int64_t bytes, uint32_t* sink,
                   int32_t workgroups, jl_stream_t stream);
 
