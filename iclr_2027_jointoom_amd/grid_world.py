@@ -22,7 +22,7 @@ import types
 
 import torch
 
-from ._abi import BUILD_SCRATCH_WORDS, GAVE_UP_WORD, MagatDesc, MapfGPTDesc, SimDesc, check, load_library, tiled_field_cells
+from ._abi import BUILD_SCRATCH_WORDS, GAVE_UP_WORD, MagatDesc, MapfGPTDesc, SimDesc, check, field_cells, load_library
 
 TASK_LIFELONG = 0
 TASK_STANDARD_MAPF = 1
@@ -275,7 +275,7 @@ class MapfGPTObservationBuilder(_Base):
             # cells (the token pass reads its windows there); -1 is unreachable
             self._agent_info = torch.zeros((N,), dtype=torch.int32, device=device)
             self._cost_tiles = torch.full(
-                (E, n_agents, tiled_field_cells(W, H)), -1, dtype=torch.int16, device=device
+                (E, n_agents, field_cells(W, H)), -1, dtype=torch.int16, device=device
             )
             # single-launch builds: number of the last launch whose diagnostics
             # were cleared (uint64) and workgroup arrival counters; zero at

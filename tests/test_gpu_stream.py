@@ -1,6 +1,7 @@
 """The HBM streaming probe (jl_hbm_stream) behind bench.py's achievable
 bandwidth: a copy reproduces its source, a write fills the whole range with
-the probe's pattern, and a read leaves its buffers alone."""
+the probe's pattern, and a read (streaming or one word per 256-byte block)
+leaves its buffers alone."""
 import numpy as np
 import pytest
 
@@ -29,9 +30,11 @@ def test_stream_probe_copy_write_read():
         assert (words[:, 0] == 0x01010101).all() and (words[:, 1] == 0x02020202).all()
         assert (words[:, 2] == 0x03030303).all() and (words[:, 3] < 37).all()
     before = src.clone()
-    for read_kind in (0, 5):
+    # kind 10: one 16-byte read per 256-byte block (the fetch-granularity probe)
+    for read_kind in (0, 5, 10):
         check(lib.jl_hbm_stream(read_kind, src.data_ptr(), None, n, sink.data_ptr(), 37, stream), "read")
         torch.cuda.synchronize()
         assert torch.equal(src, before)
-    assert lib.jl_hbm_stream(10, src.data_ptr(), dst.data_ptr(), n, sink.data_ptr(), 37, stream) == -1
+    assert lib.jl_hbm_stream(11, src.data_ptr(), dst.data_ptr(), n, sink.data_ptr(), 37, stream) == -1
+    assert lib.jl_hbm_stream(10, src.data_ptr(), None, n - 16, sink.data_ptr(), 37, stream) == -1
     assert lib.jl_hbm_stream(2, src.data_ptr(), dst.data_ptr(), n + 8, sink.data_ptr(), 37, stream) == -1
