@@ -731,7 +731,9 @@ void jlo_mapfgpt_append(const jl_mapfgpt_t* b, const uint8_t* actions) {
 
 /* refresh_occ_bitmap_from_packed_states_kernel, stateless_step.cu:140-173:
  * block j covers rows [j*A, (j+1)*A); the env of its first row is cleared
- * and the cells of rows with a valid env id are set. */
+ * and the cells of rows with a valid env id are set.  A position off the map
+ * sets no bit (the reference's word index would fall outside the env's
+ * bitmap, :168-170; the device kernel skips it the same way). */
 void jlo_magat_occupancy(const jl_magat_t* m) {
     const int E = m->n_envs, A = m->n_agents, W = m->map_w, H = m->map_h;
     const int words = W * H / 32;
@@ -743,6 +745,7 @@ void jlo_magat_occupancy(const jl_magat_t* m) {
         for (int i = 0; i < A; ++i) {
             const uint16_t* r = m->states + ((size_t)j * A + i) * 8;
             if (r[0] >= E) continue;
+            if (r[2] >= W || r[3] >= H) continue;  /* uint16: negative positions are large */
             const int cell = r[2] * H + r[3];
             occ[cell >> 5] |= 1u << (cell & 31);
         }

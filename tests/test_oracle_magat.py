@@ -159,6 +159,35 @@ def test_occupancy_kat(oracle):
     assert all(bit(x, y) for x, y in kat["set"]) and not any(bit(x, y) for x, y in kat["unset"])
 
 
+def test_occupancy_skips_positions_off_the_map(oracle):
+    """Rows at positions off the map (negative, at W or H, the int16
+    extremes) set no bit and touch nothing outside the env's bitmap: env 0
+    (every agent off the map) stays clear, env 1 (half of them off) equals
+    the bitmap of its on-map rows alone, and env 2 (rows with no valid env
+    id, never written) stays clear."""
+    E, W, A = 3, 32, 6
+    grids = np.zeros((E, W, W), np.uint8)
+    starts = np.zeros((E, A, 2), np.int16)
+    starts[:, :, 0] = np.arange(A)[None, :] * 3
+    starts[:, :, 1] = np.arange(A)[None, :] * 5
+    off = np.asarray([(-1, 0), (0, -1), (W, 0), (0, W), (-32768, 32767), (9000, -9000)], np.int16)
+    far = starts.copy()
+    far[0] = off
+    far[1, 3:] = off[:3]
+    goals = np.zeros((E, A, 2), np.int16)
+    rows = state_rows(E, A, far, goals, reset=0)
+    rows.reshape(E, A, 8)[2, :, 0] = 0xFFFF
+    m = oracle.OracleMagat(grids, A)
+    m.refresh(rows)
+    on_map = state_rows(E, A, starts, goals, reset=0)
+    on_map.reshape(E, A, 8)[1, 3:, 0] = 0xFFFF  # the off-map agents of env 1 left out
+    ref = oracle.OracleMagat(grids, A)
+    ref.refresh(on_map)
+    assert not m.grid_ocp[0].any()
+    assert np.array_equal(m.grid_ocp[1], ref.grid_ocp[1]) and m.grid_ocp[1].any()
+    assert not m.grid_ocp[2].any()
+
+
 def test_local_gather_kats(oracle):
     kat = json.loads((GOLDEN / "magat_kats.json").read_text())["local_gather"]
     A = kat["n_agents"]
