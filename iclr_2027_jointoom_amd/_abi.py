@@ -22,14 +22,6 @@ def tiled_field_cells(map_w: int, map_h: int) -> int:
     8x8 tiles over the map plus a one-tile border of unreachable cells."""
     return ((map_w + 7) // 8 + 2) * (map_h // 8 + 2) * 64
 
-
-def field_cells(map_w: int, map_h: int) -> int:
-    """uint16 cells one agent's field takes in cost_tiles: on maps of at most
-    4096 cells the tiled field twice (the second copy 64 bytes off the first's
-    128-byte lines) plus 64 cells, else once."""
-    t = tiled_field_cells(map_w, map_h)
-    return 2 * t + 64 if map_w * map_h <= 4096 else t
-
 c_void_p = ctypes.c_void_p
 c_int32 = ctypes.c_int32
 c_int64 = ctypes.c_int64

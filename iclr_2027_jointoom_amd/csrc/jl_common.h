@@ -76,20 +76,6 @@ __host__ __device__ inline size_t tiled_cells(int W, int H) {
 }
 // Cells of one column strip (its TR tiles).
 __host__ __device__ inline uint32_t strip_cells(int W) { return (uint32_t)tile_grid_rows(W) * 64u; }
-// On maps of at most kMarkedCells cells each field is stored twice: the
-// tiled layout above, then (tiled_cells + 32) cells further on the same words
-// again, 64 bytes off the 128-byte lines of the first (the field's stride and
-// cost_tiles are 128-byte aligned), so that the 11 strip rows of any window
-// lie in two lines of one of the two copies.  field_cells: a field's stride
-// in cost_tiles; shifted_copy_cells: the second copy from the first.
-__host__ __device__ inline size_t field_cells(int W, int H) {
-    return marked_fields(W, H) ? 2 * tiled_cells(W, H) + 64 : tiled_cells(W, H);
-}
-__host__ __device__ inline size_t shifted_copy_cells(int W, int H) { return tiled_cells(W, H) + 32; }
-// A window whose first row is x0 occupies strip words x0 + 8 .. x0 + 18:
-// two lines of the first copy when (x0 + 8) mod 8 <= 5, else two of the
-// second (whose lines start four words earlier).
-__host__ __device__ inline bool window_in_shifted_copy(int x0) { return ((x0 + 8) & 7) >= 6; }
 // Offset of cell (x, y) in a tiled field, for -8 <= x < W + 8, -8 <= y < H + 8.
 __device__ __forceinline__ uint32_t tile_offset(int x, int y, int W) {
     return (uint32_t)((y >> 3) + 1) * strip_cells(W) + (uint32_t)(x + 8) * 8u + (uint32_t)(y & 7);

@@ -64,7 +64,7 @@ __global__ __launch_bounds__(256) void reward_goals_kernel(jl_sim_t s, const uin
     const int b0 = best[i];
     const int k = cursor[i];
     const int xc = x < W ? x : W - 1, yc = y < H ? y : H - 1;
-    const int d = (int)field_distance(tiles[(size_t)i * field_cells(W, H) + tile_offset(xc, yc, W)],
+    const int d = (int)field_distance(tiles[(size_t)i * tiled_cells(W, H) + tile_offset(xc, yc, W)],
                                       field_mask(W, H));
     rewards[i] = d < b0 ? 0.1f : 0.0f;
     int bn = min(b0, d);
@@ -94,7 +94,7 @@ __device__ __forceinline__ void observe_agents(const jl_sim_t& s, const jl_mapfg
                                                int32_t* __restrict__ best, float* o, int i0,
                                                int nvalid, int lane) {
     const int W = s.map_w, A = s.n_agents;
-    const size_t tcells = field_cells(W, H);  // a field's stride
+    const size_t tcells = tiled_cells(W, H);
     const uint32_t fmask = field_mask(W, H);
     const int words = W * H / 32;
     // lane k < nvalid fetches agent i0 + k's position, best and refresh flag

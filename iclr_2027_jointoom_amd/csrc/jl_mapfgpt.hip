@@ -201,7 +201,7 @@ __device__ __forceinline__ uint4 unpack_agent(const jl_mapfgpt_t& b, int i,
 template <int H, bool kMarked>
 __device__ __forceinline__ uint32_t kept_greedy(const jl_mapfgpt_t& b, size_t i, int px, int py) {
     const int W = b.map_w;
-    const uint16_t* f = b.cost_tiles + i * field_cells(W, H);
+    const uint16_t* f = b.cost_tiles + i * tiled_cells(W, H);
     if (kMarked) {
         const uint32_t c = f[tile_offset(px, py, W)];
         if (c != kUnreachable) return c >> 12;
@@ -226,9 +226,7 @@ __device__ void store_field_tiles(const jl_mapfgpt_t& b, size_t agent_index, con
                                   int first, int stride) {
     const int W = b.map_w;
     const uint4* lds4 = reinterpret_cast<const uint4*>(s_dist);
-    uint4* tout = reinterpret_cast<uint4*>(b.cost_tiles + agent_index * field_cells(W, H));
-    // marked fields: the second copy, 64 bytes off the first's lines
-    uint4* tout1 = reinterpret_cast<uint4*>(b.cost_tiles + agent_index * field_cells(W, H) + shifted_copy_cells(W, H));
+    uint4* tout = reinterpret_cast<uint4*>(b.cost_tiles + agent_index * tiled_cells(W, H));
     const int map_tile_rows = (W + 7) / 8;
     for (int c = first; c < map_tile_rows * H; c += stride) {
         const int t = c >> 3, r = c & 7;  // map tile, row inside the tile
@@ -242,7 +240,6 @@ __device__ void store_field_tiles(const jl_mapfgpt_t& b, size_t agent_index, con
         v.z = in ? v.z : 0xFFFFFFFFu;
         v.w = in ? v.w : 0xFFFFFFFFu;
         tout[dst] = v;
-        if constexpr (kMarked) tout1[dst] = v;
     }
 }
 
@@ -307,7 +304,7 @@ __device__ uint32_t refresh_field_group(const jl_mapfgpt_t& b, size_t agent_inde
     const int tid = threadIdx.x;
     const int x = tid;  // this lane's map row
     const int words = W * H / 32;
-    const size_t tcells = field_cells(W, H);  // a field's stride
+    const size_t tcells = tiled_cells(W, H);
     bool ok = e < (uint32_t)b.n_envs && (uint32_t)gx < (uint32_t)W && (uint32_t)gy < (uint32_t)H;
     const uint32_t* env_bits = b.grid_bits + (size_t)(ok ? e : 0) * words;
     if (ok && bit_at(env_bits, gx * H + gy)) ok = false;
@@ -861,12 +858,10 @@ __global__ __launch_bounds__(kTokThreads) void tokens_kernel(jl_mapfgpt_t b) {
     // load is issued without a branch and touches only the window's lines.
     // Offsets are 32-bit bytes from the env's first tiled field (the host
     // checks that they fit).
-    const size_t tcells = field_cells(W, H);  // a field's stride
+    const size_t tcells = tiled_cells(W, H);
     const uint8_t* env_tiles =
         reinterpret_cast<const uint8_t*>(b.cost_tiles + (size_t)env * A * tcells);
     const uint32_t strip_bytes = strip_cells(W) * 2u;
-    const bool marked = marked_fields(W, H);
-    const uint32_t shifted_bytes = (uint32_t)shifted_copy_cells(W, H) * 2u;
     const int g_seg = lane < kSegPerEgo ? lane : lane - kSegPerEgo;
     const int g_i = g_seg / 3, g_j = g_seg - (g_seg / 3) * 3;
     auto seg_load = [&](uint32_t pos, int e, uint32_t& fill) -> uint4 {
@@ -877,10 +872,7 @@ __global__ __launch_bounds__(kTokThreads) void tokens_kernel(jl_mapfgpt_t b) {
         const int x = ex - kRadius + g_i;  // in [-5, W + 4]: the border covers it
         const int tcol = tyl + 1 + ((g_j == 2 && !third) ? 1 : g_j);
         fill = 0u;
-        // marked maps: the copy whose lines hold the window's rows in two
-        const uint32_t copy = marked && window_in_shifted_copy(ex - kRadius) ? shifted_bytes : 0u;
-        const uint32_t off =
-            (uint32_t)e * (uint32_t)tcells * 2u + copy + (uint32_t)tcol * strip_bytes + (uint32_t)(x + 8) * 16u;
+        const uint32_t off = (uint32_t)e * (uint32_t)tcells * 2u + (uint32_t)tcol * strip_bytes + (uint32_t)(x + 8) * 16u;
         return *reinterpret_cast<const uint4*>(env_tiles + off);
     };
 
@@ -1154,7 +1146,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(H <= 1
     const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
     const BuildLayout L = build_layout(A, W, H, kWaves);
     const size_t cells = (size_t)W * H;
-    const size_t tcells = field_cells(W, H);  // a field's stride
+    const size_t tcells = tiled_cells(W, H);
     const uint32_t fmask = field_mask(W, H);
     uint16_t* s_map = reinterpret_cast<uint16_t*>(smem + L.map_off);
     int* s_tmpl = reinterpret_cast<int*>(smem + L.tmpl_off);
@@ -1210,14 +1202,10 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(H <= 1
     lds_barrier();  // s_nlist and s_diag cleared
     const uint32_t strip_bytes = strip_cells(W) * 2u;
     const uint32_t field_bytes = (uint32_t)tcells * 2u;
-    const uint32_t shifted_bytes = (uint32_t)shifted_copy_cells(W, H) * 2u;  // marked maps only
     if (mine) {
         const uint32_t ex = valid ? px : 0u, ey = valid ? py : 0u;  // windows of agents off the map: cell 0
         const uint32_t y8 = ey + (8 - kRadius);                        // bordered first column
-        // the copy whose lines hold the window's 11 strip rows in two
-        const uint32_t copy = window_in_shifted_copy((int)ex - kRadius) ? shifted_bytes : 0u;
-        const uint32_t seg =
-            (uint32_t)tid * field_bytes + copy + (y8 >> 3) * strip_bytes + (ex + (8 - kRadius)) * 16u;
+        const uint32_t seg = (uint32_t)tid * field_bytes + (y8 >> 3) * strip_bytes + (ex + (8 - kRadius)) * 16u;
         uint4 rec;
         rec.x = valid ? st.y : kNoAgent;
         rec.y = st.z;
@@ -1620,7 +1608,7 @@ __global__ __launch_bounds__(256) void cost_to_go_kernel(jl_mapfgpt_t b) {
     const size_t per_field = (size_t)W * (H / 8);  // 16-byte words of a row-major field
     const size_t total = fields * per_field;
     const uint32_t strip_words = strip_cells(W) / 8u;  // 16-byte rows of a strip
-    const size_t tcells = field_cells(W, H);  // a field's stride
+    const size_t tcells = tiled_cells(W, H);
     const v4i* tiles = reinterpret_cast<const v4i*>(b.cost_tiles);
     v4i* out = reinterpret_cast<v4i*>(b.cost_to_go);
     for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (size_t)gridDim.x * blockDim.x) {
@@ -1663,7 +1651,7 @@ int check_builder(const jl_mapfgpt_t* b) {
     if ((int64_t)b->n_envs * b->n_agents > 0x7FFFFFFF) return JL_ERR_ARG;
     if (b->n_agents > 65535 || b->n_envs > 65535) return JL_ERR_ARG;
     // the token pass addresses an env's tiled fields with 32-bit byte offsets
-    if ((uint64_t)b->n_agents * field_cells(b->map_w, b->map_h) * 2u > 0xFFFFFFFFull)
+    if ((uint64_t)b->n_agents * tiled_cells(b->map_w, b->map_h) * 2u > 0xFFFFFFFFull)
         return JL_ERR_ARG;
     if (!b->grid_bits || !b->state_packed || !b->histories || !b->labels || !b->goal_cache || !b->tokens ||
         !b->active_mask || !b->diagnostics || !b->agent_info || !b->cost_tiles)

@@ -22,7 +22,7 @@ import types
 
 import torch
 
-from ._abi import BUILD_SCRATCH_WORDS, GAVE_UP_WORD, MagatDesc, MapfGPTDesc, SimDesc, check, field_cells, load_library
+from ._abi import BUILD_SCRATCH_WORDS, GAVE_UP_WORD, MagatDesc, MapfGPTDesc, SimDesc, check, load_library, tiled_field_cells
 
 TASK_LIFELONG = 0
 TASK_STANDARD_MAPF = 1
@@ -45,7 +45,14 @@ def _ptr(t: torch.Tensor | None) -> int | None:
     return None if t is None else t.data_ptr()
 
 
+_RAW_STREAM = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def _stream(device: torch.device) -> int:
+    """The current stream of `device` as a raw handle (without building a
+    torch Stream object, a few microseconds per call on the step path)."""
+    if _RAW_STREAM is not None and device.index is not None:
+        return _RAW_STREAM(device.index)
     return torch.cuda.current_stream(device).cuda_stream
 
 
@@ -275,7 +282,7 @@ class MapfGPTObservationBuilder(_Base):
             # cells (the token pass reads its windows there); -1 is unreachable
             self._agent_info = torch.zeros((N,), dtype=torch.int32, device=device)
             self._cost_tiles = torch.full(
-                (E, n_agents, field_cells(W, H)), -1, dtype=torch.int16, device=device
+                (E, n_agents, tiled_field_cells(W, H)), -1, dtype=torch.int16, device=device
             )
             # single-launch builds: number of the last launch whose diagnostics
             # were cleared (uint64) and workgroup arrival counters; zero at
@@ -306,12 +313,17 @@ class MapfGPTObservationBuilder(_Base):
         # stream of the last build: single-launch builds number themselves on
         # the device and must run one after another
         self._build_stream = None
+        self._build_raw = None  # raw handle of _build_stream
+        self._state_shape = torch.Size((self.n_envs, self.n_agents))
 
     def _order_builds(self) -> None:
         """Orders this build after the previous one when they are issued from
         different streams (single-launch builds derive their launch number
         from arrival counters that assume builds do not overlap).  Builds
         captured into a graph are ordered by the capture itself."""
+        raw = _stream(self._device)
+        if raw == self._build_raw:
+            return  # the stream of the previous build: ordered already
         if torch.cuda.is_current_stream_capturing():
             return
         cur = torch.cuda.current_stream(self._device)
@@ -319,6 +331,7 @@ class MapfGPTObservationBuilder(_Base):
         if last is not None and last != cur:
             cur.wait_stream(last)
         self._build_stream = cur
+        self._build_raw = raw
 
     def build_tokens(self, raw_rows: torch.Tensor) -> None:
         """mapf_gpt_builder.cpp:89-114."""
@@ -366,6 +379,9 @@ class MapfGPTObservationBuilder(_Base):
             self._build_scratch[GAVE_UP_WORD].zero_()
 
     def _check_state(self, t: torch.Tensor, name: str) -> None:
+        if (t.dtype is torch.int16 and t.shape == self._state_shape and t.device == self._device
+                and t.is_contiguous()):
+            return  # valid: the checks below name the first failing condition otherwise
         _require(t.is_cuda, f"{name} must be on a CUDA device")
         _require(t.dtype == torch.int16, f"{name} must use int16 dtype")
         _require(
@@ -407,6 +423,15 @@ class MapfGPTObservationBuilder(_Base):
 
     def append_actions(self, actions: torch.Tensor) -> None:
         """mapf_gpt_builder.cpp:170-192."""
+        if not (actions.dtype is torch.uint8 and actions.shape == self._state_shape
+                and actions.device == self._device and actions.is_contiguous()):
+            self._check_actions(actions)
+        check(
+            self._lib.jl_mapfgpt_append_actions(self._desc_ref, actions.data_ptr(), _stream(self._device)),
+            "MAPF-GPT action-history update",
+        )
+
+    def _check_actions(self, actions: torch.Tensor) -> None:
         _require(actions.is_cuda, "actions must be on a CUDA device")
         _require(actions.dtype == torch.uint8, "actions must use uint8 dtype")
         _require(
@@ -415,10 +440,6 @@ class MapfGPTObservationBuilder(_Base):
         )
         _require(actions.is_contiguous(), "actions must be contiguous")
         _require(actions.device == self._device, "actions must use the builder CUDA device")
-        check(
-            self._lib.jl_mapfgpt_append_actions(self._desc_ref, actions.data_ptr(), _stream(self._device)),
-            "MAPF-GPT action-history update",
-        )
 
     def reset_histories(self) -> None:
         check(
@@ -658,14 +679,16 @@ class GridWorldSimulator(_Base, _PygModeMixin, _PygStorage):
 
     def update_actions(self, new_actions: torch.Tensor) -> None:
         """grid_world_simulator.cpp:678-688."""
-        _require(new_actions.dtype == torch.uint8, "new_actions must be uint8")
-        _require(new_actions.is_cuda, "new_actions must be CUDA")
-        _require(new_actions.shape == self.t_actions.shape, "new_actions shape mismatch")
-        _require(new_actions.is_contiguous(), "new_actions must be contiguous")
-        _require(
-            new_actions.device == self._device,
-            "new_actions and simulator tensors must use the same CUDA device",
-        )
+        if not (new_actions.dtype is torch.uint8 and new_actions.shape == self.t_actions.shape
+                and new_actions.device == self._device and new_actions.is_contiguous()):
+            _require(new_actions.dtype == torch.uint8, "new_actions must be uint8")
+            _require(new_actions.is_cuda, "new_actions must be CUDA")
+            _require(new_actions.shape == self.t_actions.shape, "new_actions shape mismatch")
+            _require(new_actions.is_contiguous(), "new_actions must be contiguous")
+            _require(
+                new_actions.device == self._device,
+                "new_actions and simulator tensors must use the same CUDA device",
+            )
         check(
             self._lib.jl_update_actions(self._sim_ref, _ptr(new_actions), _stream(self._device)),
             "update_actions",

@@ -177,15 +177,11 @@ typedef struct jl_mapfgpt {
     int32_t* diagnostics;       /* [4] overflow, bad row/action, duplicate cell, bad goal/position */
     uint32_t* agent_info;       /* [N] workspace: greedy-move mask and diagnostic flags of
                                    each agent, written by the first pass of a build */
-    uint16_t* cost_tiles;       /* [E, A, F] workspace, 0xFFFF at allocation, 128-byte
-                                   aligned for full speed: the same fields as cost_to_go in
-                                   8x8 tiles (one 128-byte line per tile) inside a one-tile
-                                   border of unreachable cells that no kernel writes,
-                                   T = (ceil(W/8) + 2) * (H/8 + 2) * 64 cells; F = T, or on
-                                   maps of at most 4096 cells F = 2 T + 64 with the field
-                                   stored twice (the second copy 64 bytes off the first's
-                                   lines, so that every window reads two lines per column
-                                   strip) and bits 12-15 of a reachable cell holding its
+    uint16_t* cost_tiles;       /* [E, A, ceil(W/8) + 2, H/8 + 2, 8, 8] workspace, 0xFFFF at
+                                   allocation: the same fields as cost_to_go in 8x8 tiles
+                                   (one 128-byte line per tile) inside a one-tile border of
+                                   unreachable cells that no kernel writes; on maps of at
+                                   most 4096 cells bits 12-15 of a reachable cell hold its
                                    greedy-move mask */
     int32_t* build_scratch;     /* [JL_BUILD_SCRATCH_WORDS] workspace, zero at construction,
                                    128-byte aligned, used with this builder's n_envs only:
