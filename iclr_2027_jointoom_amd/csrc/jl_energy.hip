@@ -6,7 +6,9 @@
 // distances in LDS and storing 255-d with 16-byte coalesced writes.  The
 // reference launches one 128-thread block per row whether or not its row
 // needs a refresh (energy_map.cu:262-271) and finds the changed rows with a
-// host-synchronised cumsum (grid_world_simulator.cpp:707-753).
+// host-synchronised cumsum (grid_world_simulator.cpp:707-753); here the
+// incremental derived state is one launch on small maps (the scan, the
+// packed rows and the fields of changed goals: goal_changed_refresh_kernel).
 #include "jl_bfs.h"
 #include "jl_common.h"
 

@@ -1,20 +1,24 @@
 // jl_magat.hip - MAGAT node features and neighbour graph for gfx950.
 //
 // nodes: one workgroup per (env, 64-agent slice).  The env's static and
-// occupancy bitmaps, agent positions and goals are staged in LDS; one
-// wavefront writes each agent's 676-float row, lane l owning patch cells
-// l, l + 64, l + 128: it loads its own energy byte and stores the four
-// channels of its cells as coalesced dwords (the reference zero-fills the row
-// and rewrites it one float per thread, 128_agents_map_stateless_step.cu:
-// 414-421, 438-478).  The clamped ctg value is one of 21 float constants k/10
-// (the IEEE quotients), so no division is evaluated on the device.
-// edges: per-env edge totals (from the node pass) -> one-workgroup scan ->
-// per (env, 64-source slice) writer: lane l of each wavefront tests source l
-// of the slice against 64 ids per step (packed int16 differences, one dot2
-// per pair) into per-source neighbour bitmasks in LDS; then every thread
-// stores one edge per output position, sorted by (source, destination id)
-// (grid_world_cuda.cu:17-110, stateless_step.cu:854-935).  Envs of more
-// than 1024 agents take a ballot writer with an LDS ring.
+// occupancy bitmaps and its agents' positions and goals are staged in LDS,
+// the slice's 11 x 11 energy windows are requested (non-temporal 16-byte
+// loads) and, while they are in flight, the slice's neighbour counts are
+// taken and its edge total written; then one wavefront per agent assembles
+// the 676-float row in LDS (lane l owning patch cells l, l + 64, l + 128)
+// and stores it as 16-byte words in address order (the reference zero-fills
+// the row and rewrites it one float per thread, 128_agents_map_stateless_
+// step.cu:414-421, 438-478).  The clamped ctg value is one of 21 float
+// constants k/10 (the IEEE quotients), so no division is evaluated on the
+// device.
+// edges: one workgroup per (env, 64-source slice) sums the node pass's slice
+// totals before its own (a one-workgroup env scan runs first only beyond
+// 8,192 slices); lane l of each wavefront tests source l of the slice
+// against 64 ids per step (packed int16 differences, one dot2 per pair) into
+// per-source neighbour bitmasks in LDS; then every thread stores one edge per
+// output position, sorted by (source, destination id) (grid_world_cuda.cu:
+// 17-110, stateless_step.cu:854-935).  Envs of more than 1024 agents take a
+// ballot writer with an LDS ring.
 #include "jl_common.h"
 
 namespace jl {
