@@ -133,6 +133,19 @@ def test_rejects_invalid_layouts():
         b2.append_actions(valid)
     with pytest.raises(RuntimeError, match="shape"):
         b2.append_actions(torch.zeros((1, 1), dtype=torch.uint8, device="cuda"))
+    # the wrappers' one-test fast path falls back to the detailed messages
+    wide = torch.tensor([[10, 0, 11, 0]], dtype=torch.int16, device="cuda")
+    with pytest.raises(RuntimeError, match="cur_y must be contiguous"):
+        b2.build_tokens_from_state(valid, wide[:, ::2], valid, valid)
+    with pytest.raises(RuntimeError, match="goal_x must be on a CUDA device"):
+        b2.build_tokens_from_state(valid, valid, valid.cpu(), valid)
+    acts = torch.zeros((1, 4), dtype=torch.uint8, device="cuda")
+    with pytest.raises(RuntimeError, match="actions must be contiguous"):
+        b2.append_actions(acts[:, ::2])
+    with pytest.raises(RuntimeError, match="actions must be on a CUDA device"):
+        b2.append_actions(acts[:, :2].cpu())
+    b2.build_tokens_from_state(valid, valid, valid, valid)  # valid tensors still pass
+    b2.append_actions(acts[:, :2].contiguous())
 
 
 def test_invalid_position_is_diagnosed():

@@ -209,6 +209,22 @@ def test_load_state_validates(positions, goals, arrived, step_counts, message):
         _load(sim, positions, goals, arrived=arrived, step_counts=step_counts)
 
 
+@pytest.mark.parametrize(("make", "message"), [
+    (lambda a: a.to(torch.int16), "new_actions must be uint8"),
+    (lambda a: a.cpu(), "new_actions must be CUDA"),
+    (lambda a: a[:, :1].contiguous(), "new_actions shape mismatch"),
+    (lambda a: torch.zeros((2, 4), dtype=torch.uint8, device="cuda")[:, ::2], "new_actions must be contiguous"),
+])
+def test_update_actions_validates(make, message):
+    """update_actions keeps the reference's checks and messages
+    (grid_world_simulator.cpp:678-688) behind its one-test fast path."""
+    sim = _sim(ext_for(128, 128), num_envs=2, num_agents=2, task_mode="standard_mapf")
+    good = torch.zeros((2, 2), dtype=torch.uint8, device="cuda")
+    with pytest.raises(RuntimeError, match=message):
+        sim.update_actions(make(good))
+    sim.update_actions(good)
+
+
 @pytest.mark.parametrize("field", [0, 1, 2, 3])
 @pytest.mark.parametrize(("violation", "message"), [
     ("cpu", "must be CUDA"), ("dtype", "must be (int16|uint8|int32)"),
