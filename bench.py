@@ -373,11 +373,11 @@ def run_gpu(args) -> dict:
     graph = None
 
     def prepare_timed_region():
-        # The diagnostics check and the event objects of the timed region.
-        # Done before the last warmup step, so that the timed region follows
-        # that step after one synchronize and not after an idle GPU: the
-        # first build after an idle gap of a few hundred microseconds runs
-        # 5-9 us slower than the builds that follow it.
+        # The diagnostics check and the event objects of the timed region,
+        # done before the last warmup step: the timed region opens right
+        # after that step's synchronize, and no event is created inside it
+        # (torch creates one at its first record, a host call that delayed
+        # the first timed build by about 14 us).
         torch.cuda.synchronize()
         diag = builder.diagnostics.cpu().tolist()
         if any(diag):
