@@ -35,7 +35,6 @@
 namespace jl {
 namespace {
 
-constexpr uint32_t kEmptyKey = 0xFFFFFFFFu;
 constexpr uint32_t kNoAgent = 0xFFFFFFFFu;
 
 // agent_info word, written for every agent by pass 1, read by pass 2.
@@ -43,30 +42,6 @@ constexpr uint32_t kInfoGreedy = 0xFu;        // greedy-move mask
 constexpr uint32_t kInfoBadRow = 1u << 4;     // raw row rejected (diagnostics[1])
 constexpr uint32_t kInfoBadGoal = 1u << 5;    // refresh with goal off map / on obstacle ([3])
 constexpr int kInfoOverflowShift = 8;         // BFS frontier overflow count ([0]), 24 bits
-
-__device__ __forceinline__ uint32_t hash_cell(uint32_t cell, uint32_t mask) {
-    return (cell * 2654435761u >> 7) & mask;
-}
-
-// Insert `cell` (once per distinct cell) and return its slot.
-__device__ __forceinline__ uint32_t hash_insert(uint32_t* keys, uint32_t mask, uint32_t cell) {
-    uint32_t h = hash_cell(cell, mask);
-    while (true) {
-        const uint32_t old = atomicCAS(&keys[h], kEmptyKey, cell);
-        if (old == kEmptyKey || old == cell) return h;
-        h = (h + 1) & mask;
-    }
-}
-
-__device__ __forceinline__ uint32_t hash_find(const uint32_t* keys, uint32_t mask, uint32_t cell) {
-    uint32_t h = hash_cell(cell, mask);
-    while (true) {
-        const uint32_t k = keys[h];
-        if (k == cell) return h;
-        if (k == kEmptyKey) return kEmptyKey;
-        h = (h + 1) & mask;
-    }
-}
 
 // Greedy-move mask of one agent (mapf_gpt_cuda.cu:459-480): bit (3 - dir)
 // is set when the neighbour in direction dir, order (-1,0), (+1,0), (0,-1),
@@ -534,12 +509,14 @@ __global__ __launch_bounds__(kWave* kWaves) void unpack_bfs_kernel(
 //
 // Phase 1 (whole workgroup, one env): each agent's record (position word,
 // kNoAgent off the map, and goal word), its six ego-independent tokens (five
-// history tokens and the greedy token, :437-456; on hash maps their 16-bit raw
-// values, turned into tokens where a row copies them, to keep the LDS of 1024
-// agents under 80 KB) and a cell -> agent map live in LDS.
+// history tokens and the greedy token, :437-456; on sparse maps their 16-bit
+// raw values, turned into tokens where a row copies them, to keep the LDS of
+// 1024 agents under 80 KB) and a cell -> agent map live in LDS.
 // The map is dense (one int32 per cell of the map grown by a kRadius border
-// of empty cells, so a window probe needs no bounds test) while it fits, an
-// occupancy bitmap + hash beyond.
+// of empty cells, so a window probe needs no bounds test) while it fits;
+// beyond, it is sparse: an occupancy bitmap, the count of occupied cells
+// before each of its words, and the ids of the occupied cells in cell order,
+// so a probe is a bit test and, on an occupied cell, one rank and one read.
 // Phase 2 (each wavefront on its own, no workgroup barrier): a wavefront
 // produces its egos two at a time.  Lanes 0..32 load the 33 tile-row
 // segments of both egos' 11x11 windows (cells outside the map staged as
@@ -575,7 +552,7 @@ constexpr int kSlotStride = 16;            // per-wave top-13 slot array (words)
 constexpr int kRecWords = 2;               // per-agent record: position word, goal word
 constexpr int kCopyTokens = 6;             // per-agent tokens independent of the ego: int32
                                            // tokens on dense maps, uint16 raw values (5 history
-                                           // values, greedy mask) on hash maps, where LDS is short
+                                           // values, greedy mask) on sparse maps, where LDS is short
 constexpr int kCoordLanes = kVisible * 4;  // lanes producing the 52 coordinate tokens
 constexpr int kCopyItems = kVisible * kCopyTokens;  // 78 copied tokens per row
 // per-wavefront LDS: two egos' windows, the token row, the slot array
@@ -590,8 +567,8 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 
 struct TokLayout {
     bool dense;
-    int hash_slots;
-    size_t map_off, occ_off, keys_off, vals_off, rec_off, copy_off, wave_off, diag_off, total;
+    int occ_words;  // occupancy words of a sparse map (0 on dense maps)
+    size_t map_off, occ_off, pref_off, ids_off, rec_off, copy_off, wave_off, diag_off, total;
 };
 
 __host__ __device__ inline size_t align16(size_t v) { return (v + 15) & ~(size_t)15; }
@@ -600,18 +577,16 @@ __host__ __device__ inline TokLayout tok_layout(int A, int W, int H) {
     TokLayout L;
     const size_t cells = (size_t)W * H;
     L.dense = cells <= (size_t)kDenseCellLimit;
-    int s = 64;
-    while (s < 2 * A) s <<= 1;
-    L.hash_slots = L.dense ? 0 : s;
+    L.occ_words = L.dense ? 0 : (int)(cells / 32);
     size_t off = 0;
     L.map_off = off;
     if (L.dense) off = align16(off + (size_t)(W + 2 * kRadius) * (H + 2 * kRadius) * 4);
     L.occ_off = off;
-    if (!L.dense) off = align16(off + cells / 8);
-    L.keys_off = off;
-    off = align16(off + (size_t)L.hash_slots * 4);
-    L.vals_off = off;
-    off = align16(off + (size_t)L.hash_slots * 4);
+    off = align16(off + (size_t)L.occ_words * 4);
+    L.pref_off = off;  // uint16 per occupancy word: occupied cells before the word
+    off = align16(off + (size_t)L.occ_words * 2);
+    L.ids_off = off;   // per occupied cell in cell order: the lowest id on it
+    if (!L.dense) off = align16(off + (size_t)A * 4);
     L.rec_off = off;
     off = align16(off + (size_t)A * kRecWords * 4);
     L.copy_off = off;
@@ -721,8 +696,8 @@ __global__ __launch_bounds__(kTokThreads) void tokens_kernel(jl_mapfgpt_t b) {
     constexpr int MH = H + 2 * kRadius;  // dense map columns
     uint32_t* s_map = reinterpret_cast<uint32_t*>(smem + L.map_off);
     uint32_t* s_occ = reinterpret_cast<uint32_t*>(smem + L.occ_off);
-    uint32_t* s_keys = reinterpret_cast<uint32_t*>(smem + L.keys_off);
-    uint32_t* s_vals = reinterpret_cast<uint32_t*>(smem + L.vals_off);
+    uint16_t* s_pref = reinterpret_cast<uint16_t*>(smem + L.pref_off);
+    uint32_t* s_ids = reinterpret_cast<uint32_t*>(smem + L.ids_off);
     uint32_t* s_rec = reinterpret_cast<uint32_t*>(smem + L.rec_off);    // kRecWords per agent
     uint16_t* s_copy = reinterpret_cast<uint16_t*>(smem + L.copy_off);  // kCopyTokens per agent
     int* s_copy_tok = reinterpret_cast<int*>(smem + L.copy_off);          // the same, dense maps
@@ -731,7 +706,6 @@ __global__ __launch_bounds__(kTokThreads) void tokens_kernel(jl_mapfgpt_t b) {
     uint4* my_win = reinterpret_cast<uint4*>(my_lds);                  // [2 egos][11 rows][3 segments]
     int* my_row = reinterpret_cast<int*>(my_lds + kWinBytes);           // [kContext]
     uint32_t* my_slots = reinterpret_cast<uint32_t*>(my_lds + kWinBytes + kRowBytes);
-    const uint32_t hmask = (uint32_t)L.hash_slots - 1;
     const size_t cells = (size_t)W * H;
     const uint32_t fmask = field_mask(W, H);  // distance bits of a tiled field value
     // ---- phase 1 -----------------------------------------------------------
@@ -740,11 +714,8 @@ __global__ __launch_bounds__(kTokThreads) void tokens_kernel(jl_mapfgpt_t b) {
         uint2* m2 = reinterpret_cast<uint2*>(s_map);
         for (int k = tid; k < mcells / 2; k += kTokThreads) m2[k] = make_uint2(kNoAgent, kNoAgent);
     } else {
-        for (int k = tid; k < (int)(cells / 32); k += kTokThreads) s_occ[k] = 0;
-        for (int k = tid; k < L.hash_slots; k += kTokThreads) {
-            s_keys[k] = kEmptyKey;
-            s_vals[k] = kNoAgent;
-        }
+        for (int k = tid; k < L.occ_words; k += kTokThreads) s_occ[k] = 0;
+        for (int k = tid; k < A; k += kTokThreads) s_ids[k] = kNoAgent;
     }
     // slot arrays only ever hold agent ids (stale entries stay readable);
     // row tokens past the agent section are always padding
@@ -783,17 +754,13 @@ __global__ __launch_bounds__(kTokThreads) void tokens_kernel(jl_mapfgpt_t b) {
         d_row += (info & kInfoBadRow) ? 1 : 0;
         d_bad += (info & kInfoBadGoal) ? 1 : 0;
         if (valid) {
-            uint32_t prev;
             if (kDense) {
-                prev = atomicMin(&s_map[(px + kRadius) * MH + py + kRadius], (uint32_t)a);
+                // lowest id keeps a shared cell; each extra agent counts once
+                if (atomicMin(&s_map[(px + kRadius) * MH + py + kRadius], (uint32_t)a) != kNoAgent) ++d_dup;
             } else {
                 const uint32_t cell = px * H + py;
                 atomicOr(&s_occ[cell >> 5], 1u << (cell & 31));
-                const uint32_t slot = hash_insert(s_keys, hmask, cell);
-                prev = atomicMin(&s_vals[slot], (uint32_t)a);
             }
-            // lowest id keeps a shared cell; each extra agent counts once
-            if (prev != kNoAgent) ++d_dup;
         } else {
             ++d_bad;  // position off the map (scatter, :336-339)
         }
@@ -802,6 +769,43 @@ __global__ __launch_bounds__(kTokThreads) void tokens_kernel(jl_mapfgpt_t b) {
             cpt[5] = copy_token(greedy, 5);
         } else {
             cp[5] = (uint16_t)greedy;
+        }
+    }
+    if (!kDense) {
+        // Sparse map: the occupied cells are ranked in cell order (the count
+        // of occupied cells before each occupancy word, at most 65,536 - 32,
+        // plus the set bits below the cell's own) and the lowest id on each
+        // occupied cell is kept at its rank.  The wave sums of the scan use
+        // wavefront 0's window area, which phase 2 fills later.
+        uint32_t* s_wsum = reinterpret_cast<uint32_t*>(smem + L.wave_off);
+        lds_barrier();
+        const int per = (L.occ_words + kTokThreads - 1) / kTokThreads;
+        const int w0 = tid * per;
+        const int w1 = (w0 + per) < L.occ_words ? (w0 + per) : L.occ_words;
+        uint32_t sum = 0;
+        for (int w = w0; w < w1; ++w) sum += __popc(s_occ[w]);
+        uint32_t incl = sum;
+        for (int off = 1; off < kWave; off <<= 1) {
+            const uint32_t t = __shfl_up(incl, off, kWave);
+            if (lane >= off) incl += t;
+        }
+        if (lane == kWave - 1) s_wsum[wave] = incl;
+        lds_barrier();
+        uint32_t run = incl - sum;
+        for (int k = 0; k < wave; ++k) run += s_wsum[k];
+        for (int w = w0; w < w1; ++w) {
+            s_pref[w] = (uint16_t)run;
+            run += __popc(s_occ[w]);
+        }
+        lds_barrier();
+        for (int a = tid; a < A; a += kTokThreads) {
+            const uint32_t pos = s_rec[a * kRecWords];
+            if (pos == kNoAgent) continue;
+            const uint32_t cell = (pos & 0xFFFFu) * (uint32_t)H + (pos >> 16);
+            const uint32_t bit = 1u << (cell & 31);
+            const uint32_t rank = s_pref[cell >> 5] + __popc(s_occ[cell >> 5] & (bit - 1u));
+            // lowest id keeps a shared cell; each extra agent counts once
+            if (atomicMin(&s_ids[rank], (uint32_t)a) != kNoAgent) ++d_dup;
         }
     }
     if (part != 0) d_over = d_row = d_dup = d_bad = 0;  // the env's counts come from its first slice
@@ -840,13 +844,15 @@ __global__ __launch_bounds__(kTokThreads) void tokens_kernel(jl_mapfgpt_t b) {
     const int k_pos1 = kCostTokens + k_slot1 * kAgentTokens + 4 + k_tok1;
     const uint16_t* s_rec16 = reinterpret_cast<const uint16_t*>(s_rec);
 
-    // Agent at (x, y) of this env or kNoAgent (hash map).
-    auto agent_at_hash = [&](int x, int y) -> uint32_t {
+    // Agent at (x, y) of this env or kNoAgent (sparse map): the id at the
+    // occupied cell's rank.
+    auto agent_at_rank = [&](int x, int y) -> uint32_t {
         const bool in = x >= 0 && x < W && y >= 0 && y < H;
         if (!in) return kNoAgent;
         const uint32_t cell = (uint32_t)(x * H + y);
-        if (!((s_occ[cell >> 5] >> (cell & 31)) & 1u)) return kNoAgent;
-        return s_vals[hash_find(s_keys, hmask, cell)];
+        const uint32_t w = s_occ[cell >> 5], bit = 1u << (cell & 31);
+        if (!(w & bit)) return kNoAgent;
+        return s_ids[s_pref[cell >> 5] + __popc(w & (bit - 1u))];
     };
 
     // Window gather.  Lane l < 33 loads segment l = (row i, tile column j) of
@@ -892,8 +898,8 @@ __global__ __launch_bounds__(kTokThreads) void tokens_kernel(jl_mapfgpt_t b) {
                 id0 = mrow[map0];
                 id1 = mrow[map1];
             } else {
-                id0 = agent_at_hash(ex + di0 - kRadius, ey + dj0 - kRadius);
-                id1 = agent_at_hash(ex + di1 - kRadius, ey + dj1 - kRadius);
+                id0 = agent_at_rank(ex + di0 - kRadius, ey + dj0 - kRadius);
+                id1 = agent_at_rank(ex + di1 - kRadius, ey + dj1 - kRadius);
             }
             // candidates: (distance << 16 | id); an empty cell's key is all ones
             const uint32_t key0 = qd0 | id0, key1 = qd1 | id1;

@@ -399,12 +399,49 @@ def test_more_than_13_visible_agents_match_oracle(oracle):
     assert full > 0.5
 
 
-def test_hash_cell_map_on_256_maps_matches_oracle(oracle):
-    """256x256 maps use the LDS occupancy bitmap + hash instead of the dense map."""
+def test_sparse_cell_map_on_256_maps_matches_oracle(oracle):
+    """256x256 maps use the sparse cell -> agent map instead of the dense one."""
     from iclr_2027_jointoom_amd.synthetic import make_batch
 
     grids, starts, goals = make_batch(11, 2, 256, 256, 192)
     _state_parity(oracle, grids, starts, goals, 192)
+
+
+@pytest.mark.parametrize("W,H,A", [(256, 256, 300), (100, 256, 1024), (256, 128, 520)])
+def test_sparse_cell_map_with_shared_cells_matches_oracle(oracle, W, H, A):
+    """Maps of more than 16,384 cells take the sparse cell -> agent map
+    (occupancy bitmap, occupied cells before each word, ids in cell order):
+    shared cells (two agents, four agents, ids in either order), rejected
+    rows and positions off the map give the oracle's tokens and diagnostics,
+    with fewer occupancy words than threads (100 x 256) and an env spread
+    over two workgroups (520 agents)."""
+    from iclr_2027_jointoom_amd import profile
+
+    rng = np.random.default_rng(W * 7 + H + A)
+    E = 2
+    grids = (rng.random((E, W, H)) < 0.25).astype(np.int32)
+    ext = profile(W, H)
+    b = ext.MapfGPTObservationBuilder(torch.from_numpy(grids).cuda(), A)
+    assert not b.single_launch
+    ob = oracle.OracleMapfGPT(grids, A)
+    rows = _rows_case(rng, grids, A)
+    goals = rows[:, 4:6].copy()
+    for it in range(3):
+        rows = _rows_case(rng, grids, A, goals)
+        rows[:, 7] = 1 if it == 0 else 0
+        rows[7, 2:4] = rows[8, 2:4]                  # two agents on one cell
+        rows[A + 20:A + 23, 2:4] = rows[A + 30, 2:4]  # four agents on one cell, the lowest id not first
+        rows[A - 1, 2:4] = rows[0, 2:4]              # the highest id on the lowest one's cell
+        if it >= 1:
+            rows[5, 0] = E + 1                       # rejected row (env out of range)
+            rows[A + 2, 2] = W + 3                   # position off the map
+        t = torch.from_numpy(rows.astype(np.int16)).cuda()
+        b.build_tokens(t)
+        ob.build_rows(rows)
+        torch.cuda.synchronize()
+        assert np.array_equal(b.tokens.cpu().numpy(), ob.tokens), it
+        assert b.diagnostics.cpu().tolist() == ob.diagnostics.tolist(), it
+        assert ob.diagnostics[2] >= 5, it  # the shared cells were counted
 
 
 def test_raw_row_history_values_outside_action_range(oracle):
@@ -622,7 +659,7 @@ def test_c2_full_size_build(oracle):
 
 
 def test_c5_full_size_build(oracle):
-    """BASELINE C5 shape (256 envs x 1024 agents, 256x256 warehouses; hash
+    """BASELINE C5 shape (256 envs x 1024 agents, 256x256 warehouses; sparse
     cell -> agent map, two 512-ego workgroups per env) through two resident
     steps: two sampled envs equal the oracle, and every ego's own slot and
     window centre hold their closed-form tokens."""
