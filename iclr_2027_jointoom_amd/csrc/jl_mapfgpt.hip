@@ -514,9 +514,10 @@ __global__ __launch_bounds__(kWave* kWaves) void unpack_bfs_kernel(
 // 1024 agents under 80 KB) and a cell -> agent map live in LDS.
 // The map is dense (one int32 per cell of the map grown by a kRadius border
 // of empty cells, so a window probe needs no bounds test) while it fits;
-// beyond, it is sparse: an occupancy bitmap, the count of occupied cells
-// before each of its words, and the ids of the occupied cells in cell order,
-// so a probe is a bit test and, on an occupied cell, one rank and one read.
+// beyond, it is sparse: an occupancy bitmap of the same bordered map, the
+// count of occupied cells before each of its words, and the ids of the
+// occupied cells in cell order, so a probe is a bit test and, on an occupied
+// cell, one rank and one read.
 // Phase 2 (each wavefront on its own, no workgroup barrier): a wavefront
 // produces its egos two at a time.  Lanes 0..32 load the 33 tile-row
 // segments of both egos' 11x11 windows (cells outside the map staged as
@@ -567,7 +568,7 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 
 struct TokLayout {
     bool dense;
-    int occ_words;  // occupancy words of a sparse map (0 on dense maps)
+    int occ_words;  // occupancy words of a sparse map with its kRadius border (0 on dense maps)
     size_t map_off, occ_off, pref_off, ids_off, rec_off, copy_off, wave_off, diag_off, total;
 };
 
@@ -577,13 +578,13 @@ __host__ __device__ inline TokLayout tok_layout(int A, int W, int H) {
     TokLayout L;
     const size_t cells = (size_t)W * H;
     L.dense = cells <= (size_t)kDenseCellLimit;
-    L.occ_words = L.dense ? 0 : (int)(cells / 32);
+    L.occ_words = L.dense ? 0 : (int)(((size_t)(W + 2 * kRadius) * (H + 2 * kRadius) + 31) / 32);
     size_t off = 0;
     L.map_off = off;
     if (L.dense) off = align16(off + (size_t)(W + 2 * kRadius) * (H + 2 * kRadius) * 4);
     L.occ_off = off;
     off = align16(off + (size_t)L.occ_words * 4);
-    L.pref_off = off;  // uint16 per occupancy word: occupied cells before the word
+    L.pref_off = off;  // uint16 per occupancy word: occupied cells before the word (< A <= 65535)
     off = align16(off + (size_t)L.occ_words * 2);
     L.ids_off = off;   // per occupied cell in cell order: the lowest id on it
     if (!L.dense) off = align16(off + (size_t)A * 4);
@@ -758,7 +759,7 @@ __global__ __launch_bounds__(kTokThreads) void tokens_kernel(jl_mapfgpt_t b) {
                 // lowest id keeps a shared cell; each extra agent counts once
                 if (atomicMin(&s_map[(px + kRadius) * MH + py + kRadius], (uint32_t)a) != kNoAgent) ++d_dup;
             } else {
-                const uint32_t cell = px * H + py;
+                const uint32_t cell = (px + kRadius) * MH + py + kRadius;
                 atomicOr(&s_occ[cell >> 5], 1u << (cell & 31));
             }
         } else {
@@ -772,10 +773,11 @@ __global__ __launch_bounds__(kTokThreads) void tokens_kernel(jl_mapfgpt_t b) {
         }
     }
     if (!kDense) {
-        // Sparse map: the occupied cells are ranked in cell order (the count
-        // of occupied cells before each occupancy word, at most 65,536 - 32,
-        // plus the set bits below the cell's own) and the lowest id on each
-        // occupied cell is kept at its rank.  The wave sums of the scan use
+        // Sparse map (the map grown by a kRadius border of empty cells, so a
+        // window probe needs no bounds test): the occupied cells are ranked
+        // in cell order (the count of occupied cells before each occupancy
+        // word plus the set bits below the cell's own) and the lowest id on
+        // each occupied cell is kept at its rank.  The wave sums of the scan use
         // wavefront 0's window area, which phase 2 fills later.
         uint32_t* s_wsum = reinterpret_cast<uint32_t*>(smem + L.wave_off);
         lds_barrier();
@@ -801,7 +803,7 @@ __global__ __launch_bounds__(kTokThreads) void tokens_kernel(jl_mapfgpt_t b) {
         for (int a = tid; a < A; a += kTokThreads) {
             const uint32_t pos = s_rec[a * kRecWords];
             if (pos == kNoAgent) continue;
-            const uint32_t cell = (pos & 0xFFFFu) * (uint32_t)H + (pos >> 16);
+            const uint32_t cell = ((pos & 0xFFFFu) + kRadius) * (uint32_t)MH + (pos >> 16) + kRadius;
             const uint32_t bit = 1u << (cell & 31);
             const uint32_t rank = s_pref[cell >> 5] + __popc(s_occ[cell >> 5] & (bit - 1u));
             // lowest id keeps a shared cell; each extra agent counts once
@@ -844,12 +846,9 @@ __global__ __launch_bounds__(kTokThreads) void tokens_kernel(jl_mapfgpt_t b) {
     const int k_pos1 = kCostTokens + k_slot1 * kAgentTokens + 4 + k_tok1;
     const uint16_t* s_rec16 = reinterpret_cast<const uint16_t*>(s_rec);
 
-    // Agent at (x, y) of this env or kNoAgent (sparse map): the id at the
-    // occupied cell's rank.
-    auto agent_at_rank = [&](int x, int y) -> uint32_t {
-        const bool in = x >= 0 && x < W && y >= 0 && y < H;
-        if (!in) return kNoAgent;
-        const uint32_t cell = (uint32_t)(x * H + y);
+    // Agent on bordered cell `cell` of this env or kNoAgent (sparse map):
+    // the id at the occupied cell's rank.
+    auto agent_at_rank = [&](uint32_t cell) -> uint32_t {
         const uint32_t w = s_occ[cell >> 5], bit = 1u << (cell & 31);
         if (!(w & bit)) return kNoAgent;
         return s_ids[s_pref[cell >> 5] + __popc(w & (bit - 1u))];
@@ -898,8 +897,9 @@ __global__ __launch_bounds__(kTokThreads) void tokens_kernel(jl_mapfgpt_t b) {
                 id0 = mrow[map0];
                 id1 = mrow[map1];
             } else {
-                id0 = agent_at_rank(ex + di0 - kRadius, ey + dj0 - kRadius);
-                id1 = agent_at_rank(ex + di1 - kRadius, ey + dj1 - kRadius);
+                const int mcell = (ex + kRadius) * MH + (ey + kRadius);
+                id0 = agent_at_rank((uint32_t)(mcell + map0));
+                id1 = agent_at_rank((uint32_t)(mcell + map1));
             }
             // candidates: (distance << 16 | id); an empty cell's key is all ones
             const uint32_t key0 = qd0 | id0, key1 = qd1 | id1;
