@@ -527,9 +527,11 @@ __global__ __launch_bounds__(kWave* kWaves) void unpack_bfs_kernel(
 // number of smaller keys, counted by walking the ballot of candidates with
 // uniform readlanes; ranks 0..12 are the reference's sorted top 13 because
 // keys are unique.  Every token of the row is computed by exactly one lane
-// (two cost tokens per lane, one coordinate token on lanes 0..51, the six
-// copied tokens of the 13 slots on lanes 0..63 and 0..13) into the
-// wavefront's LDS row, which is then stored as 64 x 16-byte writes.
+// (two cost tokens per lane; agent-section token t = slot * 10 + field on
+// lane t % 64) into the wavefront's LDS row, which keeps the previous ego's
+// agent section, so only the slots in use now or then are rewritten (one
+// pass of the lanes for up to six); the row is then stored as 64 x 16-byte
+// writes.
 // ---------------------------------------------------------------------------
 constexpr int kTokThreads = 1024;
 // Bound of a single-launch workgroup's wait for its launch's cleared totals
@@ -554,8 +556,6 @@ constexpr int kRecWords = 2;               // per-agent record: position word, g
 constexpr int kCopyTokens = 6;             // per-agent tokens independent of the ego: int32
                                            // tokens on dense maps, uint16 raw values (5 history
                                            // values, greedy mask) on sparse maps, where LDS is short
-constexpr int kCoordLanes = kVisible * 4;  // lanes producing the 52 coordinate tokens
-constexpr int kCopyItems = kVisible * kCopyTokens;  // 78 copied tokens per row
 // per-wavefront LDS: two egos' windows, the token row, the slot array
 constexpr int kWinBytes = 2 * kSegPerEgo * 16;
 constexpr int kRowBytes = kContext * 4;
@@ -563,7 +563,8 @@ constexpr int kWaveBytes = kWinBytes + kRowBytes + kSlotStride * 4;
 static_assert(kWinBytes % 16 == 0 && kWaveBytes % 16 == 0, "16-byte LDS alignment");
 static_assert(kSegPerEgo <= kWave, "one window segment per lane");
 static_assert(kCostTokens + kVisible * kAgentTokens <= kContext, "row layout");
-static_assert(kCopyItems > kWave && kCopyItems <= 2 * kWave, "copied tokens take one or two per lane");
+static_assert(kVisible * kAgentTokens > 2 * kWave && kVisible * kAgentTokens <= 3 * kWave,
+              "agent-section tokens: two per lane and a few on a third pass");
 typedef int v4i __attribute__((ext_vector_type(4)));
 
 struct TokLayout {
@@ -835,15 +836,17 @@ __global__ __launch_bounds__(kTokThreads) void tokens_kernel(jl_mapfgpt_t b) {
     const uint32_t qd0 = (uint32_t)(abs(di0 - kRadius) + abs(dj0 - kRadius)) << 16;
     const uint32_t qd1 = (uint32_t)(abs(di1 - kRadius) + abs(dj1 - kRadius)) << 16;
     constexpr uint64_t kQ1Lanes = (1ull << (kCostTokens - kWave)) - 1;
-    // coordinate token of lane l < 52: slot l / 4, field l % 4 (px, py, gx, gy)
-    const int c_slot = lane >> 2, c_field = lane & 3;
-    const int c_pos = kCostTokens + c_slot * kAgentTokens + c_field;
-    // copied tokens u = lane and u = lane + 64 (< 78): slot u / 6, token u % 6
-    const int u1 = lane + kWave < kCopyItems ? lane + kWave : lane;
-    const int k_slot0 = lane / kCopyTokens, k_tok0 = lane % kCopyTokens;
-    const int k_slot1 = u1 / kCopyTokens, k_tok1 = u1 % kCopyTokens;
-    const int k_pos0 = kCostTokens + k_slot0 * kAgentTokens + 4 + k_tok0;
-    const int k_pos1 = kCostTokens + k_slot1 * kAgentTokens + 4 + k_tok1;
+    // agent-section tokens t = lane, lane + 64 and lane + 128 (< 130): slot
+    // t / 10, field t % 10 (px, py, gx, gy, then the six copied tokens)
+    constexpr int kSectionTokens = kVisible * kAgentTokens;
+    const int a_slot0 = lane / kAgentTokens, a_f0 = lane % kAgentTokens;
+    const int a_slot1 = (lane + kWave) / kAgentTokens, a_f1 = (lane + kWave) % kAgentTokens;
+    const bool has_t2 = lane + 2 * kWave < kSectionTokens;
+    const int a_slot2 = has_t2 ? (lane + 2 * kWave) / kAgentTokens : 0;
+    const int a_f2 = has_t2 ? (lane + 2 * kWave) % kAgentTokens : 0;
+    // the previous ego's slots in use on this wavefront: the row keeps that
+    // ego's agent section (all of it is written for the first ego)
+    int prev_nsel = kVisible;
     const uint16_t* s_rec16 = reinterpret_cast<const uint16_t*>(s_rec);
 
     // Agent on bordered cell `cell` of this env or kNoAgent (sparse map):
@@ -928,24 +931,29 @@ __global__ __launch_bounds__(kTokThreads) void tokens_kernel(jl_mapfgpt_t b) {
             my_row[q0] = cost_token_flat(v0, cml, fmask);
             if (has_q1) my_row[q1] = cost_token_flat(v1, cml, fmask);
             wave_sync();
-            // agent tokens; a slot at or past nsel is padding
-            if (lane < kCoordLanes) {
-                const uint32_t o = my_slots[c_slot];
-                const int v = (int)s_rec16[o * (2 * kRecWords) + c_field];
-                const int t = coord_token(v - ((c_field & 1) ? ey : ex));
-                my_row[c_pos] = c_slot < nsel ? t : kTokPad;
-            }
-            {
-                const uint32_t o = my_slots[k_slot0];
-                const int t = kDense ? s_copy_tok[o * kCopyTokens + k_tok0]
-                                     : copy_token(s_copy[o * kCopyTokens + k_tok0], k_tok0);
-                my_row[k_pos0] = k_slot0 < nsel ? t : kTokPad;
-            }
-            if (lane + kWave < kCopyItems) {
-                const uint32_t o = my_slots[k_slot1];
-                const int t = kDense ? s_copy_tok[o * kCopyTokens + k_tok1]
-                                     : copy_token(s_copy[o * kCopyTokens + k_tok1], k_tok1);
-                my_row[k_pos1] = k_slot1 < nsel ? t : kTokPad;
+            // agent tokens; a slot at or past nsel is padding.  Only the
+            // slots in use now or for the previous ego are written: up to six
+            // (tokens 0..59 and padding at 60..63) in one pass of the lanes,
+            // up to twelve in two.
+            auto agent_token = [&](int slot, int f) -> int {
+                const uint32_t o = my_slots[slot];
+                int t;
+                if (f < 4) {
+                    const int v = (int)s_rec16[o * (2 * kRecWords) + f];
+                    t = coord_token(v - ((f & 1) ? ey : ex));
+                } else {
+                    t = kDense ? s_copy_tok[o * kCopyTokens + f - 4]
+                               : copy_token(s_copy[o * kCopyTokens + f - 4], f - 4);
+                }
+                return slot < nsel ? t : kTokPad;
+            };
+            const int used = nsel > prev_nsel ? nsel : prev_nsel;
+            prev_nsel = nsel;
+            my_row[kCostTokens + lane] = agent_token(a_slot0, a_f0);
+            if (used * kAgentTokens > kWave) {
+                my_row[kCostTokens + kWave + lane] = agent_token(a_slot1, a_f1);
+                if (used * kAgentTokens > 2 * kWave && has_t2)
+                    my_row[kCostTokens + 2 * kWave + lane] = agent_token(a_slot2, a_f2);
             }
             wave_sync();
             out = reinterpret_cast<const v4i*>(my_row)[lane];
