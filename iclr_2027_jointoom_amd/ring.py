@@ -68,6 +68,7 @@ import ctypes
 import hashlib
 import json
 import multiprocessing as mp
+import signal
 import threading
 import time
 from pathlib import Path
@@ -94,14 +95,27 @@ class RingClosed(Exception):
     free stage slot."""
 
 
+_CONTEXT = None
+
+
 def _process_context():
     """Start method of producer processes, and the context the rings' locks
     and events come from: a forkserver whose server has imported this
     module.  Producers then fork from a process that never touched the GPU,
-    and they start without importing torch again."""
-    ctx = mp.get_context("forkserver")
-    ctx.set_forkserver_preload([__name__])
-    return ctx
+    and they start without importing torch again.  Where SIGCHLD or SIGINT
+    has a handler installed outside Python (a preloaded profiler library
+    does this in every process it starts), the forkserver cannot restore it
+    in the processes it forks and they exit at once: producers are then
+    spawned as fresh interpreters instead."""
+    global _CONTEXT
+    if _CONTEXT is None:
+        foreign = any(signal.getsignal(s) is None for s in (signal.SIGCHLD, signal.SIGINT))
+        if foreign:
+            _CONTEXT = mp.get_context("spawn")
+        else:
+            _CONTEXT = mp.get_context("forkserver")
+            _CONTEXT.set_forkserver_preload([__name__])
+    return _CONTEXT
 
 
 class _SharedBlock:

@@ -303,6 +303,30 @@ def test_ring_stage_source_streams_frozen_records_in_order(tmp_path):
         src.close()
 
 
+def test_producers_are_spawned_where_signal_handlers_are_foreign(tmp_path, monkeypatch):
+    """A SIGCHLD handler installed outside Python (as a preloaded profiler
+    library installs one) makes the forkserver's children exit at once, so
+    the producers are spawned instead, and they stream the same stages."""
+    from iclr_2027_jointoom_amd import ring as ring_mod
+
+    real = ring_mod.signal.getsignal
+    monkeypatch.setattr(ring_mod.signal, "getsignal",
+                        lambda s: None if s == ring_mod.signal.SIGCHLD else real(s))
+    monkeypatch.setattr(ring_mod, "_CONTEXT", None)
+    assert ring_mod._process_context().get_start_method() == "spawn"
+    grids, stages = make_records(E=2, A=3, S=4)
+    save_records(tmp_path / "rec", backend="mapf_gpt", grids=grids, stages=stages, metadata={})
+    ring = RingBuffer(capacity=2 * 6, feature_dim=13, num_envs=2, agents_per_env=3)
+    config = {"num_agents": 3, "num_steps": 4, "map_names": ["a", "b"]}
+    src = RingStageSource(ring, "mapf_gpt", config, records=tmp_path / "rec", timeout=60, workers=2)
+    try:
+        src.start()
+        for s in range(4):
+            assert np.array_equal(src.next_rows(), stages[s]), s
+    finally:
+        src.close()
+
+
 def test_close_stops_blocked_producers_without_terminating_them(tmp_path):
     """Producers waiting for a free slot (the consumer stopped reading) exit
     by themselves when the source closes: exit code 0, no SIGTERM, well
