@@ -18,7 +18,7 @@
 namespace jl {
 namespace {
 
-constexpr int kStepThreads = 256;
+constexpr int kStepThreads = 1024;  // workgroup size cap of a step
 constexpr uint32_t kEmpty = 0xFFFFFFFFu;
 
 __device__ __forceinline__ uint32_t hslot(uint32_t cell, uint32_t mask) {
@@ -129,7 +129,8 @@ __device__ __forceinline__ uint64_t rng_next(uint64_t* state) {
 // s_flag: the action as given (low byte) and the arrival latch.
 constexpr uint16_t kFlagArrived = 0x100;
 // Agents (and bitmap words) a thread holds in registers: 1 up to
-// kStepThreads agents, else 4; agents past 4 * kStepThreads go through LDS.
+// kStepThreads agents (one thread per agent), else 4; agents past
+// 4 * kStepThreads go through LDS.
 inline int step_per(int A) { return A <= kStepThreads ? 1 : 4; }
 
 // Everything the step reads from HBM is requested at its start (the env's
