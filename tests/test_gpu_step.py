@@ -128,8 +128,10 @@ def test_c1_plumbing_rollout_matches_oracle_every_step(oracle):
         assert np.array_equal(builder.histories.cpu().numpy(), ob.histories.view(np.int16))
 
 
-@pytest.mark.parametrize("W,H,E,A", [(64, 64, 64, 128), (128, 128, 8, 512), (256, 256, 2, 1024)])
+@pytest.mark.parametrize("W,H,E,A", [(64, 64, 64, 128), (128, 128, 8, 512), (256, 256, 2, 1024),
+                                     (128, 128, 2, 1100)])
 def test_random_rollouts_match_oracle(oracle, W, H, E, A):
+    """One thread per agent up to 1,024 agents per env, four per thread beyond."""
     from iclr_2027_jointoom_amd.synthetic import make_batch, random_actions
 
     grids, starts, goals = make_batch(W + A, E, W, H, A)
