@@ -606,16 +606,15 @@ __global__ __launch_bounds__(kEdgeThreads) void edges_mask_kernel(jl_magat_t m) 
     const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);  // uniform per wavefront
     const size_t base = (size_t)env * A;
     // the env's positions and counts, then the slice totals (in that order:
-    // loads complete in issue order, and the totals are needed last)
+    // loads complete in issue order), each at a clamped index without a branch
     float2 pos[kMaskStage];
     int32_t cnt[kMaskStage];
 #pragma unroll
     for (int k = 0; k < kMaskStage; ++k) {
         const int a = tid + k * kEdgeThreads;
-        if (a < A) {
-            pos[k] = reinterpret_cast<const float2*>(m.pyg_pos)[base + a];
-            cnt[k] = m.edge_counts[base + a];
-        }
+        const size_t g = base + (a < A ? a : A - 1);
+        pos[k] = reinterpret_cast<const float2*>(m.pyg_pos)[g];
+        cnt[k] = m.edge_counts[g];
     }
     long long tot[kMaskTotals];
     if constexpr (kSummed) {
@@ -623,8 +622,17 @@ __global__ __launch_bounds__(kEdgeThreads) void edges_mask_kernel(jl_magat_t m) 
 #pragma unroll
         for (int k = 0; k < kMaskTotals; ++k) {
             const int j = tid + k * kEdgeThreads;
-            tot[k] = j < slice ? totals[j] : 0;
+            const long long t = totals[j < slice ? j : 0];
+            tot[k] = j < slice ? t : 0;
         }
+    }
+    // every load above in flight together, received here (one round trip):
+    // left to itself the compiler moves loads into the branches that use them
+#pragma unroll
+    for (int k = 0; k < kMaskStage; ++k) asm volatile("" : "+v"(pos[k].x), "+v"(pos[k].y), "+v"(cnt[k]));
+    if constexpr (kSummed) {
+#pragma unroll
+        for (int k = 0; k < kMaskTotals; ++k) asm volatile("" : "+v"(tot[k]));
     }
     int wide = 0;
 #pragma unroll
