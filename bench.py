@@ -190,15 +190,32 @@ def copy_calibration() -> None:
     print(f"copied 3 x {n} bytes", flush=True)
 
 
+def load_probe():
+    """libjl_bench.so, the benchmark's own library with the HBM streaming
+    probe jl_hbm_stream (built beside libjointloom.so by the package's
+    build step; not part of the product library)."""
+    import torch  # noqa: F401  (torch's HIP runtime is the process's)
+
+    from iclr_2027_jointoom_amd.build import BENCH_OUTPUT
+
+    if not BENCH_OUTPUT.exists():
+        raise RuntimeError(f"{BENCH_OUTPUT} is missing: build first (python -c 'import __graft_entry__ as g; g.build()')")
+    lib = ctypes.CDLL(str(BENCH_OUTPUT))
+    lib.jl_hbm_stream.restype = ctypes.c_int32
+    lib.jl_hbm_stream.argtypes = [ctypes.c_int32, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64,
+                                  ctypes.c_void_p, ctypes.c_int32, ctypes.c_void_p]
+    return lib
+
+
 def fetch_probe() -> None:
     """Three launches of jl_hbm_stream kind 10 over 256 MiB: one isolated
     16-byte read per 256-byte block (1,048,576 reads), the reference reading
     for the bytes the L2 fetches per read under the FETCH_SIZE counter."""
     import torch
 
-    from iclr_2027_jointoom_amd._abi import check, load_library
+    from iclr_2027_jointoom_amd._abi import check
 
-    lib = load_library()
+    lib = load_probe()
     n = 256 << 20
     a = torch.ones(n // 4, dtype=torch.int32, device="cuda")
     sink = torch.zeros(1 << 16, dtype=torch.int32, device="cuda")
@@ -220,9 +237,9 @@ def achievable_bandwidth(reps: int = 10) -> dict:
     "fraction of achievable" beside the published peak."""
     import torch
 
-    from iclr_2027_jointoom_amd._abi import check, load_library
+    from iclr_2027_jointoom_amd._abi import check
 
-    lib = load_library()
+    lib = load_probe()
     n = 1 << 30
     a = torch.ones(n // 4, dtype=torch.int32, device="cuda")
     b = torch.empty_like(a)

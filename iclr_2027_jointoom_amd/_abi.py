@@ -209,7 +209,6 @@ SIGNATURES = {
     "jl_expand_records": (c_int32, [ctypes.POINTER(RecordsDesc), c_void_p]),
     "jl_ring_upload_compact": (c_int32, [ctypes.POINTER(StageUploadDesc), c_void_p]),
     "jl_decode_to_uint8": (c_int32, [c_void_p, c_void_p, c_int64, c_int32, c_void_p]),
-    "jl_hbm_stream": (c_int32, [c_int32, c_void_p, c_void_p, c_int64, c_void_p, c_int32, c_void_p]),
     "jl_error_string": (ctypes.c_char_p, [c_int32]),
     "jl_version": (ctypes.c_char_p, []),
 }

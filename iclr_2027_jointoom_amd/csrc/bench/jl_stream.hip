@@ -2,7 +2,23 @@
 // reaches on this device (16-byte non-temporal loads, non-temporal or plain
 // stores, grid-stride or one contiguous chunk per workgroup, four accesses in
 // flight per thread), the "achievable" denominator of the
-// measurement beside the published peak.  Not part of the hot path.
+// measurement beside the published peak.  Not part of the hot path: it is
+// built into libjl_bench.so, which only the benchmark loads.
+//
+//   int jl_hbm_stream(int32_t kind, const void* src, void* dst, int64_t bytes,
+//                     uint32_t* sink, int32_t workgroups, jl_stream_t stream);
+//
+// One launch moving `bytes` (a multiple of 16, 16-byte aligned buffers) with
+// 16-byte accesses (non-temporal loads): kind 0 = read `src` only (sink: one
+// word per workgroup, written only in a practically impossible case, so the
+// reads are kept), 1 = write `dst` only, 2 = copy `src` to `dst`
+// (non-temporal stores), 3 and 4 = write and copy with plain stores, over
+// `workgroups` 256-thread workgroups striding the whole range; kinds 5-9 are
+// kinds 0-4 with each workgroup streaming one contiguous chunk instead (5
+// read, 6 and 7 write and copy non-temporal, 8 and 9 write and copy plain).
+// Kind 10 reads one 16-byte word at the start of every 256-byte block of
+// `src` (bytes a multiple of 256), for the HBM fetch granularity under the
+// FETCH_SIZE counter.  Returns JL_OK or JL_ERR_ARG.
 #include "jl_common.h"
 
 namespace jl {

@@ -64,7 +64,10 @@ __device__ __forceinline__ void load_free_rows(const uint32_t* __restrict__ env_
                 if (H == 32) {
                     v = (uint64_t)(~row[0]) & 0xFFFFFFFFull;
                 } else {
-                    const uint64_t lo = row[2 * k], hi = row[2 * k + 1];
+                    // a row of H % 64 == 32 columns ends in half a word: its
+                    // upper half is not read (it would be the next row's)
+                    const uint64_t lo = row[2 * k];
+                    const uint64_t hi = 2 * k + 1 < H / 32 ? row[2 * k + 1] : 0xFFFFFFFFu;
                     v = ~(lo | (hi << 32));
                 }
                 if (k == HW - 1) v &= RowWords<H>::kLastMask;
@@ -258,7 +261,8 @@ __device__ __forceinline__ void load_free_row(const uint32_t* __restrict__ env_b
             if (H == 32) {
                 v = (uint64_t)(~row[0]) & 0xFFFFFFFFull;
             } else {
-                v = ~((uint64_t)row[2 * k] | ((uint64_t)row[2 * k + 1] << 32));
+                const uint64_t hi = 2 * k + 1 < H / 32 ? row[2 * k + 1] : 0xFFFFFFFFu;  // half a word (H % 64 == 32)
+                v = ~((uint64_t)row[2 * k] | (hi << 32));
             }
             if (k == HW - 1) v &= RowWords<H>::kLastMask;
         }

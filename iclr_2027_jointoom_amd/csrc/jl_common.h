@@ -81,8 +81,10 @@ __device__ __forceinline__ uint32_t tile_offset(int x, int y, int W) {
     return (uint32_t)((y >> 3) + 1) * strip_cells(W) + (uint32_t)(x + 8) * 8u + (uint32_t)(y & 7);
 }
 
+// Map profiles: H a multiple of 32 (whole bitmap words per row, as
+// setup.py:34-38 requires) up to 256, 1 <= W <= 256.
 inline bool profile_ok(int w, int h) {
-    return (h == 32 || h == 64 || h == 128 || h == 256) && w >= 1 && w <= 256;
+    return h >= 32 && h <= 256 && h % 32 == 0 && w >= 1 && w <= 256;
 }
 
 inline int status(hipError_t e) { return e == hipSuccess ? JL_OK : (int)e; }
@@ -108,7 +110,11 @@ inline int device_cus() {
     switch (h) {                                               \
         case 32: { constexpr int H = 32; __VA_ARGS__; break; } \
         case 64: { constexpr int H = 64; __VA_ARGS__; break; } \
+        case 96: { constexpr int H = 96; __VA_ARGS__; break; } \
         case 128: { constexpr int H = 128; __VA_ARGS__; break; } \
+        case 160: { constexpr int H = 160; __VA_ARGS__; break; } \
+        case 192: { constexpr int H = 192; __VA_ARGS__; break; } \
+        case 224: { constexpr int H = 224; __VA_ARGS__; break; } \
         case 256: { constexpr int H = 256; __VA_ARGS__; break; } \
         default: return JL_ERR_PROFILE;                        \
     }

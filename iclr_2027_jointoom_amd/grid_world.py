@@ -10,7 +10,7 @@ on the caller's current stream.
 
 Map profile: the reference compiles one map size (MAPF_CUDA_MAP_PROFILE=WxH,
 default 128x128, setup.py:9-40).  The kernels here take the size at run time
-(H in {32, 64, 128, 256}, W <= 256); ``profile(w, h)`` returns a module-like
+(H a multiple of 32 up to 256, W <= 256); ``profile(w, h)`` returns a module-like
 namespace whose classes check grids against that size, and the module-level
 classes use the size named by MAPF_CUDA_MAP_PROFILE.
 """
@@ -1069,19 +1069,40 @@ class StatelessGridWorldSimulator(_Base, _PygModeMixin, _PygStorage):
 # ---------------------------------------------------------------------------
 # Map profiles
 # ---------------------------------------------------------------------------
-SUPPORTED_H = (32, 64, 128, 256)
+SUPPORTED_H = tuple(range(32, 257, 32))
+MAX_MAP_W = 256
 _PROFILES: dict = {}
 
 
 def parse_profile(text: str) -> tuple[int, int]:
-    """'WxH' -> (W, H) (setup.py:9-40 format)."""
+    """'WxH' -> (W, H), with the checks and messages of setup.py:9-40
+    (format, integers, positive, H a multiple of 32), plus this build's
+    limit of 256 on both sides (the LDS and the 16-bit coordinates the
+    kernels hold)."""
+    profile_text = text.strip().lower()
+    if "x" not in profile_text:
+        raise ValueError(
+            f"MAPF_CUDA_MAP_PROFILE must look like '<width>x<height>', got {profile_text!r}"
+        )
+    w_text, h_text = profile_text.split("x", 1)
     try:
-        w_text, h_text = text.lower().split("x")
         w, h = int(w_text), int(h_text)
     except ValueError as exc:
-        raise ValueError(f"map profile must look like WxH, got {text!r}") from exc
-    if h not in SUPPORTED_H or not 1 <= w <= 256:
-        raise ValueError(f"unsupported map profile {w}x{h}: H in {SUPPORTED_H}, 1 <= W <= 256")
+        raise ValueError(
+            f"MAPF_CUDA_MAP_PROFILE must contain integer width/height, got {profile_text!r}"
+        ) from exc
+    if w <= 0 or h <= 0:
+        raise ValueError(f"MAPF_CUDA_MAP_PROFILE must be positive, got {profile_text!r}")
+    if h % 32 != 0:
+        raise ValueError(
+            "MAPF_CUDA_MAP_PROFILE height must be a multiple of 32 so the "
+            f"compressed column layout stays integral, got {profile_text!r}"
+        )
+    if w > MAX_MAP_W or h not in SUPPORTED_H:
+        raise ValueError(
+            f"unsupported map profile {w}x{h}: this build takes 1 <= W <= {MAX_MAP_W} and "
+            f"H in {SUPPORTED_H}"
+        )
     return w, h
 
 
@@ -1189,4 +1210,7 @@ def profile(w: int, h: int) -> types.SimpleNamespace:
 
 
 def default_profile() -> types.SimpleNamespace:
-    return profile(*parse_profile(os.environ.get("MAPF_CUDA_MAP_PROFILE", "128x128")))
+    """The profile MAPF_CUDA_MAP_PROFILE names; 128x128 when it is unset or
+    empty (setup.py:10-12)."""
+    text = os.environ.get("MAPF_CUDA_MAP_PROFILE", "").strip()
+    return profile(*parse_profile(text or "128x128"))

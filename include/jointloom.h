@@ -43,7 +43,7 @@ typedef void* jl_stream_t; /* hipStream_t */
 enum {
     JL_OK = 0,
     JL_ERR_ARG = -1,         /* null pointer, non-positive size, size overflow */
-    JL_ERR_PROFILE = -2,     /* map_h not in {32,64,128,256} or map_w > 256 */
+    JL_ERR_PROFILE = -2,     /* map_h not a multiple of 32 in [32, 256], or map_w outside [1, 256] */
     JL_ERR_CAPACITY = -3     /* an edge buffer too small for the worst case */
 };
 
@@ -456,22 +456,6 @@ int jl_ring_upload_compact(jl_stage_upload_t* upload, jl_stream_t stream);
  * out[b, c, r, col] = (obs[b*2*diam + c*diam + r] >> col) & 1. */
 int jl_decode_to_uint8(const uint16_t* obs, uint8_t* out, int64_t n_batch,
                        int32_t diameter, jl_stream_t stream);
-
-/* HBM streaming probe (no counterpart in the reference): one launch moving
- * `bytes` (a multiple of 16, 16-byte aligned buffers) with 16-byte
- * accesses (non-temporal loads), kind 0 = read `src` only (sink: one word
- * per workgroup, written only in a practically impossible case, so the reads
- * are kept), 1 = write `dst` only, 2 = copy `src` to `dst` (non-temporal
- * stores), 3 and 4 = write and copy with plain stores, over `workgroups`
- * 256-thread workgroups striding the whole range; kinds 5-9 are kinds 0-4
- * with each workgroup streaming one contiguous chunk instead (5 read, 6 and
- * 7 write and copy non-temporal, 8 and 9 write and copy plain).  The
- * bandwidth a plain streaming kernel reaches on the device, the "achievable"
- * figure beside the published peak.  Kind 10 reads one 16-byte word at the
- * start of every 256-byte block of `src` (bytes a multiple of 256), for the
- * HBM fetch granularity under the FETCH_SIZE counter. */
-int jl_hbm_stream(int32_t kind, const void* src, void* dst, int64_t bytes, uint32_t* sink,
-                  int32_t workgroups, jl_stream_t stream);
 
 /* Text for a status code returned by any entry point. */
 const char* jl_error_string(int code);

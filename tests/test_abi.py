@@ -36,6 +36,17 @@ def test_every_declared_entry_point_is_exported(lib):
         assert getattr(lib, name) is not None
 
 
+def test_streaming_probe_lives_in_the_bench_library_only(lib):
+    """jl_hbm_stream (the benchmark's bandwidth probe) is exported by
+    libjl_bench.so and not by the product library."""
+    from iclr_2027_jointoom_amd.build import BENCH_OUTPUT
+
+    assert not hasattr(lib, "jl_hbm_stream")
+    probe = ctypes.CDLL(str(BENCH_OUTPUT))
+    assert probe.jl_hbm_stream is not None
+    assert "jl_hbm_stream" not in HEADER.read_text()
+
+
 def test_version_and_error_strings(lib):
     assert lib.jl_version().decode().startswith("jointloom-gfx950")
     assert b"invalid argument" in lib.jl_error_string(-1)
@@ -49,11 +60,15 @@ def test_host_side_argument_checks_return_before_device_work(lib):
 
     assert lib.jl_step(None, None) == -1
     assert lib.jl_encode_map(None, None, 1, 64, 64, None) == -1
-    assert lib.jl_encode_map(1, 1, 1, 64, 48, None) == -2  # H must be 32/64/128/256
+    assert lib.jl_encode_map(1, 1, 1, 64, 48, None) == -2  # H must be a multiple of 32 up to 256
     sim = SimDesc(n_envs=1, n_agents=4, map_w=64, map_h=64, task_mode=1)
     assert lib.jl_step(ctypes.byref(sim), None) == -1  # null buffers
-    sim.map_h = 96
-    assert lib.jl_step(ctypes.byref(sim), None) == -2
+    for bad_h in (80, 288, 0):
+        sim.map_h = bad_h
+        assert lib.jl_step(ctypes.byref(sim), None) == -2, bad_h
+    for good_h in (96, 160, 192, 224):  # every multiple of 32 is a profile (setup.py:34-38)
+        sim.map_h = good_h
+        assert lib.jl_step(ctypes.byref(sim), None) == -1, good_h  # passes the profile check
     b = MapfGPTDesc(n_envs=1, n_agents=4, map_w=300, map_h=64)
     assert lib.jl_mapfgpt_build_state(ctypes.byref(b), 1, 1, 1, 1, None) == -2
     assert lib.jl_mapfgpt_build_rows(ctypes.byref(b), None, None) == -1

@@ -1,4 +1,4 @@
-"""The HBM streaming probe (jl_hbm_stream) behind bench.py's achievable
+"""The HBM streaming probe (jl_hbm_stream in libjl_bench.so) behind bench.py's achievable
 bandwidth: a copy reproduces its source, a write fills the whole range with
 the probe's pattern, and a read (streaming or one word per 256-byte block)
 leaves its buffers alone."""
@@ -10,9 +10,10 @@ pytestmark = pytest.mark.gpu
 
 
 def test_stream_probe_copy_write_read():
-    from iclr_2027_jointoom_amd._abi import check, load_library
+    from bench import load_probe
+    from iclr_2027_jointoom_amd._abi import check
 
-    lib = load_library()
+    lib = load_probe()
     n = (1 << 20) + 4096  # not a multiple of the grid's stride
     src = torch.randint(0, 1 << 30, (n // 4,), dtype=torch.int32, device="cuda")
     dst = torch.zeros_like(src)
