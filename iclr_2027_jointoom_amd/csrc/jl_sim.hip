@@ -456,8 +456,9 @@ __global__ __launch_bounds__(kStepThreads) void step_kernel(jl_sim_t s) {
     __syncthreads();
     for (int a = tid; a < A; a += nt) {
         const uint32_t goal = s_goal[a];
-        if (s_cur[a] != goal) {
-            const uint32_t cell = (goal & 0xFFFFu) * H + (goal >> 16);
+        const uint32_t gx = goal & 0xFFFFu, gy = goal >> 16;
+        if (s_cur[a] != goal && gx < (uint32_t)W && gy < (uint32_t)H) {  // goals off the map reserve nothing
+            const uint32_t cell = gx * H + gy;
             atomicOr(&goal_bits[cell >> 5], 1u << (cell & 31));
         }
     }
@@ -1034,7 +1035,7 @@ extern "C" const char* jl_error_string(int code) {
     switch (code) {
         case JL_OK: return "success";
         case JL_ERR_ARG: return "invalid argument (null pointer or size out of range)";
-        case JL_ERR_PROFILE: return "unsupported map profile (map_h in {32,64,128,256}, map_w <= 256)";
+        case JL_ERR_PROFILE: return "unsupported map profile (map_h a multiple of 32 up to 256, 1 <= map_w <= 256)";
         case JL_ERR_CAPACITY: return "edge buffer smaller than the worst case";
         default: return code > 0 ? hipGetErrorString((hipError_t)code) : "unknown error";
     }

@@ -676,6 +676,14 @@ class GridWorldSimulator(_Base, _PygModeMixin, _PygStorage):
                 "lifelong initialisation",
             )
             self.t_max_free_cell_count.copy_(self.t_counts.max().reshape(1))
+            # every agent takes two distinct cells; with fewer the reference's
+            # slot search (utils_cuda.h:39-61) never ends, here it raises
+            fewest = int(self.t_counts.min().item())
+            _require(
+                fewest >= 2 * self.n_agents,
+                f"run_initialization needs 2 * n_agents = {2 * self.n_agents} free cells inside every env's "
+                f"real extent (distinct starts and goals); an env has {fewest}",
+            )
 
     def update_actions(self, new_actions: torch.Tensor) -> None:
         """grid_world_simulator.cpp:678-688."""

@@ -24,6 +24,14 @@
  *                           empty grids, history roll KAT
  *   jlo_magat_*             cell-level FOV KATs, edge closed forms,
  *                           integer goal-projection identity
+ *   jlo_splitmix64          published outputs of SplitMix64 from state 0
+ *   jlo_xorshift64s         an independent pure-Python restatement of the
+ *                           published generator, period structure checks
+ *   jlo_free_cells, jlo_init_agents, random lifelong goals
+ *                           hand-derived known answers, a set-based
+ *                           Python restatement on seeded rollouts, and the
+ *                           rule's invariants (distinct cells, free cells
+ *                           inside the real extent, reserved goals skipped)
  */
 #include <stdint.h>
 #include <stdlib.h>
@@ -307,21 +315,166 @@ static int assign_candidate_goals(const jl_sim_t* s, int e, const int32_t* fin) 
     return failed;
 }
 
+/* ---- generator-drawn lifelong goals and random placement ----------------
+ * The reference draws from one cuRAND XORWOW stream per agent
+ * (curand_init(seed, id, 0), grid_world_cuda.cu:458-479) with one thread per
+ * agent racing on atomicOr (128_agents_map_step.cu:265-343,
+ * grid_world_cuda.cu:405-436, utils_cuda.h:39-61), so its result depends on
+ * thread timing and cannot be restated.  This build's device rule, restated
+ * here, keeps the reference's search (a random start index into the env's
+ * free-cell list, then a linear probe with wrap-around) and makes it
+ * deterministic: one xorshift64* generator per agent (Marsaglia 2003, with
+ * the output multiplier of Vigna 2016, "An experimental exploration of
+ * Marsaglia's xorshift generators, scrambled") seeded through splitmix64
+ * (Steele, Lea and Flood 2014), start index = (output >> 32) mod count, and
+ * agents settled one after the other in id order. */
+uint64_t jlo_splitmix64(uint64_t x) {
+    x += 0x9E3779B97F4A7C15ull;
+    x = (x ^ (x >> 30)) * 0xBF58476D1CE4E5B9ull;
+    x = (x ^ (x >> 27)) * 0x94D049BB133111EBull;
+    return x ^ (x >> 31);
+}
+
+uint64_t jlo_xorshift64s(uint64_t* state) {
+    uint64_t x = *state;
+    x ^= x >> 12;
+    x ^= x << 25;
+    x ^= x >> 27;
+    *state = x;
+    return x * 0x2545F4914F6CDD1Dull;
+}
+
+/* Per-agent generator states for init_rng(seed) (setup_rng_kernel,
+ * grid_world_cuda.cu:458-470): state i = splitmix64(seed ^ splitmix64(i)),
+ * a zero state replaced by the golden-ratio constant (xorshift states must
+ * be nonzero). */
+void jlo_seed_rng(uint64_t* state, int64_t count, uint64_t seed) {
+    for (int64_t i = 0; i < count; ++i) {
+        const uint64_t v = jlo_splitmix64(seed ^ jlo_splitmix64((uint64_t)i));
+        state[i] = v ? v : 0x9E3779B97F4A7C15ull;
+    }
+}
+
+/* Free cells of each env inside its real extent (cache_map_free_cells_kernel,
+ * grid_world_cuda.cu:225-320): cells (x, y) with x < rw, y < rh and no
+ * obstacle, packed x << 16 | y, in cell order (x major), at offset e*W*H of
+ * free_cells; offsets[e] = e*W*H, or -1 for an env without a free cell. */
+void jlo_free_cells(const jl_sim_t* s, const int32_t* extents, uint32_t* free_cells, int32_t* offsets,
+                    int32_t* counts) {
+    const int E = s->n_envs, W = s->map_w, H = s->map_h;
+    const int words = W * H / 32;
+    for (int e = 0; e < E; ++e) {
+        const int rw = extents[2 * e], rh = extents[2 * e + 1];
+        const uint32_t* bits = s->grid_bits + (size_t)e * words;
+        uint32_t* out = free_cells + (size_t)e * W * H;
+        int n = 0;
+        for (int x = 0; x < W && x < rw; ++x)
+            for (int y = 0; y < H && y < rh; ++y) {
+                const int cell = x * H + y;
+                if (!((bits[cell >> 5] >> (cell & 31)) & 1u)) out[n++] = ((uint32_t)x << 16) | (uint32_t)y;
+            }
+        counts[e] = n;
+        offsets[e] = n > 0 ? e * W * H : -1;
+    }
+}
+
+/* Random distinct starts and goals (init_agents_kernel,
+ * grid_world_cuda.cu:405-436, with find_unique_slot utils_cuda.h:39-61):
+ * agents in id order, each drawing a start and then a goal: a start index
+ * into the env's list, then the first list entry at or after it (with
+ * wrap-around) not taken by an earlier draw of the env.  A draw that finds
+ * no entry (more than count draws) leaves 0xFFFF coordinates, where the
+ * reference would search forever. */
+void jlo_init_agents(const jl_sim_t* s, const uint32_t* free_cells, const int32_t* offsets,
+                     const int32_t* counts) {
+    const int E = s->n_envs, A = s->n_agents;
+    for (int e = 0; e < E; ++e) {
+        const int count = counts[e], offset = offsets[e];
+        uint8_t* used = (uint8_t*)calloc((size_t)(count > 0 ? count : 1), 1);
+        for (int a = 0; a < A; ++a) {
+            const size_t g = (size_t)e * A + a;
+            uint64_t st = s->rng_state[g];
+            uint32_t picked[2] = {0xFFFFFFFFu, 0xFFFFFFFFu};
+            for (int which = 0; which < 2 && count > 0; ++which) {
+                int k = (int)((jlo_xorshift64s(&st) >> 32) % (uint64_t)count);
+                for (int attempt = 0; attempt < count; ++attempt) {
+                    if (!used[k]) {
+                        used[k] = 1;
+                        picked[which] = free_cells[offset + k];
+                        break;
+                    }
+                    if (++k >= count) k = 0;
+                }
+            }
+            s->rng_state[g] = st;
+            s->cur_x[g] = (uint16_t)(picked[0] >> 16);
+            s->cur_y[g] = (uint16_t)(picked[0] & 0xFFFFu);
+            s->goal_x[g] = (uint16_t)(picked[1] >> 16);
+            s->goal_y[g] = (uint16_t)(picked[1] & 0xFFFFu);
+        }
+        free(used);
+    }
+}
+
+/* Generator-drawn lifelong goals of one env after its move
+ * (128_agents_map_step.cu:265-343, made deterministic as above): goals of
+ * agents off their goal are reserved; each agent on its goal, in id order,
+ * draws a start index into the env's free-cell list and takes the first
+ * entry at or after it (with wrap-around) whose cell is not reserved, and
+ * reserves it.  Its own cell is not reserved, so it may draw it again (the
+ * goal is then unchanged but still flagged, as in the reference).  The
+ * generator advances once per agent on its goal, whether or not a cell is
+ * found.  Goals outside the map reserve nothing. */
+static void assign_random_goals(const jl_sim_t* s, int e, const int32_t* fin) {
+    const int A = s->n_agents, W = s->map_w, H = s->map_h;
+    const int count = s->env_counts[e], offset = s->env_offsets[e];
+    uint8_t* reserved = (uint8_t*)calloc((size_t)W * H, 1);
+    for (int i = 0; i < A; ++i) {
+        const size_t g = (size_t)e * A + i;
+        const int gx = s->goal_x[g], gy = s->goal_y[g];
+        if (fin[2 * i] == gx && fin[2 * i + 1] == gy) continue;
+        if (gx < W && gy < H) reserved[gx * H + gy] = 1;
+    }
+    for (int i = 0; i < A && count > 0; ++i) {
+        const size_t g = (size_t)e * A + i;
+        if (fin[2 * i] != s->goal_x[g] || fin[2 * i + 1] != s->goal_y[g]) continue;
+        uint64_t st = s->rng_state[g];
+        int k = (int)((jlo_xorshift64s(&st) >> 32) % (uint64_t)count);
+        for (int attempt = 0; attempt < count; ++attempt) {
+            const uint32_t packed = s->free_cells[offset + k];
+            const int x = (int)(packed >> 16), y = (int)(packed & 0xFFFFu);
+            if (x < W && y < H && !reserved[x * H + y]) {
+                reserved[x * H + y] = 1;
+                s->goal_x[g] = (uint16_t)x;
+                s->goal_y[g] = (uint16_t)y;
+                s->goal_changed[g] = 1;
+                break;
+            }
+            if (++k >= count) k = 0;
+        }
+        s->rng_state[g] = st;
+    }
+    free(reserved);
+}
+
 /* Batched step, step_kernel 128_agents_map_step.cu:25-262 (positions are
  * cached as uint8 there, :39-43; supported maps are at most 256 wide so the
  * cache is exact).  CostTracer steps (task mode 2, rebuttal/online-rl/native/
  * src/cuda_backend/128_agents_map_step.cu:219-222) count the step and stop
  * before the packed rows.  Lifelong steps with candidate lists take new goals
- * in canonical order (assign_candidate_goals) and count the step; the
- * generator-drawn resampling (:265-343) draws from cuRAND and is not
- * restated: without candidate lists this oracle leaves goals, goal_changed
- * (0) and reset flags (0) as a step without arrivals would. */
+ * in canonical order (assign_candidate_goals) and count the step; without
+ * them, given the generator states and free-cell lists, goals are drawn by
+ * assign_random_goals (the reference's :265-343 rule made deterministic; no
+ * step count, as there), and with neither goals stay as a step without
+ * arrivals would leave them. */
 void jlo_step(const jl_sim_t* s, int naive) {
     const int E = s->n_envs, A = s->n_agents, W = s->map_w, H = s->map_h;
     const int words = W * H / 32;
     const int standard = s->task_mode == JL_TASK_STANDARD_MAPF;
     const int costtracer = s->task_mode == JL_TASK_COSTTRACER;
     const int by_candidates = s->task_mode == JL_TASK_LIFELONG && s->goal_candidates != NULL;
+    const int by_draws = s->task_mode == JL_TASK_LIFELONG && !by_candidates && s->rng_state != NULL &&
+                         s->free_cells != NULL && s->env_offsets != NULL && s->env_counts != NULL;
     int32_t* cur = (int32_t*)malloc(sizeof(int32_t) * (size_t)A * 4);
     int32_t* fin = cur + 2 * A;
     uint8_t* cat = (uint8_t*)malloc((size_t)A);
@@ -362,6 +515,8 @@ void jlo_step(const jl_sim_t* s, int naive) {
         if (by_candidates) {
             assign_candidate_goals(s, e, fin);
             s->step_counts[e] += 1;
+        } else if (by_draws) {
+            assign_random_goals(s, e, fin);
         }
         if (standard) {
             int all = 1;
@@ -593,6 +748,10 @@ void jlo_mapfgpt_bfs(const jl_mapfgpt_t* b) {
     for (int i = 0; i < N; ++i) {
         const uint16_t* st = b->state_packed + (size_t)i * 8;
         if (st[7] == 0) continue;
+        if (st[0] >= b->n_envs) { /* a row this builder never wrote: no field to refresh */
+            b->diagnostics[1] += 1;
+            continue;
+        }
         int overflow = 0;
         const int bad = jlo_bfs_u16(b->grid_bits + (size_t)st[0] * words, W, H, st[4], st[5],
                                     b->cost_to_go + (size_t)i * W * H, &overflow);
@@ -611,6 +770,7 @@ void jlo_mapfgpt_tokens(const jl_mapfgpt_t* b) {
     for (size_t c = 0; c < (size_t)E * cells; ++c) b->agent_at_cell[c] = -1;
     for (int i = 0; i < N; ++i) {
         const uint16_t* st = b->state_packed + (size_t)i * 8;
+        if (st[0] >= E) continue; /* no env to scatter into (rows written by this builder never have one) */
         if (st[2] >= W || st[3] >= H) {
             b->diagnostics[3] += 1;
             continue;
@@ -627,7 +787,7 @@ void jlo_mapfgpt_tokens(const jl_mapfgpt_t* b) {
         for (int t = 0; t < JLO_CONTEXT; ++t) out[t] = JLO_TOK_PAD;
         const uint16_t* ego = b->state_packed + (size_t)ego_i * 8;
         b->active_mask[ego_i] = (uint8_t)(ego[2] != ego[4] || ego[3] != ego[5]);
-        if (ego[2] >= W || ego[3] >= H) continue;
+        if (ego[2] >= W || ego[3] >= H || ego[0] >= E) continue;
         const uint16_t* cost = b->cost_to_go + (size_t)ego_i * cells;
         const uint16_t center = cost[ego[2] * H + ego[3]];
         for (int t = 0; t < JLO_COST_TOKENS; ++t) {

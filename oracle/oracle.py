@@ -11,6 +11,7 @@ through the same descriptor structs (with host pointers).
 from __future__ import annotations
 
 import ctypes
+import os
 import subprocess
 from pathlib import Path
 
@@ -19,12 +20,16 @@ import numpy as np
 from iclr_2027_jointoom_amd._abi import MagatDesc, MapfGPTDesc, SimDesc
 
 ORACLE_DIR = Path(__file__).resolve().parent
-LIB_PATH = ORACLE_DIR / "libjl_oracle.so"
+# JLO_SANITIZE=1: the AddressSanitizer + UBSan build (`make -C oracle sanitize`;
+# the interpreter needs the ASan runtime preloaded, see `make check-sanitize`)
+SANITIZE = os.environ.get("JLO_SANITIZE") == "1"
+LIB_PATH = ORACLE_DIR / ("libjl_oracle_asan.so" if SANITIZE else "libjl_oracle.so")
 _LIB = None
 
 
 def build() -> Path:
-    subprocess.run(["make", "-s", "-C", str(ORACLE_DIR)], check=True)
+    target = ["sanitize"] if SANITIZE else []
+    subprocess.run(["make", "-s", "-C", str(ORACLE_DIR), *target], check=True)
     return LIB_PATH
 
 
@@ -52,6 +57,14 @@ def lib() -> ctypes.CDLL:
         L.jlo_mapfgpt_append.argtypes = [ctypes.POINTER(MapfGPTDesc), vp]
         for name in ("jlo_magat_occupancy", "jlo_magat_nodes", "jlo_magat_edges"):
             getattr(L, name).argtypes = [ctypes.POINTER(MagatDesc)]
+        u64 = ctypes.c_uint64
+        L.jlo_splitmix64.argtypes = [u64]
+        L.jlo_splitmix64.restype = u64
+        L.jlo_xorshift64s.argtypes = [ctypes.POINTER(u64)]
+        L.jlo_xorshift64s.restype = u64
+        L.jlo_seed_rng.argtypes = [vp, ctypes.c_int64, u64]
+        L.jlo_free_cells.argtypes = [ctypes.POINTER(SimDesc), vp, vp, vp, vp]
+        L.jlo_init_agents.argtypes = [ctypes.POINTER(SimDesc), vp, vp, vp]
         _LIB = L
     return _LIB
 
@@ -145,6 +158,31 @@ class OracleSim:
             np.zeros((self.E, self.A)) if arrived is None else arrived, dtype=np.uint8)
         cnt = np.ascontiguousarray(np.zeros(self.E) if step_counts is None else step_counts, dtype=np.int32)
         lib().jlo_load_state(ctypes.byref(self.desc), _p(pos), _p(gol), _p(arr), _p(cnt))
+
+    def seed_rng(self, seed: int) -> None:
+        """init_rng: one xorshift64* state per agent (jlo_seed_rng)."""
+        self.rng_state = np.zeros(self.E * self.A, np.uint64)
+        lib().jlo_seed_rng(_p(self.rng_state), self.rng_state.size, int(seed) & 0xFFFFFFFFFFFFFFFF)
+        self.desc.rng_state = _p(self.rng_state)
+
+    def lifelong_init(self, extents=None) -> None:
+        """run_initialization: free-cell lists inside the real extents, then
+        random distinct starts and goals drawn from them; afterwards
+        lifelong steps draw new goals from the same lists."""
+        E, W, H = self.E, self.W, self.H
+        ext = np.ascontiguousarray(
+            np.tile([W, H], (E, 1)) if extents is None else extents, dtype=np.int32)
+        self.free_cells = np.zeros(E * W * H, np.uint32)
+        self.env_offsets = np.zeros(E, np.int32)
+        self.env_counts = np.zeros(E, np.int32)
+        lib().jlo_free_cells(ctypes.byref(self.desc), _p(ext), _p(self.free_cells), _p(self.env_offsets),
+                             _p(self.env_counts))
+        lib().jlo_init_agents(ctypes.byref(self.desc), _p(self.free_cells), _p(self.env_offsets),
+                              _p(self.env_counts))
+        d = self.desc
+        d.free_cells = _p(self.free_cells)
+        d.env_offsets = _p(self.env_offsets)
+        d.env_counts = _p(self.env_counts)
 
     def set_goal_candidates(self, candidates, cells, counts) -> None:
         """Candidate lists of the deterministic lifelong mode (host copies)."""

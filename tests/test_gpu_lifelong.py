@@ -120,3 +120,75 @@ def test_costtracer_mode_matches_oracle(oracle, W, E, A):
         osim.step(acts)
         compare_with_oracle(sim, osim, f"t={t}")
     assert sim.step_counts.cpu().tolist() == [8] * E
+
+
+@pytest.mark.parametrize("W,H,E,A,T,extent", [(32, 32, 3, 40, 40, None), (64, 64, 4, 128, 30, (50, 60)),
+                                              (96, 96, 2, 300, 20, (65, 65)), (128, 128, 2, 500, 12, None)])
+def test_random_lifelong_rollouts_match_oracle(oracle, W, H, E, A, T, extent):
+    """The generator-drawn lifelong path (the default task mode without
+    candidate lists; 128_agents_map_step.cu:265-343 and
+    grid_world_cuda.cu:225-479 with cuRAND's racing draws replaced by
+    per-agent xorshift64* draws settled in id order): init_rng, the free-cell
+    lists inside the real extents, the random distinct starts and goals, then
+    a reload with a third of the agents on their goal and a rollout in which
+    every agent reaching its goal draws a new one.  Cells, goals, flags, packed
+    rows, occupancy and every generator state equal the oracle's after each
+    step."""
+    from iclr_2027_jointoom_amd import profile
+    from iclr_2027_jointoom_amd.synthetic import iid_grid
+
+    print(f"[random lifelong] {W}x{H} E={E} A={A} T={T} extent={extent}", flush=True)
+    rng = np.random.default_rng(W + A)
+    grids = np.stack([iid_grid(rng, W, H, 0.2) for _ in range(E)])
+    extents = np.tile([W, H] if extent is None else extent, (E, 1)).astype(np.int32)
+    ext = profile(W, H)
+    g = torch.from_numpy(grids.astype(np.int32)).cuda()
+    seed = 4242 + A
+    sim = ext.GridWorldSimulator(g, A, 2, E * W * H, seed)
+    sim.set_real_map_extents(torch.from_numpy(extents).cuda())
+    sim.run_initialization()
+    osim = oracle.OracleSim(grids, A, task_mode=0, max_episode_steps=256)
+    osim.seed_rng(seed)
+    osim.lifelong_init(extents)
+    torch.cuda.synchronize()
+    assert np.array_equal(sim.counts.cpu().numpy(), osim.env_counts)
+    assert np.array_equal(sim.memory_tensors["offsets"].cpu().numpy(), osim.env_offsets)
+    fc = sim.memory_tensors["free_cell_list"].cpu().numpy().view(np.uint32)
+    for e in range(E):
+        lo = e * W * H
+        assert np.array_equal(fc[lo:lo + osim.env_counts[e]], osim.free_cells[lo:lo + osim.env_counts[e]])
+
+    def check(tag):
+        _compare_lifelong_goals(sim, osim, E * A, tag)
+
+    check("init")
+    # reload: every third agent's goal on its start, so it draws at once
+    starts = osim.positions()
+    goals = np.stack([osim.goal_x, osim.goal_y], -1).astype(np.int16)
+    goals[:, ::3] = starts[:, ::3]
+    sim.load_state(torch.from_numpy(starts).cuda(), torch.from_numpy(goals).cuda(),
+                   torch.zeros((E, A), dtype=torch.uint8, device="cuda"), torch.zeros(E, dtype=torch.int32, device="cuda"))
+    osim.load_state(starts, goals)
+    changed = 0
+    for t in range(T):
+        acts = rng.integers(0, 5, size=(E, A)).astype(np.uint8)
+        if t == 0:
+            acts[:] = 0
+        sim.update_actions(torch.from_numpy(acts).cuda())
+        sim.step_sim_only()
+        osim.step(acts)
+        compare_with_oracle(sim, osim, f"step {t}")
+        check(f"step {t}")
+        changed += int(osim.goal_changed.sum())
+    assert changed >= E * len(range(0, A, 3))
+
+
+def _compare_lifelong_goals(sim, osim, n, tag):
+    torch.cuda.synchronize()
+    for name, got, exp in (("cur_x", sim.cur_x, osim.cur_x.astype(np.int16)),
+                           ("cur_y", sim.cur_y, osim.cur_y.astype(np.int16)),
+                           ("goal_x", sim.goal_x, osim.goal_x.astype(np.int16)),
+                           ("goal_y", sim.goal_y, osim.goal_y.astype(np.int16)),
+                           ("rng_states", sim.memory_tensors["rng_states"][:n], osim.rng_state.view(np.int64))):
+        g = got.cpu().numpy()
+        assert np.array_equal(g, exp), f"{tag} {name} differs at {np.argwhere(g != exp)[:5].tolist()}"
