@@ -248,6 +248,85 @@ __device__ void wave_bfs_batched(const uint64_t (&fr)[RowWords<H>::HW], int gx, 
     }
 }
 
+// Planes of the levels of a search on a map of at most 4,096 cells (levels
+// stay below 4,096): four low planes in registers, eight high ones in LDS.
+constexpr int kFieldPlanes = 12;
+constexpr int kHighPlanes = kFieldPlanes - 4;
+// LDS of one wavefront's high planes: [plane][lane] 64-bit words.
+constexpr int kHighPlaneBytes = kHighPlanes * kWave * 8;
+
+// wave_bfs_batched without a distance array: the level of every reached cell
+// of this lane's row is left bit-sliced, bits 0-3 in lowp (lowp[b] bit y =
+// bit b of the level of cell (lane, y)) and bits 4-11 in s_high[b - 4][lane]
+// (this wavefront's kHighPlaneBytes of LDS), and the reached cells in vis
+// (the start included, at level 0).  One wavefront, one map row per lane,
+// rows of at most 64 columns.  Batch b runs levels 16 b + 1 .. 16 b + 16
+// unrolled; with a[j] the free cells not reached before batch level j, the
+// cells of level 16 b + 1 + j are a[j] ^ a[j + 1], so the low level bits of
+// the batch come from a few of those snapshots (bit 1: levels 16 b + 2, 3,
+// 6, 7, 10, 11, 14, 15 = (a1 ^ a3) | (a5 ^ a7) | (a9 ^ a11) | (a13 ^ a15);
+// bit 2: (a3 ^ a7) | (a11 ^ a15); bit 3: a7 ^ a15), the high bits are b for
+// a0 ^ a15 and b + 1 for a15 ^ a16 (level 16 b + 16), ORed into the LDS
+// planes by LDS atomics once per batch, and bit 0 is no work at all: a grid
+// is bipartite, so a level's parity is that of the Manhattan distance,
+// x + y + gx + gy.  Per level only the expansion and the update of the free
+// cells remain.  The search stops after the first batch whose last level
+// reached nothing (levels past the last reach nothing).
+template <int H>
+__device__ void wave_bfs_levels(uint64_t fr, int gx, int gy, uint64_t& vis, uint64_t (&lowp)[4],
+                                uint64_t* s_high) {
+    static_assert(RowWords<H>::HW == 1, "one 64-bit word per row");
+    const int lane = threadIdx.x & (kWave - 1);
+    uint64_t front = lane == gx ? 1ull << gy : 0ull;
+    uint64_t avail = fr & ~front;
+#pragma unroll
+    for (int p = 0; p < 4; ++p) lowp[p] = 0;
+#pragma unroll
+    for (int p = 0; p < kHighPlanes; ++p) s_high[p * kWave + lane] = 0;
+    for (int b = 0;; ++b) {
+        // snapshots are folded into the planes as soon as their partner
+        // exists, so that few of them are live at once
+        const uint64_t a0 = avail;
+        uint64_t s1 = 0, s3 = 0, s5 = 0, s7 = 0, s9 = 0, s11 = 0, s13 = 0, most = 0, last = 0;
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            const uint64_t up = from_lane_below(front);
+            const uint64_t down = from_lane_above(front);
+            const uint64_t nf = ((front << 1) | (front >> 1) | up | down) & avail;
+            avail ^= nf;
+            front = nf;
+            switch (j + 1) {  // avail is now a[j + 1]
+                case 1: s1 = avail; break;
+                case 3: lowp[1] |= s1 ^ avail; s3 = avail; break;
+                case 5: s5 = avail; break;
+                case 7: lowp[1] |= s5 ^ avail; lowp[2] |= s3 ^ avail; s7 = avail; break;
+                case 9: s9 = avail; break;
+                case 11: lowp[1] |= s9 ^ avail; s11 = avail; break;
+                case 13: s13 = avail; break;
+                case 15:
+                    lowp[1] |= s13 ^ avail;
+                    lowp[2] |= s11 ^ avail;
+                    lowp[3] |= s7 ^ avail;
+                    most = a0 ^ avail;
+                    last = avail;
+                    break;
+                case 16: last ^= avail; break;
+                default: break;
+            }
+        }
+        const int hb = __builtin_amdgcn_readfirstlane(b), hn = hb + 1;
+#pragma unroll
+        for (int k = 0; k < kHighPlanes; ++k) {
+            const uint64_t m = (((hb >> k) & 1) ? most : 0ull) | (((hn >> k) & 1) ? last : 0ull);
+            if (((hb | hn) >> k) & 1) atomicOr(reinterpret_cast<unsigned long long*>(s_high + k * kWave + lane), m);
+        }
+        if (!__any(front != 0)) break;
+    }
+    vis = fr & ~avail;
+    const uint64_t odd_cols = ((lane + gx + gy) & 1) ? 0x5555555555555555ull : 0xAAAAAAAAAAAAAAAAull;
+    lowp[0] = vis & odd_cols;
+}
+
 // Free-cell masks of map row x (0 for x >= W), for the group BFS.
 template <int H>
 __device__ __forceinline__ void load_free_row(const uint32_t* __restrict__ env_bits, int W, int x,

@@ -218,10 +218,107 @@ __device__ void store_field_tiles(const jl_mapfgpt_t& b, size_t agent_index, con
     }
 }
 
+// refresh_field on a marked map of at most 64 rows of at most 64 columns,
+// with no LDS field: wave_bfs_levels leaves every reached cell's level in
+// bit planes (the high ones in s_high, this wavefront's kHighPlaneBytes of
+// LDS); the greedy marks come from the two low planes without any
+// comparison of distances (two reachable neighbours' levels differ by
+// exactly one, the grid being bipartite, so a reachable neighbour is closer
+// iff a0 ^ a1 ^ b1, with a0, a1 the cell's level bits 0-1 and b1 the
+// neighbour's bit 1); and each lane turns its map row into the field's
+// 8-cell tile-row segments, two 8x8 bit transposes per segment (level bits
+// 0-7, then level bits 8-11 and the four mark bits), stored as 16-byte words
+// (consecutive lanes, consecutive rows of a strip).  Same tiles and info
+// bits as refresh_field<H, 1, true> (no level of such a map can overflow the
+// frontier).  Every lane calls it with wavefront-uniform arguments.
+template <int H>
+__device__ uint32_t refresh_field_levels(const jl_mapfgpt_t& b, size_t agent_index, uint32_t e, int gx, int gy,
+                                         int spx, int spy, uint64_t* s_high) {
+    const int W = b.map_w;
+    const int x = threadIdx.x & (kWave - 1);  // this lane's map row
+    const int words = W * H / 32;
+    bool ok = e < (uint32_t)b.n_envs && (uint32_t)gx < (uint32_t)W && (uint32_t)gy < (uint32_t)H;
+    const uint32_t* env_bits = b.grid_bits + (size_t)(ok ? e : 0) * words;
+    if (ok && bit_at(env_bits, gx * H + gy)) ok = false;
+    uint64_t vis = 0, pl[4] = {0, 0, 0, 0};
+    if (ok) {
+        uint64_t fr[1][1];
+        load_free_rows<H, 1>(env_bits, W, fr);
+        wave_bfs_levels<H>(fr[0][0], gx, gy, vis, pl, s_high);
+    } else {
+#pragma unroll
+        for (int p = 0; p < kHighPlanes; ++p) s_high[p * kWave + x] = 0;
+    }
+    // neighbours' reached cells aligned with this row's columns (off the
+    // map: none), and the closer reachable neighbours
+    const uint64_t v_up = from_lane_below(vis), v_dn = from_lane_above(vis);
+    const uint64_t v_lf = vis << 1, v_rt = vis >> 1;
+    const uint64_t a01 = pl[0] ^ pl[1];
+    const uint64_t m_up = vis & v_up & (a01 ^ from_lane_below(pl[1]));
+    const uint64_t m_dn = vis & v_dn & (a01 ^ from_lane_above(pl[1]));
+    const uint64_t m_lf = vis & v_lf & (a01 ^ (pl[1] << 1));
+    const uint64_t m_rt = vis & v_rt & (a01 ^ (pl[1] >> 1));
+    uint32_t info = ok ? 0u : kInfoBadGoal;
+    if ((uint32_t)spx < (uint32_t)W && (uint32_t)spy < (uint32_t)H) {
+        // greedy_mask at (spx, spy): a reachable cell's closer neighbours;
+        // an unreachable one is farther than each reachable neighbour
+        const bool reached = (lane_value(vis, spx) >> spy) & 1;
+        const uint64_t q0 = lane_value(reached ? m_up : v_up, spx), q1 = lane_value(reached ? m_dn : v_dn, spx);
+        const uint64_t q2 = lane_value(reached ? m_lf : v_lf, spx), q3 = lane_value(reached ? m_rt : v_rt, spx);
+        info |= (uint32_t)((q0 >> spy) & 1) << 3 | (uint32_t)((q1 >> spy) & 1) << 2 |
+                (uint32_t)((q2 >> spy) & 1) << 1 | (uint32_t)((q3 >> spy) & 1);
+    }
+    // the 16 bits of every cell's tile value: level bits 0-11, then the
+    // marks (bit 12 right, 13 left, 14 down, 15 up); every bit of an
+    // unreachable cell set (its byte of ~vis ORed into all 16)
+    if (x < (W + 7) / 8 * 8) {
+        uint4* tout = reinterpret_cast<uint4*>(b.cost_tiles + agent_index * tiled_cells(W, H));
+        const int strip_words = (int)(strip_cells(W) / 8u);
+        const uint32_t* s_high32 = reinterpret_cast<const uint32_t*>(s_high);
+#pragma unroll 1
+        for (int half = 0; half < (H + 31) / 32; ++half) {
+            // groups 4 half .. 4 half + 3: this 32-bit half of the high planes
+            uint32_t hp[kHighPlanes];
+#pragma unroll
+            for (int p = 0; p < kHighPlanes; ++p) hp[p] = s_high32[(p * kWave + x) * 2 + half];
+#pragma unroll 1
+            for (int q = 0; q < 4; ++q) {
+                const int k = 4 * half + q;  // segment: columns 8 k .. 8 k + 7
+                const uint64_t unr = (uint64_t)((uint32_t)(~vis >> (8 * k)) & 0xFFu) * 0x0101010101010101ull;
+                uint64_t lo = 0, hi = 0;
+#pragma unroll
+                for (int p = 0; p < 4; ++p) lo |= ((pl[p] >> (8 * k)) & 0xFFull) << (8 * p);
+#pragma unroll
+                for (int p = 0; p < 4; ++p) lo |= (uint64_t)((hp[p] >> (8 * q)) & 0xFFu) << (8 * (4 + p));
+#pragma unroll
+                for (int p = 0; p < 4; ++p) hi |= (uint64_t)((hp[4 + p] >> (8 * q)) & 0xFFu) << (8 * p);
+                hi |= ((m_rt >> (8 * k)) & 0xFFull) << 32 | ((m_lf >> (8 * k)) & 0xFFull) << 40 |
+                      ((m_dn >> (8 * k)) & 0xFFull) << 48 | ((m_up >> (8 * k)) & 0xFFull) << 56;
+                lo = transpose8x8(lo | unr);  // byte c: bits 0-7 of cell 8 k + c
+                hi = transpose8x8(hi | unr);  // byte c: bits 8-15
+                uint32_t w[4];
+#pragma unroll
+                for (int c = 0; c < 8; c += 2) {
+                    w[c / 2] = (uint32_t)((lo >> (8 * c)) & 0xFF) | (uint32_t)((hi >> (8 * c)) & 0xFF) << 8 |
+                               (uint32_t)((lo >> (8 * c + 8)) & 0xFF) << 16 |
+                               (uint32_t)((hi >> (8 * c + 8)) & 0xFF) << 24;
+                }
+                if (k < H / 8) tout[(k + 1) * strip_words + x + 8] = make_uint4(w[0], w[1], w[2], w[3]);
+            }
+        }
+    }
+    return info;
+}
+
 template <int H, int R, bool kMarked, bool kTiles = true>
 __device__ uint32_t refresh_field(const jl_mapfgpt_t& b, size_t agent_index, uint32_t e, int gx,
                                   int gy, int spx, int spy, uint16_t* s_dist) {
     constexpr int HW = RowWords<H>::HW;
+    if constexpr (R == 1 && HW == 1 && kMarked && kTiles) {
+        // no LDS field on this path: the caller's s_dist (at least
+        // kHighPlaneBytes, marked_wave_lds) holds the high level planes
+        return refresh_field_levels<H>(b, agent_index, e, gx, gy, spx, spy, reinterpret_cast<uint64_t*>(s_dist));
+    }
     const int W = b.map_w;
     const int lane = threadIdx.x & (kWave - 1);
     const int cells = W * H;
@@ -458,6 +555,14 @@ __global__ __launch_bounds__(kWave* R) void bfs_group_kernel(jl_mapfgpt_t b, int
     }
 }
 
+// LDS bytes of one wavefront of unpack_bfs_kernel: its field, or the high
+// level planes of refresh_field_levels where that is the path (W <= 64,
+// H <= 64) and they are larger.
+__host__ __device__ inline size_t marked_wave_lds(int W, int H) {
+    const size_t field = (size_t)W * H * 2;
+    return (W <= kWave && H <= 64 && field < (size_t)kHighPlaneBytes) ? (size_t)kHighPlaneBytes : field;
+}
+
 // ---------------------------------------------------------------------------
 // Pass 1 for maps of at most kMarkedCells cells (8 KB fields) when the
 // single-launch build does not apply: 1a and 1b in one launch, one lane per
@@ -476,7 +581,7 @@ __global__ __launch_bounds__(kWave* kWaves) void unpack_bfs_kernel(
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
     const int i = blockIdx.x * (kWave * kWaves) + threadIdx.x;
-    uint16_t* s_dist = s_dist_all + (size_t)wave * W * H;  // this wavefront's field
+    uint16_t* s_dist = s_dist_all + (size_t)wave * (marked_wave_lds(W, H) / 2);  // this wavefront's field
     // the build's diagnostics start from zero; pass 2 and append_actions add
     if (blockIdx.x == 0 && threadIdx.x < 4) b.diagnostics[threadIdx.x] = 0;
 
@@ -1095,7 +1200,10 @@ __host__ __device__ inline BuildLayout build_layout(int A, int W, int H, int wav
     const size_t room = off > kBuildFieldRoom ? off : kBuildFieldRoom;
     const size_t fit = room / field;
     L.bfs_waves = (int)(fit < (size_t)waves ? fit : (size_t)waves);
-    const size_t fields = (size_t)L.bfs_waves * field;
+    size_t fields = (size_t)L.bfs_waves * field;
+    // builds whose fields stay in registers keep their high level planes
+    // in the overlay instead (refresh_field_levels)
+    if (W <= kWave && H <= 64 && fields < (size_t)waves * kHighPlaneBytes) fields = (size_t)waves * kHighPlaneBytes;
     L.overlay = align16(off > fields ? off : fields);
     off = L.overlay;
     L.rec_off = off;
@@ -1231,10 +1339,29 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(H <= 1
     }
     lds_barrier();
 
-    // ---- changed goals: BFS fields overlaying the token area -----------------
+    // ---- changed goals: BFS fields --------------------------------------------
     const int nlist = __builtin_amdgcn_readfirstlane(*s_nlist);
-    // rounds of up to bfs_waves fields: each wavefront searches one into its
-    // LDS field, then the whole workgroup stores the round's tiles
+    if constexpr (R == 1 && RowWords<H>::HW == 1) {
+        // fields in registers (refresh_field_levels): wavefront w refreshes
+        // list entries w, w + kWaves, ... and stores their tiles itself
+        for (int k = wave; k < nlist; k += kWaves) {
+            const uint2 it = s_list[k];
+            const uint32_t a = (uint32_t)__builtin_amdgcn_readfirstlane((int)it.x);
+            const uint32_t sx = (uint32_t)__builtin_amdgcn_readfirstlane((int)it.y);
+            const uint32_t pos = (uint32_t)__builtin_amdgcn_readfirstlane((int)s_rec[a * kBuildRecWords]);
+            const uint32_t goal = (uint32_t)__builtin_amdgcn_readfirstlane((int)s_rec[a * kBuildRecWords + 1]);
+            const uint32_t bits = refresh_field_levels<H>(
+                b, (size_t)env * A + a, sx & 0xFFFFu, (int)(goal & 0xFFFFu), (int)(goal >> 16), (int)(pos & 0xFFFFu),
+                (int)(pos >> 16), reinterpret_cast<uint64_t*>(smem + (size_t)wave * kHighPlaneBytes));
+            if (lane == 0) s_info[a] |= bits;
+        }
+        // the refreshed tiles are stored before any window load of this
+        // workgroup
+        if (nlist > 0) __syncthreads();
+    } else
+    // rounds of up to bfs_waves fields overlaying the token area: each
+    // wavefront searches one into its LDS field, then the whole workgroup
+    // stores the round's tiles
     for (int r0 = 0; r0 < nlist; r0 += L.bfs_waves) {
         if (wave < L.bfs_waves && r0 + wave < nlist) {
             uint16_t* s_dist = reinterpret_cast<uint16_t*>(smem) + (size_t)wave * cells;
@@ -1696,7 +1823,7 @@ int launch_pass1(const jl_mapfgpt_t* b, const int16_t* rows, const int16_t* cx, 
     // LDS fields) run pass 1 as one launch; only that launch writes marks
     if (marked_fields(b->map_w, H)) {
         const dim3 grid((N + kWave * 4 - 1) / (kWave * 4));
-        const size_t lds = (size_t)4 * b->map_w * H * sizeof(uint16_t);
+        const size_t lds = (size_t)4 * marked_wave_lds(b->map_w, H);
         hipLaunchKernelGGL((unpack_bfs_kernel<H, R, kRows, 4>), grid, dim3(kWave * 4), lds, stream,
                            *b, rows, cx, cy, gx, gy);
         return launch_status();
