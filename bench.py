@@ -112,8 +112,11 @@ def cpu_baseline(args) -> dict:
 # invalidates the caches where it is recorded, which slowed the resident
 # loop by about 7 us per step with two events around every build.
 HIP_EVENT_DISABLE_SYSTEM_FENCE = 0x20000000
-# the timed loops bracket the hot kernel with events on every EVENT_EVERY-th step only
-EVENT_EVERY = 4
+# the timed loops bracket the hot kernel with events on every EVENT_EVERY-th
+# step only: each event is a packet of its own that the command processor
+# takes about 1.7 us to pass between the kernels, so a pair on every fourth
+# step cost the resident loop about 0.9 us per step
+EVENT_EVERY = 10
 
 
 class HipEvents:
