@@ -525,33 +525,56 @@ __global__ __launch_bounds__(kWave* kWaves) void bfs_kernel(jl_mapfgpt_t b, int 
     }
 }
 
-// Pass 1b on maps of more than 64 rows: one field at a time per workgroup
-// of R wavefronts (refresh_field_group), workgroup g scanning agents
-// [g * per_group, (g + 1) * per_group).
-template <int H, int R>
-__global__ __launch_bounds__(kWave* R) void bfs_group_kernel(jl_mapfgpt_t b, int per_group) {
+// Pass 1 as one launch on maps of more than 64 rows (and more than
+// kMarkedCells cells): unpack_kernel's work and the BFS of the changed goals.
+// Workgroup g of R wavefronts unpacks agents [g * per_group, (g + 1) *
+// per_group), one thread per agent and pass, and lists those whose goal
+// changed (reset flag) in LDS; then the whole workgroup refreshes their
+// fields one after the other (refresh_field_group), and each agent's thread
+// completes its info word.  A build without a changed goal is the unpack
+// alone.  The grid is sized to the workgroups resident at once (the group
+// BFS's registers allow two per CU), so the unpack's round trips overlap.
+template <int H, int R, bool kRows>
+__global__ __launch_bounds__(kWave* R) void unpack_group_bfs_kernel(
+    jl_mapfgpt_t b, const int16_t* __restrict__ raw_rows, const int16_t* __restrict__ cur_x,
+    const int16_t* __restrict__ cur_y, const int16_t* __restrict__ goal_x,
+    const int16_t* __restrict__ goal_y, int per_group) {
+    constexpr int kThreads = kWave * R;
     __shared__ uint64_t s_words[group_bfs_words<H, R>()];
     __shared__ uint32_t s_gm[8];
+    __shared__ int s_n;
+    extern __shared__ __align__(16) uint4 s_list[];  // [per_group]: agent, state row words y, z
     const int N = b.n_envs * b.n_agents;
     const int tid = threadIdx.x;
-    const int lane = tid & (kWave - 1);
     const int begin = blockIdx.x * per_group;
     const int end = (begin + per_group) < N ? (begin + per_group) : N;
-    for (int c0 = begin; c0 < end; c0 += kWave) {
-        // every wavefront reads the same 64 info words, so the ballots agree
-        const int i = c0 + lane;
-        const uint32_t mine = i < end ? b.agent_info[i] : 0u;
-        uint64_t todo = __ballot((mine & kInfoNeedsBfs) != 0);
-        while (todo) {
-            const int src = __ffsll((unsigned long long)todo) - 1;
-            todo &= todo - 1;
-            const size_t agent_index = (size_t)c0 + src;
-            const uint4 row = *reinterpret_cast<const uint4*>(b.state_packed + agent_index * 8);
-            const uint32_t bits = refresh_field_group<H, R>(
-                b, agent_index, row.x & 0xFFFFu, (int)(row.z & 0xFFFFu), (int)(row.z >> 16),
-                (int)(row.y & 0xFFFFu), (int)(row.y >> 16), s_words, s_gm);
-            if (tid == src) b.agent_info[agent_index] = (mine & ~(kInfoNeedsBfs | kInfoGreedy)) | bits;
+    // the build's diagnostics start from zero; pass 2 and append_actions add
+    if (blockIdx.x == 0 && tid < 4) b.diagnostics[tid] = 0;
+    if (tid == 0) s_n = 0;
+    __syncthreads();
+    for (int i = begin + tid; i < end; i += kThreads) {
+        uint32_t info;
+        const uint4 st = unpack_agent<kRows>(b, i, raw_rows, cur_x, cur_y, goal_x, goal_y, info);
+        const uint32_t px = st.y & 0xFFFFu, py = st.y >> 16;
+        if ((st.w >> 16) != 0) {
+            // info of a listed agent: completed after its refresh
+            s_list[atomicAdd(&s_n, 1)] = make_uint4((uint32_t)i, info | (st.x << 16), st.y, st.z);
+            continue;
         }
+        if (px < (uint32_t)b.map_w && py < (uint32_t)H) info |= kept_greedy<H, false>(b, (size_t)i, (int)px, (int)py);
+        b.agent_info[i] = info;
+    }
+    __syncthreads();
+    const int n = __builtin_amdgcn_readfirstlane(s_n);
+    for (int k = 0; k < n; ++k) {
+        const uint4 it = s_list[k];
+        const uint32_t agent = (uint32_t)__builtin_amdgcn_readfirstlane((int)it.x);
+        const uint32_t head = (uint32_t)__builtin_amdgcn_readfirstlane((int)it.y);
+        const uint32_t pos = (uint32_t)__builtin_amdgcn_readfirstlane((int)it.z);
+        const uint32_t goal = (uint32_t)__builtin_amdgcn_readfirstlane((int)it.w);
+        const uint32_t bits = refresh_field_group<H, R>(b, agent, head >> 16, (int)(goal & 0xFFFFu), (int)(goal >> 16),
+                                                        (int)(pos & 0xFFFFu), (int)(pos >> 16), s_words, s_gm);
+        if (tid == 0) b.agent_info[agent] = (head & 0xFFFFu) | bits;
     }
 }
 
@@ -657,7 +680,9 @@ constexpr int kDenseCellLimit = 16384;     // map cells up to which the agent ma
 constexpr int kSegPerEgo = kDiam * 3;
 constexpr int kRegionCols = 24;            // cells per region row (3 tile columns)
 constexpr int kSlotStride = 16;            // per-wave top-13 slot array (words)
-constexpr int kRecWords = 2;               // per-agent record: position word, goal word
+constexpr int kRecWords = 4;               // per-agent record: position word, goal word, window
+                                           // segment offset (bit 0: three strips), LDS map cell |
+                                           // window column shift << 24
 constexpr int kCopyTokens = 6;             // per-agent tokens independent of the ego: int32
                                            // tokens on dense maps, uint16 raw values (5 history
                                            // values, greedy mask) on sparse maps, where LDS is short
@@ -692,8 +717,8 @@ __host__ __device__ inline TokLayout tok_layout(int A, int W, int H) {
     off = align16(off + (size_t)L.occ_words * 4);
     L.pref_off = off;  // uint16 per occupancy word: occupied cells before the word (< A <= 65535)
     off = align16(off + (size_t)L.occ_words * 2);
-    L.ids_off = off;   // per occupied cell in cell order: the lowest id on it
-    if (!L.dense) off = align16(off + (size_t)A * 4);
+    L.ids_off = off;   // per occupied cell in cell order: the lowest id on it (+ a spare entry)
+    if (!L.dense) off = align16(off + (size_t)(A + 1) * 4);
     L.rec_off = off;
     off = align16(off + (size_t)A * kRecWords * 4);
     L.copy_off = off;
@@ -822,7 +847,7 @@ __global__ __launch_bounds__(kTokThreads) void tokens_kernel(jl_mapfgpt_t b) {
         for (int k = tid; k < mcells / 2; k += kTokThreads) m2[k] = make_uint2(kNoAgent, kNoAgent);
     } else {
         for (int k = tid; k < L.occ_words; k += kTokThreads) s_occ[k] = 0;
-        for (int k = tid; k < A; k += kTokThreads) s_ids[k] = kNoAgent;
+        for (int k = tid; k <= A; k += kTokThreads) s_ids[k] = kNoAgent;
     }
     // slot arrays only ever hold agent ids (stale entries stay readable);
     // row tokens past the agent section are always padding
@@ -840,9 +865,22 @@ __global__ __launch_bounds__(kTokThreads) void tokens_kernel(jl_mapfgpt_t b) {
         const uint32_t gx = st.z & 0xFFFFu, gy = st.z >> 16;
         if (a >= e_begin && a < e_end) b.active_mask[g] = (px != gx || py != gy) ? 1 : 0;
         const bool valid = px < (uint32_t)W && py < (uint32_t)H;
-        // position word (kNoAgent off the map: such an ego's row is padding)
-        s_rec[a * kRecWords + 0] = valid ? st.y : kNoAgent;
-        s_rec[a * kRecWords + 1] = st.z;
+        // position word (kNoAgent off the map: such an ego's row is padding),
+        // goal word, and the ego's window: the byte offset of its first
+        // tile-row segment from the env's first tiled field (bit 0: the
+        // window spans three column strips), its cell in the bordered LDS map
+        // and the window's first column inside its first strip
+        {
+            const int ex = valid ? (int)px : 0, ey = valid ? (int)py : 0;
+            const int tyl = ((ey - kRadius + 64) >> 3) - 8;  // floor((ey - 5) / 8)
+            const bool third = (tyl + 2) * 8 <= ey + kRadius;
+            const uint32_t seg = (uint32_t)a * (uint32_t)tiled_cells(W, H) * 2u +
+                                 (uint32_t)(tyl + 1) * strip_cells(W) * 2u + (uint32_t)(ex - kRadius + 8) * 16u;
+            const uint32_t mcell = (uint32_t)((ex + kRadius) * MH + ey + kRadius);
+            *reinterpret_cast<uint4*>(s_rec + a * kRecWords) =
+                make_uint4(valid ? st.y : kNoAgent, st.z, seg | (third ? 1u : 0u),
+                           mcell | ((uint32_t)((ey + 3) & 7) << 24));
+        }
         // raw history values (any uint16 is legal in a raw row, :442-451);
         // the greedy mask (:452-456) last, below
         const uint16_t* h = b.histories + g * 5;
@@ -956,10 +994,12 @@ __global__ __launch_bounds__(kTokThreads) void tokens_kernel(jl_mapfgpt_t b) {
 
     // Agent on bordered cell `cell` of this env or kNoAgent (sparse map):
     // the id at the occupied cell's rank.
+    // The rank is read unconditionally (an empty cell's rank is at most the
+    // occupied-cell count, the spare entry): no branch per probe.
     auto agent_at_rank = [&](uint32_t cell) -> uint32_t {
         const uint32_t w = s_occ[cell >> 5], bit = 1u << (cell & 31);
-        if (!(w & bit)) return kNoAgent;
-        return s_ids[s_pref[cell >> 5] + __popc(w & (bit - 1u))];
+        const uint32_t id = s_ids[s_pref[cell >> 5] + __popc(w & (bit - 1u))];
+        return (w & bit) ? id : kNoAgent;
     };
 
     // Window gather.  Lane l < 33 loads segment l = (row i, tile column j) of
@@ -977,37 +1017,36 @@ __global__ __launch_bounds__(kTokThreads) void tokens_kernel(jl_mapfgpt_t b) {
     const uint32_t strip_bytes = strip_cells(W) * 2u;
     const int g_seg = lane < kSegPerEgo ? lane : lane - kSegPerEgo;
     const int g_i = g_seg / 3, g_j = g_seg - (g_seg / 3) * 3;
-    auto seg_load = [&](uint32_t pos, int e, uint32_t& fill) -> uint4 {
-        const bool ok = pos != kNoAgent;
-        const int ex = ok ? (int)(pos & 0xFFFFu) : 0, ey = ok ? (int)(pos >> 16) : 0;
-        const int tyl = ((ey - kRadius + 64) >> 3) - 8;  // floor((ey - 5) / 8)
-        const bool third = (tyl + 2) * 8 <= ey + kRadius;
-        const int x = ex - kRadius + g_i;  // in [-5, W + 4]: the border covers it
-        const int tcol = tyl + 1 + ((g_j == 2 && !third) ? 1 : g_j);
+    // lane part of a segment's offset: row g_i of the window, strip g_j (a
+    // window of two strips re-reads the second for its third)
+    const uint32_t lane_seg3 = (uint32_t)g_i * 16u + (uint32_t)g_j * strip_bytes;
+    const uint32_t lane_seg2 = (uint32_t)g_i * 16u + (uint32_t)(g_j < 1 ? g_j : 1) * strip_bytes;
+    auto seg_load = [&](uint32_t seg, uint32_t& fill) -> uint4 {
         fill = 0u;
-        const uint32_t off = (uint32_t)e * (uint32_t)tcells * 2u + (uint32_t)tcol * strip_bytes + (uint32_t)(x + 8) * 16u;
+        const uint32_t off = (seg & ~15u) + ((seg & 1u) ? lane_seg3 : lane_seg2);
         return *reinterpret_cast<const uint4*>(env_tiles + off);
     };
 
     // One ego's row: tokens into my_row, then the 16-byte store.
-    auto produce = [&](uint32_t pos, int e, const uint16_t* win_base) {
+    auto produce = [&](const uint4 rec, int e, const uint16_t* win_base) {
         v4i out = {kTokPad, kTokPad, kTokPad, kTokPad};
+        const uint32_t pos = rec.x;
         if (pos != kNoAgent) {
             const int ex = (int)(pos & 0xFFFFu), ey = (int)(pos >> 16);
-            // region row = dx + 5, column = ey + dy - 8 * tyl (see seg_load)
-            const uint16_t* win = win_base + (ey - 8 * (((ey - kRadius + 64) >> 3) - 8) - kRadius);
+            // region row = dx + 5, column = dy + 5 + ((ey + 3) & 7) (see seg_load)
+            const uint16_t* win = win_base + (rec.w >> 24);
             const uint32_t center = field_distance(win[kRadius * kRegionCols + kRadius], fmask);
             const uint32_t v0 = win[win0];  // raw tiled values: cost_token_flat strips the marks
             const uint32_t v1 = win[win1];
             uint32_t id0, id1;
+            const uint32_t mcell = rec.w & 0xFFFFFFu;
             if (kDense) {
-                const uint32_t* mrow = s_map + (ex + kRadius) * MH + (ey + kRadius);
+                const uint32_t* mrow = s_map + mcell;
                 id0 = mrow[map0];
                 id1 = mrow[map1];
             } else {
-                const int mcell = (ex + kRadius) * MH + (ey + kRadius);
-                id0 = agent_at_rank((uint32_t)(mcell + map0));
-                id1 = agent_at_rank((uint32_t)(mcell + map1));
+                id0 = agent_at_rank(mcell + (uint32_t)map0);
+                id1 = agent_at_rank(mcell + (uint32_t)map1);
             }
             // candidates: (distance << 16 | id); an empty cell's key is all ones
             const uint32_t key0 = qd0 | id0, key1 = qd1 | id1;
@@ -1040,16 +1079,16 @@ __global__ __launch_bounds__(kTokThreads) void tokens_kernel(jl_mapfgpt_t b) {
             // slots in use now or for the previous ego are written: up to six
             // (tokens 0..59 and padding at 60..63) in one pass of the lanes,
             // up to twelve in two.
+            // both kinds read and the lane's kind selected (f is per lane):
+            // no divergent branch
             auto agent_token = [&](int slot, int f) -> int {
                 const uint32_t o = my_slots[slot];
-                int t;
-                if (f < 4) {
-                    const int v = (int)s_rec16[o * (2 * kRecWords) + f];
-                    t = coord_token(v - ((f & 1) ? ey : ex));
-                } else {
-                    t = kDense ? s_copy_tok[o * kCopyTokens + f - 4]
-                               : copy_token(s_copy[o * kCopyTokens + f - 4], f - 4);
-                }
+                const int fc = f & 3, fk = f < 4 ? 0 : f - 4;
+                const int v = (int)s_rec16[o * (2 * kRecWords) + fc];
+                const int ct = coord_token(v - ((f & 1) ? ey : ex));
+                const int kt = kDense ? s_copy_tok[o * kCopyTokens + fk]
+                                      : copy_token(s_copy[o * kCopyTokens + fk], fk);
+                const int t = f < 4 ? ct : kt;
                 return slot < nsel ? t : kTokPad;
             };
             const int used = nsel > prev_nsel ? nsel : prev_nsel;
@@ -1081,14 +1120,18 @@ __global__ __launch_bounds__(kTokThreads) void tokens_kernel(jl_mapfgpt_t b) {
     const uint16_t* win_b = reinterpret_cast<const uint16_t*>(my_win + kSegPerEgo);
     auto ego_a = [&](int p) { return e_begin + 2 * p; };
     auto ego_b = [&](int p) { return (e_begin + 2 * p + 1) < e_end ? e_begin + 2 * p + 1 : e_begin + 2 * p; };
-    auto uniform_pos = [&](int e) {
-        return (uint32_t)__builtin_amdgcn_readfirstlane((int)s_rec[e * kRecWords]);
+    // an ego's record, wavefront-uniform (the goal word is not needed here)
+    auto record = [&](int e) {
+        const uint4 r = *reinterpret_cast<const uint4*>(s_rec + e * kRecWords);
+        return make_uint4((uint32_t)__builtin_amdgcn_readfirstlane((int)r.x), 0u,
+                          (uint32_t)__builtin_amdgcn_readfirstlane((int)r.z),
+                          (uint32_t)__builtin_amdgcn_readfirstlane((int)r.w));
     };
     uint4 ga, gb;
     uint32_t fa, fb;
     auto stage = [&](int p) {
-        ga = seg_load(uniform_pos(ego_a(p)), ego_a(p), fa);
-        gb = seg_load(uniform_pos(ego_b(p)), ego_b(p), fb);
+        ga = seg_load(record(ego_a(p)).z, fa);
+        gb = seg_load(record(ego_b(p)).z, fb);
     };
     auto commit = [&]() {
         // every use of the loaded values stays here, so that the loads stay
@@ -1105,12 +1148,12 @@ __global__ __launch_bounds__(kTokThreads) void tokens_kernel(jl_mapfgpt_t b) {
     commit();
     for (int p = wave; p < npairs; p += kTokWaves) {
         const int pn = p + kTokWaves;
-        const uint32_t pos_a = uniform_pos(ego_a(p)), pos_b = uniform_pos(ego_b(p));
+        const uint4 rec_a = record(ego_a(p)), rec_b = record(ego_b(p));
         // always staged (no branch around the loads, which would make the
         // compiler wait for them early); after the last pair it repeats this one
         stage(pn < npairs ? pn : p);
-        produce(pos_a, ego_a(p), win_a);
-        produce(pos_b, ego_b(p), win_b);
+        produce(rec_a, ego_a(p), win_a);
+        produce(rec_b, ego_b(p), win_b);
         commit();
     }
 }
@@ -1828,21 +1871,25 @@ int launch_pass1(const jl_mapfgpt_t* b, const int16_t* rows, const int16_t* cx, 
                            *b, rows, cx, cy, gx, gy);
         return launch_status();
     }
+    if constexpr (R > 1) {
+        // unpack and the changed goals' fields in one launch: two workgroups
+        // of R wavefronts per CU (the group BFS's registers), each over a
+        // whole number of passes of its threads
+        const int max_groups = (N + kWave * R - 1) / (kWave * R);
+        int groups = device_cus() * 2;
+        if (groups > max_groups) groups = max_groups;
+        constexpr int kMaxList = 3072;  // 48 KB of LDS list per workgroup
+        if ((N + groups - 1) / groups > kMaxList) groups = (N + kMaxList - 1) / kMaxList;
+        const int per_group = ((N + groups - 1) / groups + kWave * R - 1) / (kWave * R) * (kWave * R);
+        hipLaunchKernelGGL((unpack_group_bfs_kernel<H, R, kRows>), dim3((N + per_group - 1) / per_group),
+                           dim3(kWave * R), (size_t)per_group * sizeof(uint4), stream, *b, rows, cx, cy, gx, gy,
+                           per_group);
+        return launch_status();
+    }
     hipLaunchKernelGGL((unpack_kernel<H, kRows>), dim3((N + kUnpackThreads - 1) / kUnpackThreads),
                        dim3(kUnpackThreads), 0, stream, *b, rows, cx, cy, gx, gy);
     int rc = launch_status();
     if (rc) return rc;
-    if constexpr (R > 1) {
-        // one field per workgroup of R wavefronts, the levels in registers:
-        // two workgroups per CU
-        const int max_groups = (N + kWave - 1) / kWave;
-        int groups = device_cus() * 2;
-        if (groups > max_groups) groups = max_groups;
-        const int per_group = ((N + groups - 1) / groups + kWave - 1) / kWave * kWave;
-        hipLaunchKernelGGL((bfs_group_kernel<H, R>), dim3((N + per_group - 1) / per_group), dim3(kWave * R), 0,
-                           stream, *b, per_group);
-        return launch_status();
-    }
     const int waves = pass1_waves(b->map_w, H);
     const size_t lds = (size_t)waves * b->map_w * H * sizeof(uint16_t);
     const int per_cu = (int)(160 * 1024 / lds) < 8 ? (int)(160 * 1024 / lds) : 8;
@@ -1963,7 +2010,9 @@ std::mutex g_scratch_mutex;
 int32_t* g_scratch_ptr[kMaxScratchDevices] = {};
 
 // Device address of `scratch` on the current device, looked up once per
-// device (with that device current) and kept.
+// device (with that device current) and kept for the life of the process
+// (so a hipDeviceReset, after which the array may live elsewhere, is not
+// supported between calls).
 int current_scratch(int32_t** out) {
     int dev = 0;
     int rc = status(hipGetDevice(&dev));

@@ -174,12 +174,18 @@ __global__ __launch_bounds__(kStepThreads) void step_kernel(jl_sim_t s) {
     const int cand_count = by_candidates ? min(s.candidate_counts[env], s.candidate_stride) : 0;
     const uint4* bits4 = reinterpret_cast<const uint4*>(s.grid_bits + (size_t)env * words);
     const int nvec = vec_words ? words / 4 : 0;
-    uint4 rb[kStepPer];
+    // the bitmap words as four scalar arrays: an array of uint4 was left in
+    // scratch memory (not promoted to registers) when kStepPer > 1
+    uint32_t rbx[kStepPer], rby[kStepPer], rbz[kStepPer], rbw[kStepPer];
     uint32_t rc[kStepPer], rg[kStepPer], rf[kStepPer];
 #pragma unroll
     for (int j = 0; j < kStepPer; ++j) {
         const int k = tid + j * nt;
-        rb[j] = bits4[k < nvec ? k : 0];
+        const uint4 v = bits4[k < nvec ? k : 0];
+        rbx[j] = v.x;
+        rby[j] = v.y;
+        rbz[j] = v.z;
+        rbw[j] = v.w;
     }
 #pragma unroll
     for (int j = 0; j < kStepPer; ++j) {
@@ -195,7 +201,7 @@ __global__ __launch_bounds__(kStepThreads) void step_kernel(jl_sim_t s) {
 #pragma unroll
     for (int j = 0; j < kStepPer; ++j) {
         const int k = tid + j * nt;
-        reinterpret_cast<uint4*>(s_bits)[k < nvec ? k : nvec] = rb[j];
+        reinterpret_cast<uint4*>(s_bits)[k < nvec ? k : nvec] = make_uint4(rbx[j], rby[j], rbz[j], rbw[j]);
     }
 #pragma unroll
     for (int j = 0; j < kStepPer; ++j) {

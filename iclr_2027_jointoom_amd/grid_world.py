@@ -455,7 +455,11 @@ class MapfGPTObservationBuilder(_Base):
         """Exact BFS distances [E, A, W, H] (-1 = unreachable), filled from the
         tiled fields on every read, on the current stream, so that builds
         replayed from captured graphs are seen as well (the reference writes
-        them on every refresh, mapf_gpt_cuda.cu:318-325)."""
+        them on every refresh, mapf_gpt_cuda.cu:318-325).  The tensor is the
+        same object on every read, but its contents are a snapshot of the
+        builds before that read: builds write only the private tiled copy,
+        so a caller that keeps the tensor must read ``builder.cost_to_go``
+        again after a build to see it."""
         check(
             self._lib.jl_mapfgpt_cost_to_go(self._desc_ref, _stream(self._device)),
             "MAPF-GPT cost-to-go copy",
@@ -469,7 +473,9 @@ class MapfGPTObservationBuilder(_Base):
 
     @property
     def agent_at_cell(self) -> torch.Tensor:
-        """Cell -> agent id map of the last build (-1 empty), filled on read."""
+        """Cell -> agent id map of the last build (-1 empty), filled on read:
+        like ``cost_to_go``, a snapshot that a kept tensor does not follow
+        into later builds."""
         check(
             self._lib.jl_mapfgpt_agent_at_cell(self._desc_ref, _stream(self._device)),
             "MAPF-GPT agent identity grid",
@@ -478,6 +484,10 @@ class MapfGPTObservationBuilder(_Base):
 
     @property
     def memory_tensors(self) -> dict:
+        """The builder's tensors (bind.cpp:98-116).  ``cost_to_go`` and
+        ``agent_at_cell`` are filled when this dict is read: snapshots of the
+        builds so far, to be read again through the attributes after a
+        later build."""
         return {
             "grid_compressed": self.t_grid_compressed,
             "state_packed": self.t_state_packed,
@@ -486,7 +496,7 @@ class MapfGPTObservationBuilder(_Base):
             "tokens": self.t_tokens,
             "active_mask": self.t_active_mask,
             "cost_to_go": self.cost_to_go,
-            "agent_at_cell": self.t_agent_at_cell,
+            "agent_at_cell": self.agent_at_cell,
             "goal_cache": self.t_goal_cache,
             "diagnostics": self.t_diagnostics,
             "pyg_ptr": self.t_pyg_ptr,

@@ -68,6 +68,7 @@ import ctypes
 import hashlib
 import json
 import multiprocessing as mp
+import platform
 import signal
 import threading
 import time
@@ -169,6 +170,20 @@ class _PublishedRows:
 _W_RESERVE, _W_COMPUTE, _W_ENVS = 0, 1, 2
 
 
+_TSO_MACHINES = ("x86_64", "amd64")
+
+
+def _require_total_store_order(machine: str | None = None) -> None:
+    """The stage ring publishes an env block with plain stores (rows, then the
+    env word) and no fence; only a host that keeps stores in program order
+    for other cores (x86-64) makes that a publication."""
+    machine = (machine if machine is not None else platform.machine()).lower()
+    if machine not in _TSO_MACHINES:
+        raise RuntimeError(
+            f"the stage ring needs a host with total store order (x86-64) to publish stages without a "
+            f"lock; this host is {machine!r}")
+
+
 class RingBuffer:
     """Shared host ring of ``capacity`` rows x ``feature_dim`` int16.
 
@@ -187,6 +202,7 @@ class RingBuffer:
         self.stage_mode = self.num_envs is not None and self.agents_per_env is not None
         self.stage_rows = self.num_stage_slots = None
         if self.stage_mode:
+            _require_total_store_order()
             if self.num_envs <= 0:
                 raise ValueError(f"num_envs must be positive, got {self.num_envs}")
             if self.agents_per_env <= 0:

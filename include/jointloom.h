@@ -229,7 +229,10 @@ int jl_mapfgpt_build_rows(const jl_mapfgpt_t* b, const int16_t* raw_rows,
  * device share its scratch: calls that overlap on one device (other streams,
  * other threads) race and must be serialised by the caller.  The count of
  * diagnostics waits that gave up is cleared with the scratch on every call
- * and is not reported.  `stream` must belong to the current device. */
+ * and is not reported.  `stream` must belong to the current device.  The
+ * scratch's device address is looked up once per device and kept for the
+ * life of the process: hipDeviceReset (which may move the array) is not
+ * supported between calls. */
 int jl_mapfgpt_build_rows_noalloc(const jl_mapfgpt_t* b, const int16_t* raw_rows,
                                   jl_stream_t stream);
 

@@ -399,3 +399,19 @@ def test_stage_ready_counts_and_reserve_pointer_follow_the_env_words():
         ring.write_stage_range(0, np.concatenate([env_block(1), env_block(0)]))
     ring.release_stage(0)
     assert list(ring.stage_ready_counts) == [0, 2] and not ring.is_stage_ready(0)
+
+
+def test_stage_ring_requires_total_store_order():
+    """Stage publication is lock-free and fence-free: hosts without x86-64's
+    store order are refused up front rather than left to race."""
+    from iclr_2027_jointoom_amd.ring import _require_total_store_order
+
+    _require_total_store_order("x86_64")
+    _require_total_store_order("AMD64")
+    for machine in ("aarch64", "ppc64le", "riscv64"):
+        with pytest.raises(RuntimeError, match="total store order"):
+            _require_total_store_order(machine)
+    with patch("platform.machine", return_value="aarch64"):
+        with pytest.raises(RuntimeError, match="total store order"):
+            RingBuffer(capacity=8, num_envs=2, agents_per_env=2)
+        RingBuffer(capacity=8)  # the stage-less ring takes reserve_lock

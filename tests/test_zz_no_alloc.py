@@ -3,7 +3,10 @@
 jl_mapfgpt_build_rows on identical builders: every output bit-exact, over
 calls in a row through the C ABI whose env counts shrink and grow again (the
 scratch keeps the previous call's contents), with rows whose diagnostics are
-nonzero, and on a map whose build takes the two-launch path."""
+nonzero, and on a map whose build takes the two-launch path.  No call
+allocates: torch's allocator and the device's free memory are unchanged
+around each one (the first call of the process aside, which may set up the
+HIP runtime's own state)."""
 import ctypes
 
 import numpy as np
@@ -59,6 +62,7 @@ def test_noalloc_build_matches_build_rows(W, H, sizes):
 
     lib = load_library()
     ext = profile(W, H)
+    warmed = False  # the first call may set up HIP's own state (module, kernel arguments)
     for call, (E, A) in enumerate(sizes):
         print(f"noalloc build: map {W}x{H}, call {call}, E={E}, A={A}", flush=True)
         rng = np.random.default_rng(1000 * call + E + A)
@@ -74,9 +78,15 @@ def test_noalloc_build_matches_build_rows(W, H, sizes):
             ref.build_tokens(rows)
             torch.cuda.synchronize()
             before = torch.cuda.memory_allocated()
+            free_before = torch.cuda.mem_get_info()[0]
             _noalloc_build(lib, mine, rows)
             torch.cuda.synchronize()
+            # nothing from torch's allocator, and (after the first call) no
+            # device memory from anywhere else in the process either
             assert torch.cuda.memory_allocated() == before
+            if warmed:
+                assert torch.cuda.mem_get_info()[0] == free_before, (call, "device memory was allocated")
+            warmed = True
             for name in OUTPUTS:
                 assert torch.equal(getattr(ref, name), getattr(mine, name)), (call, name)
         assert mine.diagnostics.abs().sum().item() > 0, call
