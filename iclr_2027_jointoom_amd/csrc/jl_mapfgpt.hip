@@ -635,31 +635,32 @@ __global__ __launch_bounds__(kWave* kWaves) void unpack_bfs_kernel(
 // Pass 2: tokens (mapf_gpt_materialize_tokens_kernel, :350-497) plus the
 // agent scatter and its diagnostics (:328-347).
 //
-// Phase 1 (whole workgroup, one env): each agent's record (position word,
-// kNoAgent off the map, and goal word), its six ego-independent tokens (five
-// history tokens and the greedy token, :437-456; on sparse maps their 16-bit
-// raw values, turned into tokens where a row copies them, to keep the LDS of
-// 1024 agents under 80 KB) and a cell -> agent map live in LDS.
-// The map is dense (one int32 per cell of the map grown by a kRadius border
-// of empty cells, so a window probe needs no bounds test) while it fits;
-// beyond, it is sparse: an occupancy bitmap of the same bordered map, the
-// count of occupied cells before each of its words, and the ids of the
-// occupied cells in cell order, so a probe is a bit test and, on an occupied
-// cell, one rank and one read.
+// Phase 1 (whole workgroup, one env): per agent a template of ten uint16
+// (position, goal, and codes of its five history values and greedy mask,
+// :437-456, from which a row's tokens follow in two operations) and the
+// offset of its window in its tiled field, and a cell -> agent map, in LDS.  The map is dense (one int32 per cell of the map
+// grown by a kRadius border of empty cells, so a window probe needs no bounds
+// test) while it fits; beyond, it is sparse: the ids of the occupied cells in
+// cell order, and per 32 cells of the same bordered map their occupancy bits
+// beside the count of occupied cells before them, so a probe is one 8-byte
+// read, a bit test, a rank (a bit-field extract and a population count) and
+// one read.
 // Phase 2 (each wavefront on its own, no workgroup barrier): a wavefront
 // produces its egos two at a time.  Lanes 0..32 load the 33 tile-row
 // segments of both egos' 11x11 windows (cells outside the map staged as
 // unreachable) for the next pair while the current pair is turned into
 // tokens.  Visible agents: lane l probes window cells l and l + 64 in the
-// map; a candidate's rank under the key (Manhattan distance, id) is the
-// number of smaller keys, counted by walking the ballot of candidates with
-// uniform readlanes; ranks 0..12 are the reference's sorted top 13 because
-// keys are unique.  Every token of the row is computed by exactly one lane
-// (two cost tokens per lane; agent-section token t = slot * 10 + field on
-// lane t % 64) into the wavefront's LDS row, which keeps the previous ego's
-// agent section, so only the slots in use now or then are rewritten (one
-// pass of the lanes for up to six); the row is then stored as 64 x 16-byte
-// writes.
+// map.  The window centre holds the ego's cell, whose agent has the only
+// distance-0 key and takes slot 0; every other candidate's rank under the key
+// (Manhattan distance, id) is 1 + the number of smaller keys, counted by
+// walking the ballot of candidates with uniform readlanes; ranks 0..12 are
+// the reference's sorted top 13 because keys are unique.  Every token of the
+// row is computed by exactly one lane (two cost tokens per lane through an
+// LDS table; agent-section token t = slot * 10 + field on lane t % 64, from
+// the slot's template) into the wavefront's LDS row, which keeps the previous
+// ego's agent section, so only the slots in use now or then are rewritten
+// (one pass of the lanes for up to six); the row is then stored as 64 x
+// 16-byte writes.
 // ---------------------------------------------------------------------------
 constexpr int kTokThreads = 1024;
 // Bound of a single-launch workgroup's wait for its launch's cleared totals
@@ -680,12 +681,22 @@ constexpr int kDenseCellLimit = 16384;     // map cells up to which the agent ma
 constexpr int kSegPerEgo = kDiam * 3;
 constexpr int kRegionCols = 24;            // cells per region row (3 tile columns)
 constexpr int kSlotStride = 16;            // per-wave top-13 slot array (words)
-constexpr int kRecWords = 4;               // per-agent record: position word, goal word, window
-                                           // segment offset (bit 0: three strips), LDS map cell |
-                                           // window column shift << 24
-constexpr int kCopyTokens = 6;             // per-agent tokens independent of the ego: int32
-                                           // tokens on dense maps, uint16 raw values (5 history
-                                           // values, greedy mask) on sparse maps, where LDS is short
+constexpr int kCopyTokens = 6;             // per-agent tokens independent of the ego: five history
+                                           // tokens and the greedy token
+// Per-agent template of the token pass: uint16 half f is the value behind
+// agent-section field f (position x, y, goal x, y, the codes of the five
+// history values, the greedy mask); an agent off the map has position
+// 0xFFFF, 0xFFFF (its first word is kNoAgent).
+constexpr int kTmplBytes = kAgentTokens * 2;
+static_assert(kAgentTokens == 4 + kCopyTokens, "template: four coordinates and the copied values");
+// Code of a history value v (any uint16) from which its token, 44 for the
+// empty action v = 5 and 45 + v otherwise (:437-451), follows as code + 44 +
+// (code >= 6): 0 for v = 5, v + 1 for v <= 4, v itself from 6 on.  The
+// greedy mask is its own code (token 50 + mask, :452-456).
+constexpr uint32_t kHistCodeStep = 6;
+__device__ __forceinline__ uint32_t history_code(uint32_t v) { return v == 5 ? 0u : (v < 5 ? v + 1 : v); }
+static_assert(kTokWait == kTokEmptyAction + 1, "history codes: 45 + v = code + 44 for v <= 4");
+
 // per-wavefront LDS: two egos' windows, the token row, the slot array
 constexpr int kWinBytes = 2 * kSegPerEgo * 16;
 constexpr int kRowBytes = kContext * 4;
@@ -697,10 +708,21 @@ static_assert(kVisible * kAgentTokens > 2 * kWave && kVisible * kAgentTokens <= 
               "agent-section tokens: two per lane and a few on a third pass");
 typedef int v4i __attribute__((ext_vector_type(4)));
 
+constexpr int kCentreCell = kRadius * kDiam + kRadius;  // 60: the ego's own cell
+static_assert(kCentreCell < kWave, "the centre is a first-cell probe");
+// Cost-token table: entry i in [0, 42] is the token of d - c = i - 21 (42
+// below -20, 0..40 between, 43 above +20); entry 43 is an unreachable cell's.
+constexpr int kLutEntries = 2 * kCostLimit + 4;
+constexpr int kLutUnreachable = 2 * kCostLimit + 3;
+__device__ __forceinline__ int cost_lut_entry(int i) {
+    return i == kLutUnreachable ? kTokUnreachable
+                                : (i == 0 ? kTokNegClip : (i > 2 * kCostLimit + 1 ? kTokPosClip : i - 1));
+}
+
 struct TokLayout {
     bool dense;
     int occ_words;  // occupancy words of a sparse map with its kRadius border (0 on dense maps)
-    size_t map_off, occ_off, pref_off, ids_off, rec_off, copy_off, wave_off, diag_off, total;
+    size_t map_off, occ_off, ids_off, tmpl_off, seg_off, lut_off, wave_off, diag_off, total;
 };
 
 __host__ __device__ inline size_t align16(size_t v) { return (v + 15) & ~(size_t)15; }
@@ -713,16 +735,16 @@ __host__ __device__ inline TokLayout tok_layout(int A, int W, int H) {
     size_t off = 0;
     L.map_off = off;
     if (L.dense) off = align16(off + (size_t)(W + 2 * kRadius) * (H + 2 * kRadius) * 4);
-    L.occ_off = off;
-    off = align16(off + (size_t)L.occ_words * 4);
-    L.pref_off = off;  // uint16 per occupancy word: occupied cells before the word (< A <= 65535)
-    off = align16(off + (size_t)L.occ_words * 2);
-    L.ids_off = off;   // per occupied cell in cell order: the lowest id on it (+ a spare entry)
+    L.occ_off = off;  // uint2 per 32 bordered cells: occupancy bits, occupied cells before them
+    off = align16(off + (size_t)L.occ_words * 8);
+    L.ids_off = off;  // per occupied cell in cell order: the lowest id on it (+ a spare entry)
     if (!L.dense) off = align16(off + (size_t)(A + 1) * 4);
-    L.rec_off = off;
-    off = align16(off + (size_t)A * kRecWords * 4);
-    L.copy_off = off;
-    off = align16(off + (size_t)A * kCopyTokens * (L.dense ? 4 : 2));
+    L.tmpl_off = off;
+    off = align16(off + (size_t)A * kTmplBytes);
+    L.seg_off = off;  // per agent: its window's first segment offset | three strips (see the kernel)
+    off = align16(off + (size_t)A * 4);
+    L.lut_off = off;
+    off = align16(off + (size_t)kLutEntries * 4);
     L.wave_off = off;
     off = align16(off + (size_t)kTokWaves * kWaveBytes);
     L.diag_off = off;
@@ -731,21 +753,22 @@ __host__ __device__ inline TokLayout tok_layout(int A, int W, int H) {
     return L;
 }
 
-// Cost token of a window value (mapf_gpt_cuda.cu:413-428) without branches;
-// unreachable cells, including those outside the map, hold kUnreachable, and
-// fmask strips a reachable value's greedy marks (field_mask).
-__device__ __forceinline__ int cost_token_flat(uint32_t v, int center_minus_limit, uint32_t fmask) {
-    const int t = (int)(v & fmask) - center_minus_limit;  // d + kCostLimit (marks stripped)
-    const int clip = t < 0 ? kTokNegClip : kTokPosClip;
-    const int r = (uint32_t)t <= (uint32_t)(2 * kCostLimit) ? t : clip;
-    return v == kUnreachable ? kTokUnreachable : r;
-}
-
 // Token of a copied per-agent value: a raw history value v (5 = empty,
 // else kTokWait + v, any uint16, mapf_gpt_cuda.cu:437-451) or, for k = 5, the
 // greedy mask (:452-456).
 __device__ __forceinline__ int copy_token(uint32_t v, int k) {
     return k == kCopyTokens - 1 ? kTokGreedy + (int)v : (v == 5 ? kTokEmptyAction : kTokWait + (int)v);
+}
+
+// Lanes of an agent-section pass whose token t = base + lane is a
+// coordinate field (t % 10 < 4), and of those the y fields (odd).
+__host__ __device__ constexpr uint64_t coord_lanes(int base, bool y_only) {
+    uint64_t m = 0;
+    for (int l = 0; l < kWave; ++l) {
+        const int f = (base + l) % kAgentTokens;
+        if (f < 4 && (!y_only || (f & 1))) m |= 1ull << l;
+    }
+    return m;
 }
 
 // build_scratch of the single-launch build (JL_BUILD_SCRATCH_WORDS int32):
@@ -825,28 +848,34 @@ __global__ __launch_bounds__(kTokThreads) void tokens_kernel(jl_mapfgpt_t b) {
     const int lane = tid & (kWave - 1);
     const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);  // uniform per wavefront
     const TokLayout L = tok_layout(A, W, H);
-    constexpr int MH = H + 2 * kRadius;  // dense map columns
+    constexpr int MH = H + 2 * kRadius;  // bordered map columns
     uint32_t* s_map = reinterpret_cast<uint32_t*>(smem + L.map_off);
-    uint32_t* s_occ = reinterpret_cast<uint32_t*>(smem + L.occ_off);
-    uint16_t* s_pref = reinterpret_cast<uint16_t*>(smem + L.pref_off);
+    uint2* s_occ = reinterpret_cast<uint2*>(smem + L.occ_off);
     uint32_t* s_ids = reinterpret_cast<uint32_t*>(smem + L.ids_off);
-    uint32_t* s_rec = reinterpret_cast<uint32_t*>(smem + L.rec_off);    // kRecWords per agent
-    uint16_t* s_copy = reinterpret_cast<uint16_t*>(smem + L.copy_off);  // kCopyTokens per agent
-    int* s_copy_tok = reinterpret_cast<int*>(smem + L.copy_off);          // the same, dense maps
+    uint32_t* s_tmpl = reinterpret_cast<uint32_t*>(smem + L.tmpl_off);  // kTmplBytes / 4 words per agent
+    uint32_t* s_seg = reinterpret_cast<uint32_t*>(smem + L.seg_off);
+    int* s_lut = reinterpret_cast<int*>(smem + L.lut_off);
     int* s_diag = reinterpret_cast<int*>(smem + L.diag_off);
     uint8_t* my_lds = smem + L.wave_off + (size_t)wave * kWaveBytes;
     uint4* my_win = reinterpret_cast<uint4*>(my_lds);                  // [2 egos][11 rows][3 segments]
     int* my_row = reinterpret_cast<int*>(my_lds + kWinBytes);           // [kContext]
     uint32_t* my_slots = reinterpret_cast<uint32_t*>(my_lds + kWinBytes + kRowBytes);
-    const size_t cells = (size_t)W * H;
-    const uint32_t fmask = field_mask(W, H);  // distance bits of a tiled field value
+    constexpr int kTmplWords = kTmplBytes / 4;
+    static_assert(kTmplBytes % 4 == 0, "template words");
+    // distance bits of a tiled field value: only maps of at most
+    // kMarkedCells cells, all of them dense here, carry greedy marks
+    const uint32_t fmask = kDense ? field_mask(W, H) : 0xFFFFu;
+    // phase 1 at the highest priority; the ego loop lowers it as each
+    // wavefront advances
+    __builtin_amdgcn_s_setprio(3);
+
     // ---- phase 1 -----------------------------------------------------------
     if (kDense) {
         const int mcells = (W + 2 * kRadius) * MH;  // even: MH is
         uint2* m2 = reinterpret_cast<uint2*>(s_map);
         for (int k = tid; k < mcells / 2; k += kTokThreads) m2[k] = make_uint2(kNoAgent, kNoAgent);
     } else {
-        for (int k = tid; k < L.occ_words; k += kTokThreads) s_occ[k] = 0;
+        for (int k = tid; k < L.occ_words; k += kTokThreads) s_occ[k] = make_uint2(0u, 0u);
         for (int k = tid; k <= A; k += kTokThreads) s_ids[k] = kNoAgent;
     }
     // slot arrays only ever hold agent ids (stale entries stay readable);
@@ -854,6 +883,7 @@ __global__ __launch_bounds__(kTokThreads) void tokens_kernel(jl_mapfgpt_t b) {
     if (lane < kSlotStride) my_slots[lane] = 0;
     if (lane < kContext - (kCostTokens + kVisible * kAgentTokens))
         my_row[kCostTokens + kVisible * kAgentTokens + lane] = kTokPad;
+    if (tid < kLutEntries) s_lut[tid] = cost_lut_entry(tid);
     if (tid < 4) s_diag[tid] = 0;
     lds_barrier();
     int d_over = 0, d_row = 0, d_dup = 0, d_bad = 0;
@@ -861,59 +891,45 @@ __global__ __launch_bounds__(kTokThreads) void tokens_kernel(jl_mapfgpt_t b) {
         const size_t g = (size_t)env * A + a;
         const uint4 st = *reinterpret_cast<const uint4*>(b.state_packed + g * 8);
         const uint32_t info = b.agent_info[g];
+        const uint16_t* h = b.histories + g * 5;
+        uint32_t hist[5];
+#pragma unroll
+        for (int k = 0; k < 5; ++k) hist[k] = h[k];  // any uint16 is legal in a raw row (:442-451)
         const uint32_t px = st.y & 0xFFFFu, py = st.y >> 16;
         const uint32_t gx = st.z & 0xFFFFu, gy = st.z >> 16;
         if (a >= e_begin && a < e_end) b.active_mask[g] = (px != gx || py != gy) ? 1 : 0;
         const bool valid = px < (uint32_t)W && py < (uint32_t)H;
-        // position word (kNoAgent off the map: such an ego's row is padding),
-        // goal word, and the ego's window: the byte offset of its first
-        // tile-row segment from the env's first tiled field (bit 0: the
-        // window spans three column strips), its cell in the bordered LDS map
-        // and the window's first column inside its first strip
+        // the byte offset of the first tile-row segment of the agent's
+        // window from the env's first tiled field, bit 0 set when the window
+        // spans three column strips (an agent off the map: cell 0's window)
         {
             const int ex = valid ? (int)px : 0, ey = valid ? (int)py : 0;
             const int tyl = ((ey - kRadius + 64) >> 3) - 8;  // floor((ey - 5) / 8)
             const bool third = (tyl + 2) * 8 <= ey + kRadius;
-            const uint32_t seg = (uint32_t)a * (uint32_t)tiled_cells(W, H) * 2u +
-                                 (uint32_t)(tyl + 1) * strip_cells(W) * 2u + (uint32_t)(ex - kRadius + 8) * 16u;
-            const uint32_t mcell = (uint32_t)((ex + kRadius) * MH + ey + kRadius);
-            *reinterpret_cast<uint4*>(s_rec + a * kRecWords) =
-                make_uint4(valid ? st.y : kNoAgent, st.z, seg | (third ? 1u : 0u),
-                           mcell | ((uint32_t)((ey + 3) & 7) << 24));
+            s_seg[a] = (uint32_t)a * (uint32_t)tiled_cells(W, H) * 2u + (uint32_t)(tyl + 1) * strip_cells(W) * 2u +
+                       (uint32_t)(ex - kRadius + 8) * 16u + (third ? 1u : 0u);
         }
-        // raw history values (any uint16 is legal in a raw row, :442-451);
-        // the greedy mask (:452-456) last, below
-        const uint16_t* h = b.histories + g * 5;
-        uint16_t* cp = s_copy + a * kCopyTokens;
-        int* cpt = s_copy_tok + a * kCopyTokens;
-#pragma unroll
-        for (int k = 0; k < 5; ++k) {
-            const uint16_t v = h[k];
-            if (kDense) {
-                cpt[k] = copy_token(v, k);
-            } else {
-                cp[k] = v;
-            }
-        }
+        // the template: position (kNoAgent off the map: such an ego's row is
+        // padding, and no window holds it), goal, history codes, greedy mask
+        uint32_t* tp = s_tmpl + a * kTmplWords;
+        tp[0] = valid ? st.y : kNoAgent;
+        tp[1] = st.z;
+        tp[2] = history_code(hist[0]) | (history_code(hist[1]) << 16);
+        tp[3] = history_code(hist[2]) | (history_code(hist[3]) << 16);
+        tp[4] = history_code(hist[4]) | ((info & kInfoGreedy) << 16);
         d_over += (int)(info >> kInfoOverflowShift);
         d_row += (info & kInfoBadRow) ? 1 : 0;
         d_bad += (info & kInfoBadGoal) ? 1 : 0;
         if (valid) {
+            const uint32_t cell = (px + kRadius) * MH + py + kRadius;
             if (kDense) {
                 // lowest id keeps a shared cell; each extra agent counts once
-                if (atomicMin(&s_map[(px + kRadius) * MH + py + kRadius], (uint32_t)a) != kNoAgent) ++d_dup;
+                if (atomicMin(&s_map[cell], (uint32_t)a) != kNoAgent) ++d_dup;
             } else {
-                const uint32_t cell = (px + kRadius) * MH + py + kRadius;
-                atomicOr(&s_occ[cell >> 5], 1u << (cell & 31));
+                atomicOr(&s_occ[cell >> 5].x, 1u << (cell & 31));
             }
         } else {
             ++d_bad;  // position off the map (scatter, :336-339)
-        }
-        const uint32_t greedy = info & kInfoGreedy;
-        if (kDense) {
-            cpt[5] = copy_token(greedy, 5);
-        } else {
-            cp[5] = (uint16_t)greedy;
         }
     }
     if (!kDense) {
@@ -921,15 +937,15 @@ __global__ __launch_bounds__(kTokThreads) void tokens_kernel(jl_mapfgpt_t b) {
         // window probe needs no bounds test): the occupied cells are ranked
         // in cell order (the count of occupied cells before each occupancy
         // word plus the set bits below the cell's own) and the lowest id on
-        // each occupied cell is kept at its rank.  The wave sums of the scan use
-        // wavefront 0's window area, which phase 2 fills later.
+        // each occupied cell is kept at its rank.  The wave sums of the scan use wavefront 0's
+        // window area, which phase 2 fills later.
         uint32_t* s_wsum = reinterpret_cast<uint32_t*>(smem + L.wave_off);
         lds_barrier();
         const int per = (L.occ_words + kTokThreads - 1) / kTokThreads;
         const int w0 = tid * per;
         const int w1 = (w0 + per) < L.occ_words ? (w0 + per) : L.occ_words;
         uint32_t sum = 0;
-        for (int w = w0; w < w1; ++w) sum += __popc(s_occ[w]);
+        for (int w = w0; w < w1; ++w) sum += __popc(s_occ[w].x);
         uint32_t incl = sum;
         for (int off = 1; off < kWave; off <<= 1) {
             const uint32_t t = __shfl_up(incl, off, kWave);
@@ -940,16 +956,16 @@ __global__ __launch_bounds__(kTokThreads) void tokens_kernel(jl_mapfgpt_t b) {
         uint32_t run = incl - sum;
         for (int k = 0; k < wave; ++k) run += s_wsum[k];
         for (int w = w0; w < w1; ++w) {
-            s_pref[w] = (uint16_t)run;
-            run += __popc(s_occ[w]);
+            s_occ[w].y = run;
+            run += __popc(s_occ[w].x);
         }
         lds_barrier();
         for (int a = tid; a < A; a += kTokThreads) {
-            const uint32_t pos = s_rec[a * kRecWords];
+            const uint32_t pos = s_tmpl[a * kTmplWords];
             if (pos == kNoAgent) continue;
             const uint32_t cell = ((pos & 0xFFFFu) + kRadius) * (uint32_t)MH + (pos >> 16) + kRadius;
-            const uint32_t bit = 1u << (cell & 31);
-            const uint32_t rank = s_pref[cell >> 5] + __popc(s_occ[cell >> 5] & (bit - 1u));
+            const uint2 ow = s_occ[cell >> 5];
+            const uint32_t rank = ow.y + __popc(ow.x & ((1u << (cell & 31)) - 1u));
             // lowest id keeps a shared cell; each extra agent counts once
             if (atomicMin(&s_ids[rank], (uint32_t)a) != kNoAgent) ++d_dup;
         }
@@ -968,38 +984,65 @@ __global__ __launch_bounds__(kTokThreads) void tokens_kernel(jl_mapfgpt_t b) {
 
     // ---- phase 2: lane constants ---------------------------------------------
     // Window cells q0 = lane and q1 = lane + 64 (row-major over the 11x11
-    // window; q1 exists on lanes 0..56): probed for agents and turned into
-    // cost tokens q0, q1.
-    const bool has_q1 = lane + kWave < kCostTokens;
-    const int q0 = lane, q1 = has_q1 ? lane + kWave : lane;
+    // window; lanes 57..63 repeat cell 120, whose probe they leave out):
+    // probed for agents and turned into cost tokens q0, q1.
+    const bool own_q1 = lane + kWave < kCostTokens;
+    const int q0 = lane, q1 = own_q1 ? lane + kWave : kCostTokens - 1;
     const int di0 = q0 / kDiam, dj0 = q0 % kDiam, di1 = q1 / kDiam, dj1 = q1 % kDiam;
     const int win0 = di0 * kRegionCols + dj0, win1 = di1 * kRegionCols + dj1;
     const int map0 = (di0 - kRadius) * MH + (dj0 - kRadius);
     const int map1 = (di1 - kRadius) * MH + (dj1 - kRadius);
     const uint32_t qd0 = (uint32_t)(abs(di0 - kRadius) + abs(dj0 - kRadius)) << 16;
     const uint32_t qd1 = (uint32_t)(abs(di1 - kRadius) + abs(dj1 - kRadius)) << 16;
-    constexpr uint64_t kQ1Lanes = (1ull << (kCostTokens - kWave)) - 1;
-    // agent-section tokens t = lane, lane + 64 and lane + 128 (< 130): slot
-    // t / 10, field t % 10 (px, py, gx, gy, then the six copied tokens)
-    constexpr int kSectionTokens = kVisible * kAgentTokens;
+    // probe lanes whose cell can hold a candidate other than the centre's
+    // agent: every q0 but the centre, q1 on lanes 0..56
+    constexpr uint64_t kProbe0 = ~(1ull << kCentreCell);
+    constexpr uint64_t kProbe1 = (1ull << (kCostTokens - kWave)) - 1;
+    // agent-section passes: token 121 + t, t = lane (pass 0), lane + 64 (pass
+    // 1), lane + 128 (pass 2, lanes 0..1: slot 12's fields 8 and 9); field f
+    // of slot s is half f of the template of the slot's agent
     const int a_slot0 = lane / kAgentTokens, a_f0 = lane % kAgentTokens;
     const int a_slot1 = (lane + kWave) / kAgentTokens, a_f1 = (lane + kWave) % kAgentTokens;
-    const bool has_t2 = lane + 2 * kWave < kSectionTokens;
-    const int a_slot2 = has_t2 ? (lane + 2 * kWave) / kAgentTokens : 0;
-    const int a_f2 = has_t2 ? (lane + 2 * kWave) % kAgentTokens : 0;
+    const int a_f2 = (lane & 1) + 8;
+    const uint32_t toff0 = (uint32_t)L.tmpl_off + (uint32_t)a_f0 * 2u;
+    const uint32_t toff1 = (uint32_t)L.tmpl_off + (uint32_t)a_f1 * 2u;
+    const uint32_t toff2 = (uint32_t)L.tmpl_off + (uint32_t)a_f2 * 2u;
+    constexpr uint64_t kCoord0 = coord_lanes(0, false), kCoordY0 = coord_lanes(0, true);
+    constexpr uint64_t kCoord1 = coord_lanes(kWave, false), kCoordY1 = coord_lanes(kWave, true);
+    const bool coord0 = (kCoord0 >> lane) & 1, coord1 = (kCoord1 >> lane) & 1;
+    // all ones on lanes of a y coordinate (selects ey over ex)
+    const int ysel0 = ((kCoordY0 >> lane) & 1) ? -1 : 0, ysel1 = ((kCoordY1 >> lane) & 1) ? -1 : 0;
+    // copied fields: token = code + base + (code >= step); the greedy
+    // field's step is past every code
+    const int cbase0 = a_f0 == kAgentTokens - 1 ? kTokGreedy : kTokEmptyAction;
+    const int cbase1 = a_f1 == kAgentTokens - 1 ? kTokGreedy : kTokEmptyAction;
+    const int cbase2 = a_f2 == kAgentTokens - 1 ? kTokGreedy : kTokEmptyAction;
+    const uint32_t cstep0 = a_f0 == kAgentTokens - 1 ? 0x10000u : kHistCodeStep;
+    const uint32_t cstep1 = a_f1 == kAgentTokens - 1 ? 0x10000u : kHistCodeStep;
+    const uint32_t cstep2 = a_f2 == kAgentTokens - 1 ? 0x10000u : kHistCodeStep;
+    uint32_t* const sink = my_slots + kSlotStride - 1;  // writes of lanes with nothing to write
+    int* const row_sink = reinterpret_cast<int*>(sink);
     // the previous ego's slots in use on this wavefront: the row keeps that
-    // ego's agent section (all of it is written for the first ego)
-    int prev_nsel = kVisible;
-    const uint16_t* s_rec16 = reinterpret_cast<const uint16_t*>(s_rec);
+    // ego's agent section (all of it is padding before the first ego)
+    int prev_n = kVisible;
 
-    // Agent on bordered cell `cell` of this env or kNoAgent (sparse map):
-    // the id at the occupied cell's rank.
-    // The rank is read unconditionally (an empty cell's rank is at most the
-    // occupied-cell count, the spare entry): no branch per probe.
-    auto agent_at_rank = [&](uint32_t cell) -> uint32_t {
-        const uint32_t w = s_occ[cell >> 5], bit = 1u << (cell & 31);
-        const uint32_t id = s_ids[s_pref[cell >> 5] + __popc(w & (bit - 1u))];
-        return (w & bit) ? id : kNoAgent;
+    // Agent on bordered cell `cell` of this env (sparse map): the id at the
+    // occupied cell's rank.  The rank is read unconditionally (an empty
+    // cell's rank is at most the occupied-cell count, the spare entry) and
+    // the caller keeps the id of an occupied cell only.
+    // (Bit-field extracts take the low five bits of their offset and width.
+    // The word index and the rank are formed in assembly: the compiler would
+    // otherwise fold the shift into the index scaling as a shift and a mask,
+    // and distribute the rank's scaling over its two terms.)
+    auto probe_sparse = [&](uint32_t cell, uint32_t& id) -> bool {
+        uint32_t w, rank;
+        asm("v_lshrrev_b32 %0, 5, %1" : "=v"(w) : "v"(cell));
+        const uint2 ow = s_occ[w];
+        // rank: the occupied cells below this cell in its word (the field
+        // of width cell & 31 from bit 0) plus those before the word
+        asm("v_bcnt_u32_b32 %0, %1, %2" : "=v"(rank) : "v"(__builtin_amdgcn_ubfe(ow.x, 0u, cell)), "v"(ow.y));
+        id = s_ids[rank];
+        return __builtin_amdgcn_ubfe(ow.x, cell, 1u) != 0u;
     };
 
     // Window gather.  Lane l < 33 loads segment l = (row i, tile column j) of
@@ -1021,10 +1064,29 @@ __global__ __launch_bounds__(kTokThreads) void tokens_kernel(jl_mapfgpt_t b) {
     // window of two strips re-reads the second for its third)
     const uint32_t lane_seg3 = (uint32_t)g_i * 16u + (uint32_t)g_j * strip_bytes;
     const uint32_t lane_seg2 = (uint32_t)g_i * 16u + (uint32_t)(g_j < 1 ? g_j : 1) * strip_bytes;
-    auto seg_load = [&](uint32_t seg, uint32_t& fill) -> uint4 {
-        fill = 0u;
+    auto seg_load = [&](uint32_t seg) -> uint4 {
         const uint32_t off = (seg & ~15u) + ((seg & 1u) ? lane_seg3 : lane_seg2);
         return *reinterpret_cast<const uint4*>(env_tiles + off);
+    };
+
+    // One agent-section token from template half w of a slot's agent: a
+    // coordinate relative to the ego, clip(w - e, -20, 20) + 20 with e = ex,
+    // or ey on lanes of a y field, computed as clamp(w + (20 - ex) + (ysel &
+    // (ex - ey)), 0, 40); a copied value's token from its code.
+    auto agent_token = [&](uint32_t o, uint32_t toff, bool coord, int ysel, int x20, int dxy, int cbase,
+                           uint32_t cstep) -> int {
+        const uint32_t w = *reinterpret_cast<const uint16_t*>(smem + (__umul24(o, (uint32_t)kTmplBytes) + toff));
+        const int c = (int)w + x20 + (ysel & dxy);
+        const int ct = c < 0 ? 0 : (c > 2 * kCostLimit ? 2 * kCostLimit : c);
+        const int kt = (int)w + cbase + (w >= cstep ? 1 : 0);
+        return coord ? ct : kt;
+    };
+    // Cost token of a window value through the LDS table: index clamp(d - c +
+    // 21, 0, 42) (42 below -20, 43 above +20) or 43 for an unreachable cell.
+    auto cost_token_lut = [&](uint32_t v, int c_minus_21) {
+        const int t = (int)(v & fmask) - c_minus_21;
+        const int i = t < 0 ? 0 : (t > 2 * kCostLimit + 2 ? 2 * kCostLimit + 2 : t);
+        return s_lut[v == kUnreachable ? kLutUnreachable : i];
     };
 
     // One ego's row: tokens into my_row, then the 16-byte store.
@@ -1035,70 +1097,78 @@ __global__ __launch_bounds__(kTokThreads) void tokens_kernel(jl_mapfgpt_t b) {
             const int ex = (int)(pos & 0xFFFFu), ey = (int)(pos >> 16);
             // region row = dx + 5, column = dy + 5 + ((ey + 3) & 7) (see seg_load)
             const uint16_t* win = win_base + (rec.w >> 24);
-            const uint32_t center = field_distance(win[kRadius * kRegionCols + kRadius], fmask);
-            const uint32_t v0 = win[win0];  // raw tiled values: cost_token_flat strips the marks
+            const uint32_t craw = win[kRadius * kRegionCols + kRadius];
+            const uint32_t center = field_distance((uint32_t)__builtin_amdgcn_readfirstlane((int)craw), fmask);
+            const uint32_t v0 = win[win0];  // raw tiled values: the table index strips the marks
             const uint32_t v1 = win[win1];
             uint32_t id0, id1;
+            bool occ0, occ1;
             const uint32_t mcell = rec.w & 0xFFFFFFu;
             if (kDense) {
                 const uint32_t* mrow = s_map + mcell;
                 id0 = mrow[map0];
                 id1 = mrow[map1];
+                occ0 = id0 != kNoAgent;
+                occ1 = id1 != kNoAgent;
             } else {
-                id0 = agent_at_rank(mcell + (uint32_t)map0);
-                id1 = agent_at_rank(mcell + (uint32_t)map1);
+                occ0 = probe_sparse(mcell + (uint32_t)map0, id0);
+                occ1 = probe_sparse(mcell + (uint32_t)map1, id1);
             }
-            // candidates: (distance << 16 | id); an empty cell's key is all ones
+            // the centre's agent (an ego on the map stands there) is slot 0
+            const uint32_t centre_id = (uint32_t)__builtin_amdgcn_readlane((int)id0, kCentreCell);
+            // other candidates: (distance << 16 | id), ranked among themselves
             const uint32_t key0 = qd0 | id0, key1 = qd1 | id1;
-            const uint64_t m0 = __ballot(id0 != kNoAgent);
-            const uint64_t m1 = __ballot(id1 != kNoAgent) & kQ1Lanes;
-            int r0 = 0, r1 = 0;
-            for (uint64_t m = m0; m; m &= m - 1) {
-                const uint32_t k =
-                    (uint32_t)__builtin_amdgcn_readlane((int)key0, __ffsll((unsigned long long)m) - 1);
+            const uint64_t m0 = __ballot(occ0) & kProbe0;
+            const uint64_t m1 = __ballot(occ1) & kProbe1;
+            int r0 = 1, r1 = 1;
+            for (uint64_t m = m0; m;) {
+                const int l = __builtin_ctzll(m);
+                m &= ~(1ull << l);
+                const uint32_t k = (uint32_t)__builtin_amdgcn_readlane((int)key0, l);
                 r0 += k < key0;
                 r1 += k < key1;
             }
-            for (uint64_t m = m1; m; m &= m - 1) {
-                const uint32_t k =
-                    (uint32_t)__builtin_amdgcn_readlane((int)key1, __ffsll((unsigned long long)m) - 1);
+            for (uint64_t m = m1; m;) {
+                const int l = __builtin_ctzll(m);
+                m &= ~(1ull << l);
+                const uint32_t k = (uint32_t)__builtin_amdgcn_readlane((int)key1, l);
                 r0 += k < key0;
                 r1 += k < key1;
             }
-            const int count = __popcll(m0) + __popcll(m1);
-            const int nsel = count < kVisible ? count : kVisible;
+            const int others = __popcll(m0) + __popcll(m1);
+            const int nsel = others + 1 < kVisible ? others + 1 : kVisible;
             // the selected ids move through the wave's slot array
-            if (id0 != kNoAgent && r0 < kVisible) my_slots[r0] = id0;
-            if (has_q1 && id1 != kNoAgent && r1 < kVisible) my_slots[r1] = id1;
+            if (occ0 && lane != kCentreCell && r0 < kVisible) my_slots[r0] = id0;
+            if (occ1 && own_q1 && r1 < kVisible) my_slots[r1] = id1;
+            my_slots[0] = centre_id;
             // cost tokens
-            const int cml = (int)center - kCostLimit;
-            my_row[q0] = cost_token_flat(v0, cml, fmask);
-            if (has_q1) my_row[q1] = cost_token_flat(v1, cml, fmask);
+            const int c21 = (int)center - (kCostLimit + 1);
+            my_row[q0] = cost_token_lut(v0, c21);
+            my_row[q1] = cost_token_lut(v1, c21);
             wave_sync();
-            // agent tokens; a slot at or past nsel is padding.  Only the
-            // slots in use now or for the previous ego are written: up to six
-            // (tokens 0..59 and padding at 60..63) in one pass of the lanes,
-            // up to twelve in two.
-            // both kinds read and the lane's kind selected (f is per lane):
-            // no divergent branch
-            auto agent_token = [&](int slot, int f) -> int {
-                const uint32_t o = my_slots[slot];
-                const int fc = f & 3, fk = f < 4 ? 0 : f - 4;
-                const int v = (int)s_rec16[o * (2 * kRecWords) + fc];
-                const int ct = coord_token(v - ((f & 1) ? ey : ex));
-                const int kt = kDense ? s_copy_tok[o * kCopyTokens + fk]
-                                      : copy_token(s_copy[o * kCopyTokens + fk], fk);
-                const int t = f < 4 ? ct : kt;
-                return slot < nsel ? t : kTokPad;
-            };
-            const int used = nsel > prev_nsel ? nsel : prev_nsel;
-            prev_nsel = nsel;
-            my_row[kCostTokens + lane] = agent_token(a_slot0, a_f0);
-            if (used * kAgentTokens > kWave) {
-                my_row[kCostTokens + kWave + lane] = agent_token(a_slot1, a_f1);
-                if (used * kAgentTokens > 2 * kWave && has_t2)
-                    my_row[kCostTokens + 2 * kWave + lane] = agent_token(a_slot2, a_f2);
+            // agent section: slots in use now or for the previous ego; a
+            // slot at or past nsel is padding.  Up to six slots (tokens
+            // 0..59, padding at 60..63) take one pass of the lanes.
+            const int span = (nsel > prev_n ? nsel : prev_n) * kAgentTokens;
+            const int live = nsel * kAgentTokens;
+            const int x20 = kCostLimit - ex, dxy = ex - ey;
+            {
+                const uint32_t o = my_slots[a_slot0];
+                const int t = agent_token(o, toff0, coord0, ysel0, x20, dxy, cbase0, cstep0);
+                my_row[kCostTokens + lane] = lane < live ? t : kTokPad;
             }
+            if (span > kWave) {
+                const uint32_t o = my_slots[a_slot1];
+                const int t = agent_token(o, toff1, coord1, ysel1, x20, dxy, cbase1, cstep1);
+                my_row[kCostTokens + kWave + lane] = lane + kWave < live ? t : kTokPad;
+                if (span > 2 * kWave) {
+                    const uint32_t o2 = my_slots[kVisible - 1];
+                    const int t2 = agent_token(o2, toff2, false, 0, 0, 0, cbase2, cstep2);
+                    *(lane < 2 ? my_row + kCostTokens + 2 * kWave + lane : row_sink) =
+                        nsel == kVisible ? t2 : kTokPad;
+                }
+            }
+            prev_n = nsel;
             wave_sync();
             out = reinterpret_cast<const v4i*>(my_row)[lane];
             wave_sync();  // row and slot reads done before the next ego's writes
@@ -1120,18 +1190,23 @@ __global__ __launch_bounds__(kTokThreads) void tokens_kernel(jl_mapfgpt_t b) {
     const uint16_t* win_b = reinterpret_cast<const uint16_t*>(my_win + kSegPerEgo);
     auto ego_a = [&](int p) { return e_begin + 2 * p; };
     auto ego_b = [&](int p) { return (e_begin + 2 * p + 1) < e_end ? e_begin + 2 * p + 1 : e_begin + 2 * p; };
-    // an ego's record, wavefront-uniform (the goal word is not needed here)
+    // An ego's record, wavefront-uniform: its position word; its window
+    // segment offset; its cell in the bordered map | the window's first
+    // column inside its first strip << 24 (used for an ego on the map only).
     auto record = [&](int e) {
-        const uint4 r = *reinterpret_cast<const uint4*>(s_rec + e * kRecWords);
-        return make_uint4((uint32_t)__builtin_amdgcn_readfirstlane((int)r.x), 0u,
-                          (uint32_t)__builtin_amdgcn_readfirstlane((int)r.z),
-                          (uint32_t)__builtin_amdgcn_readfirstlane((int)r.w));
+        const uint32_t pos = (uint32_t)__builtin_amdgcn_readfirstlane((int)s_tmpl[e * kTmplWords]);
+        const uint32_t seg = (uint32_t)__builtin_amdgcn_readfirstlane((int)s_seg[e]);
+        const uint32_t ex = pos & 0xFFFFu, ey = pos >> 16;
+        const uint32_t mcell = (ex + kRadius) * (uint32_t)MH + ey + kRadius;
+        return make_uint4(pos, 0u, seg, mcell | (((ey + 3) & 7) << 24));
     };
     uint4 ga, gb;
-    uint32_t fa, fb;
+    uint4 rec_a, rec_b;  // records of the pair whose windows are staged
     auto stage = [&](int p) {
-        ga = seg_load(record(ego_a(p)).z, fa);
-        gb = seg_load(record(ego_b(p)).z, fb);
+        rec_a = record(ego_a(p));
+        rec_b = record(ego_b(p));
+        ga = seg_load(rec_a.z);
+        gb = seg_load(rec_b.z);
     };
     auto commit = [&]() {
         // every use of the loaded values stays here, so that the loads stay
@@ -1139,22 +1214,37 @@ __global__ __launch_bounds__(kTokThreads) void tokens_kernel(jl_mapfgpt_t b) {
         asm volatile("" : "+v"(ga.x), "+v"(ga.y), "+v"(ga.z), "+v"(ga.w));
         asm volatile("" : "+v"(gb.x), "+v"(gb.y), "+v"(gb.z), "+v"(gb.w));
         if (lane < kSegPerEgo) {
-            my_win[lane] = make_uint4(ga.x | fa, ga.y | fa, ga.z | fa, ga.w | fa);
-            my_win[kSegPerEgo + lane] = make_uint4(gb.x | fb, gb.y | fb, gb.z | fb, gb.w | fb);
+            my_win[lane] = ga;
+            my_win[kSegPerEgo + lane] = gb;
         }
         wave_sync();
     };
     stage(wave);
     commit();
-    for (int p = wave; p < npairs; p += kTokWaves) {
-        const int pn = p + kTokWaves;
-        const uint4 rec_a = record(ego_a(p)), rec_b = record(ego_b(p));
-        // always staged (no branch around the loads, which would make the
-        // compiler wait for them early); after the last pair it repeats this one
-        stage(pn < npairs ? pn : p);
-        produce(rec_a, ego_a(p), win_a);
-        produce(rec_b, ego_b(p), win_b);
-        commit();
+    // The hardware issues the oldest wavefront first, which lets the first
+    // workgroup of a CU race ahead and leaves the last one alone at the end;
+    // wavefronts further along yield instead: priority 3 for the first
+    // quarter of this wavefront's pairs, 2, 1, then 0 for the last.
+    const int iters = (npairs - wave + kTokWaves - 1) / kTokWaves;
+    int p = wave, it = 0;
+    for (int quarter = 0; quarter < 4; ++quarter) {
+        switch (quarter) {
+            case 0: __builtin_amdgcn_s_setprio(3); break;
+            case 1: __builtin_amdgcn_s_setprio(2); break;
+            case 2: __builtin_amdgcn_s_setprio(1); break;
+            default: __builtin_amdgcn_s_setprio(0); break;
+        }
+        const int it_end = ((quarter + 1) * iters + 3) / 4;  // the first pair of the next quarter
+        for (; it < it_end; ++it, p += kTokWaves) {
+            const uint4 cur_a = rec_a, cur_b = rec_b;
+            const int pn = p + kTokWaves;
+            // always staged (no branch around the loads, which would make the
+            // compiler wait for them early); after the last pair it repeats this one
+            stage(pn < npairs ? pn : p);
+            produce(cur_a, ego_a(p), win_a);
+            produce(cur_b, ego_b(p), win_b);
+            commit();
+        }
     }
 }
 
@@ -1196,16 +1286,6 @@ constexpr int kTmplWords = 10;  // slot template: x, y, goal x, goal y, 5 histor
 // LDS the BFS fields of a refresh may overlay: at least this much, so that
 // four 64x64 fields refresh at once in each workgroup
 constexpr size_t kBuildFieldRoom = 32768;
-constexpr int kCentreCell = kRadius * kDiam + kRadius;  // 60: the ego's own cell
-// Cost-token table: entry i in [0, 42] is the token of d - c = i - 21 (42
-// below -20, 0..40 between, 43 above +20); entry 43 is an unreachable cell's.
-constexpr int kLutEntries = 2 * kCostLimit + 4;
-constexpr int kLutUnreachable = 2 * kCostLimit + 3;
-__device__ __forceinline__ int cost_lut_entry(int i) {
-    return i == kLutUnreachable ? kTokUnreachable
-                                : (i == 0 ? kTokNegClip : (i > 2 * kCostLimit + 1 ? kTokPosClip : i - 1));
-}
-static_assert(kCentreCell < kWave, "the centre is a first-cell probe");
 // Visible-agent keys of the single-launch build, 16 bits: (Manhattan
 // distance << 10) | id, below 2^15 (distance <= 10, id < 1024), so a 16-bit
 // difference of two keys is negative exactly when the first is smaller.  The
@@ -1281,17 +1361,6 @@ __device__ __forceinline__ uint32_t map16_min(uint16_t* map, uint32_t cell, uint
         if (seen == cur) return held;
         cur = seen;
     }
-}
-
-// Lanes of an agent-section pass whose token t = base + lane is a
-// coordinate field (t % 10 < 4), and of those the y fields (odd).
-__host__ __device__ constexpr uint64_t coord_lanes(int base, bool y_only) {
-    uint64_t m = 0;
-    for (int l = 0; l < kWave; ++l) {
-        const int f = (base + l) % kAgentTokens;
-        if (f < 4 && (!y_only || (f & 1))) m |= 1ull << l;
-    }
-    return m;
 }
 
 template <int H, bool kRows, int R, int kThreads>

@@ -444,6 +444,56 @@ def test_sparse_cell_map_with_shared_cells_matches_oracle(oracle, W, H, A):
         assert ob.diagnostics[2] >= 5, it  # the shared cells were counted
 
 
+@pytest.mark.parametrize("W,H,A,block", [(128, 96, 1100, True), (256, 128, 1300, False)])
+def test_token_pass_beyond_1024_agents_matches_oracle(oracle, W, H, A, block):
+    """More than 1024 agents (three workgroups per env of the token pass, ids
+    past ten bits in the visible-agent keys) on a dense cell -> agent map
+    (128 x 96, the agents on a block of consecutive cells, so most windows
+    hold more than 13 of them) and on a sparse one (256 x 128, random
+    cells), with a shared cell and an agent off the map: tokens and
+    diagnostics equal the oracle's over two builds."""
+    from iclr_2027_jointoom_amd import profile
+
+    rng = np.random.default_rng(A + W)
+    E = 2
+    grids = (rng.random((E, W, H)) < 0.1).astype(np.int32)
+    ext = profile(W, H)
+    b = ext.MapfGPTObservationBuilder(torch.from_numpy(grids).cuda(), A)
+    assert not b.single_launch
+    ob = oracle.OracleMapfGPT(grids, A)
+    goals = None
+    for it in range(2):
+        rows = np.zeros((E * A, 13), np.uint16)
+        rows[:, 0] = np.repeat(np.arange(E), A)
+        rows[:, 1] = np.tile(np.arange(A), E)
+        for e in range(E):
+            # dense case: a block of consecutive cells (whole map rows), so
+            # windows there hold up to 121 agents; else distinct random cells
+            if block:
+                cells = rng.integers(0, W * H - A) + np.arange(A)
+            else:
+                cells = rng.permutation(W * H)[:A]
+            rows[e * A:(e + 1) * A, 2] = cells // H
+            rows[e * A:(e + 1) * A, 3] = cells % H
+        if goals is None:
+            goals = np.stack([rows[:, 2][::-1], rows[:, 3][::-1]], -1).copy()
+        rows[:, 4:6] = goals
+        rows[:, 6] = rng.integers(0, 5, E * A)
+        rows[:, 7] = 1 if it == 0 else 0
+        rows[:, 8:13] = rng.integers(0, 6, (E * A, 5))
+        rows[3, 2:4] = rows[1030, 2:4]        # two agents on one cell
+        rows[A + 1050, 2] = W + 1             # position off the map
+        t = torch.from_numpy(rows.astype(np.int16)).cuda()
+        b.build_tokens(t)
+        ob.build_rows(rows)
+        torch.cuda.synchronize()
+        assert np.array_equal(b.tokens.cpu().numpy(), ob.tokens), it
+        assert b.diagnostics.cpu().tolist() == ob.diagnostics.tolist(), it
+    if block:
+        # the visible-agent block is full for most egos
+        assert (b.tokens[:, 121 + 12 * 10].cpu().numpy() != 66).mean() > 0.5
+
+
 def test_raw_row_history_values_outside_action_range(oracle):
     """The reference emits 45 + value for any uint16 history value of a raw row."""
     grids, rows = _parity_fixture()
