@@ -59,6 +59,7 @@ PEAK_HBM_BPS = 8.0e12
 TRAFFIC_FILE = ROOT / "profiles" / "build_kernel_pmc_1024x128_64.txt"
 
 MAGAT_TRAFFIC_FILE = ROOT / "profiles" / "magat_nodes_pmc_512x256_64.txt"
+C5_TRAFFIC_FILE = ROOT / "profiles" / "tokens_kernel_pmc_256x1024_256.txt"
 
 # Algorithmic bytes per agent: the compulsory reads and writes of each operation.
 B_TOKEN_KERNEL = 8 + 10 + 242 + 1024 + 1  # pos+goal, history, 11x11 u16 window, tokens, mask
@@ -491,8 +492,10 @@ def run_gpu(args) -> dict:
             "peak": PEAK_HBM_BPS / 1e9,
             "unit": "GB/s",
             "frac": achieved / PEAK_HBM_BPS,
-            # the committed PMC summary is for the default workload only
-            "traffic": measured_traffic() if (E, A, W, args.map_kind) == (1024, 128, 64, "iid") else None,
+            # committed PMC summaries: the default workload and C5
+            "traffic": (measured_traffic() if (E, A, W, args.map_kind) == (1024, 128, 64, "iid")
+                        else measured_traffic(C5_TRAFFIC_FILE) if (E, A, W, args.map_kind) == (256, 1024, 256, "warehouse")
+                        else None),
             "bytes_per_launch": tok_bytes,
             "avg_launch_us": tok_avg_s * 1e6,
             "timed_launches": len(tok_ms),  # HIP events on every EVENT_EVERY-th timed step
