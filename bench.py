@@ -1302,7 +1302,8 @@ def main() -> int:
                         "every goal fresh (all BFS fields, maze maps by default)")
     p.add_argument("--map-kind", choices=("iid", "maze", "warehouse"), default="iid")
     p.add_argument("--ring-workers", type=int, default=8, help="record producer processes (ring workload)")
-    p.add_argument("--ring-slots", type=int, default=4, help="stage slots of the ring (ring workload)")
+    p.add_argument("--ring-slots", type=int, default=4,
+                   help="stage slots of the ring (ring workload; 16 unless given)")
     p.add_argument("--ring-compact-only", action="store_true",
                    help="skip the row-format comparison run (ring workload)")
     p.add_argument("--ct-horizon", type=int, default=512, help="episode horizon (costtracer workload)")
@@ -1313,10 +1314,12 @@ def main() -> int:
                    help="resident workload: standard MAPF, or lifelong with deterministic candidate goals")
     args = p.parse_args()
     if args.workload == "ring":
+        # 16 stage slots (109 MB of HBM ring, 38 MB of host ring at C5): the
+        # producers stay far enough ahead that the ring never runs dry
         for flag, name, value in (("--envs", "envs", 256), ("--agents", "agents", 1024),
                                   ("--map", "map", 256), ("--map-kind", "map_kind", "warehouse"),
                                   ("--steps", "steps", 40), ("--warmup", "warmup", 4),
-                                  ("--cpu-steps", "cpu_steps", 3)):
+                                  ("--cpu-steps", "cpu_steps", 3), ("--ring-slots", "ring_slots", 16)):
             if flag not in sys.argv:
                 setattr(args, name, value)
     if args.policy is None:
