@@ -469,22 +469,15 @@ __global__ __launch_bounds__(kStepThreads) void step_kernel(jl_sim_t s) {
         }
     }
     __syncthreads();
-    if (by_candidates) {
-        // Canonical agent order over per-agent candidate lists
-        // (128_agents_map_step.cu:303-330 of rebuttal/online-rl/native/src/
-        // cuda_backend; its CPU twin assign_goals, rebuttal/online-il/
-        // tasks.py:51-65): agent i on its goal takes the first cell of its
-        // env's list, from candidates[i][cursor % length] on, that is neither
-        // its own cell nor the goal of an agent off its goal or of an agent
-        // before it.  The reached agents are listed in id order, their first
-        // two candidates fetched in parallel, and one thread settles them in
-        // order against the goal bitmap.
-        uint32_t* life = reinterpret_cast<uint32_t*>(smem + L.life_off);
-        uint32_t* r_list = life;
-        int32_t* r_start = reinterpret_cast<int32_t*>(life + A);
-        int32_t* r_cursor = reinterpret_cast<int32_t*>(life + 2 * A);
-        uint32_t* r_pref = life + 3 * A;  // [2A]: candidates, then the chosen cell
-        uint32_t* r_meta = life + 5 * A;  // [0] reached count, [1 + c] count of chunk c
+    // The agents on their goal, listed in id order (ballots per chunk of 64
+    // agents and the chunks' counts); both rules settle them in that order.
+    uint32_t* life = reinterpret_cast<uint32_t*>(smem + L.life_off);
+    uint32_t* r_list = life;
+    int32_t* r_start = reinterpret_cast<int32_t*>(life + A);
+    int32_t* r_cursor = reinterpret_cast<int32_t*>(life + 2 * A);
+    uint32_t* r_pref = life + 3 * A;  // [2A]: first two cells, then the chosen cell
+    uint32_t* r_meta = life + 5 * A;  // [0] reached count, [1 + c] count of chunk c
+    {
         const int lane = tid & (kWave - 1);
         const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
         const int nwaves = nt / kWave;
@@ -505,7 +498,18 @@ __global__ __launch_bounds__(kStepThreads) void step_kernel(jl_sim_t s) {
             if (c == nchunks - 1 && lane == 0) r_meta[0] = before + (uint32_t)__popcll(m);
         }
         __syncthreads();
-        const int nr = (int)r_meta[0];
+    }
+    const int nr = (int)r_meta[0];
+    if (by_candidates) {
+        // Canonical agent order over per-agent candidate lists
+        // (128_agents_map_step.cu:303-330 of rebuttal/online-rl/native/src/
+        // cuda_backend; its CPU twin assign_goals, rebuttal/online-il/
+        // tasks.py:51-65): agent i on its goal takes the first cell of its
+        // env's list, from candidates[i][cursor % length] on, that is neither
+        // its own cell nor the goal of an agent off its goal or of an agent
+        // before it.  The reached agents' first two candidates are fetched in
+        // parallel, and one thread settles them in order against the goal
+        // bitmap.
         const int count = cand_count;
         const int clen = s.candidate_length;
         const uint16_t* cells = s.candidate_cells + (size_t)env * s.candidate_stride * 2;
@@ -562,31 +566,59 @@ __global__ __launch_bounds__(kStepThreads) void step_kernel(jl_sim_t s) {
             s.goal_changed[g] = 1;
             s.goal_cursors[g] = r_cursor[j] + 1;
         }
-    } else if (tid == 0) {
+    } else {
+        // Generator draws (128_agents_map_step.cu:265-343): agent i on its
+        // goal draws a start index into the env's free-cell list from its own
+        // generator (one draw per reached agent) and takes the first cell from
+        // there on, wrapping, that is not the goal of an agent off its goal or
+        // of an agent before it.  Each reached agent draws and fetches its
+        // first two cells in parallel; one thread settles them in id order
+        // against the goal bitmap, reading further cells of the list only when
+        // both are taken.
         const int count = s.env_counts[env];
         const int offset = s.env_offsets[env];
-        for (int a = 0; a < A; ++a) {
-            const size_t g = base + a;
-            if (s_cur[a] != s_goal[a]) continue;
-            if (count <= 0) continue;
-            uint64_t st = s.rng_state[g];
-            int k = (int)((rng_next(&st) >> 32) % (uint64_t)count);
-            for (int attempt = 0; attempt < count; ++attempt) {
-                const uint32_t packed = s.free_cells[offset + k];
-                const uint32_t x = packed >> 16, y = packed & 0xFFFFu;
-                const uint32_t cell = x * H + y;
-                if (!((goal_bits[cell >> 5] >> (cell & 31)) & 1u)) {
-                    goal_bits[cell >> 5] |= 1u << (cell & 31);
-                    s_goal[a] = x | (y << 16);
-                    s.goal_x[g] = (uint16_t)x;
-                    s.goal_y[g] = (uint16_t)y;
-                    s.goal_changed[g] = 1;
-                    s_flag[a] |= 0x8000;  // goal changed this step
-                    break;
-                }
-                if (++k >= count) k = 0;
+        if (count > 0) {
+            for (int j = tid; j < nr; j += nt) {
+                const size_t g = base + r_list[j];
+                uint64_t st = s.rng_state[g];
+                const int k = (int)((rng_next(&st) >> 32) % (uint64_t)count);
+                s.rng_state[g] = st;
+                r_start[j] = k;
+                r_pref[2 * j] = s.free_cells[offset + k];
+                r_pref[2 * j + 1] = s.free_cells[offset + (k + 1 < count ? k + 1 : 0)];
             }
-            s.rng_state[g] = st;
+        }
+        __syncthreads();
+        if (tid == 0 && count > 0) {
+            for (int j = 0; j < nr; ++j) {
+                int k = r_start[j];
+                uint32_t chosen = kEmpty;
+                for (int attempt = 0; attempt < count; ++attempt) {
+                    // free-cell list entries are x << 16 | y
+                    const uint32_t packed = attempt < 2 ? r_pref[2 * j + attempt] : s.free_cells[offset + k];
+                    const uint32_t x = packed >> 16, y = packed & 0xFFFFu;
+                    const uint32_t cell = x * H + y;
+                    if (!((goal_bits[cell >> 5] >> (cell & 31)) & 1u)) {
+                        goal_bits[cell >> 5] |= 1u << (cell & 31);
+                        chosen = x | (y << 16);
+                        break;
+                    }
+                    if (++k >= count) k = 0;
+                }
+                r_pref[2 * j] = chosen;
+            }
+        }
+        __syncthreads();
+        for (int j = tid; j < nr && count > 0; j += nt) {
+            const uint32_t c = r_pref[2 * j];
+            if (c == kEmpty) continue;
+            const int a = (int)r_list[j];
+            const size_t g = base + a;
+            s_goal[a] = c;
+            s_flag[a] |= 0x8000;  // goal changed this step
+            s.goal_x[g] = (uint16_t)(c & 0xFFFFu);
+            s.goal_y[g] = (uint16_t)(c >> 16);
+            s.goal_changed[g] = 1;
         }
     }
     __syncthreads();

@@ -183,6 +183,48 @@ def test_random_lifelong_rollouts_match_oracle(oracle, W, H, E, A, T, extent):
     assert changed >= E * len(range(0, A, 3))
 
 
+def test_random_lifelong_draws_past_held_goals_match_oracle(oracle):
+    """Seven agents in a 4 x 4 real extent of free cells: most cells of the
+    free-cell list are goals held by agents off their goal, so a draw often
+    finds its first two cells held and reads further cells of the list
+    (the settling thread's fallback).  Every agent starts on its goal, so all
+    draw at once, in id order, at the first step.  Cells, goals and
+    generator states equal the oracle's after each step."""
+    from iclr_2027_jointoom_amd import profile
+
+    W = H = 32
+    E, A, T = 3, 7, 60
+    grids = np.zeros((E, W, H), np.uint8)
+    extents = np.tile([4, 4], (E, 1)).astype(np.int32)
+    ext = profile(W, H)
+    seed = 777
+    sim = ext.GridWorldSimulator(torch.from_numpy(grids.astype(np.int32)).cuda(), A, 2, E * W * H, seed)
+    sim.set_real_map_extents(torch.from_numpy(extents).cuda())
+    sim.run_initialization()
+    osim = oracle.OracleSim(grids, A, task_mode=0, max_episode_steps=256)
+    osim.seed_rng(seed)
+    osim.lifelong_init(extents)
+    _compare_lifelong_goals(sim, osim, E * A, "init")
+    starts = osim.positions()
+    goals = starts.astype(np.int16)  # every agent on its goal
+    sim.load_state(torch.from_numpy(starts).cuda(), torch.from_numpy(goals).cuda(),
+                   torch.zeros((E, A), dtype=torch.uint8, device="cuda"), torch.zeros(E, dtype=torch.int32, device="cuda"))
+    osim.load_state(starts, goals)
+    rng = np.random.default_rng(5)
+    changed = 0
+    for t in range(T):
+        acts = rng.integers(0, 5, size=(E, A)).astype(np.uint8)
+        if t == 0:
+            acts[:] = 0
+        sim.update_actions(torch.from_numpy(acts).cuda())
+        sim.step_sim_only()
+        osim.step(acts)
+        compare_with_oracle(sim, osim, f"step {t}")
+        _compare_lifelong_goals(sim, osim, E * A, f"step {t}")
+        changed += int(osim.goal_changed.sum())
+    assert changed >= E * A
+
+
 def _compare_lifelong_goals(sim, osim, n, tag):
     torch.cuda.synchronize()
     for name, got, exp in (("cur_x", sim.cur_x, osim.cur_x.astype(np.int16)),
