@@ -444,6 +444,49 @@ def test_sparse_cell_map_with_shared_cells_matches_oracle(oracle, W, H, A):
         assert ob.diagnostics[2] >= 5, it  # the shared cells were counted
 
 
+@pytest.mark.parametrize("W,H", [(256, 256), (128, 128), (200, 96)])
+def test_token_pass_windows_at_corners_and_edges_match_oracle(oracle, W, H):
+    """Agents packed into the four corners and along the four edges of the
+    map, so that windows reach into the empty border of the cell -> agent
+    map (sparse beyond 16,384 cells, dense below) and the unreachable border
+    of the tiled fields on every side; goals in the opposite corners.  The
+    two-launch token pass equals the oracle over two builds."""
+    from iclr_2027_jointoom_amd import profile
+
+    E = 2
+    cells = []
+    for cx, cy in ((0, 0), (0, H - 1), (W - 1, 0), (W - 1, H - 1)):
+        for dx in range(4):
+            for dy in range(4):
+                cells.append((abs(cx - dx), abs(cy - dy)))
+    for k in range(6, W - 6, max(1, W // 9)):
+        cells += [(k, 0), (k, H - 1)]
+    for k in range(6, H - 6, max(1, H // 9)):
+        cells += [(0, k), (W - 1, k)]
+    cells = list(dict.fromkeys(cells))
+    A = len(cells)
+    grids = np.zeros((E, W, H), np.int32)
+    grids[:, W // 2, 1:H - 1] = 1  # a wall through the middle with gaps at both ends
+    ext = profile(W, H)
+    b = ext.MapfGPTObservationBuilder(torch.from_numpy(grids).cuda(), A)
+    assert not b.single_launch
+    ob = oracle.OracleMapfGPT(grids.astype(np.uint8), A)
+    pos = np.array(cells, np.int16)
+    goal = np.stack([W - 1 - pos[:, 0], H - 1 - pos[:, 1]], -1).astype(np.int16)
+    rng = np.random.default_rng(W + H)
+    for it in range(2):
+        p = np.stack([pos] * E)
+        if it:
+            p[1] = p[1][rng.permutation(A)]  # the same cells, other agents on them
+        g = np.stack([goal] * E)
+        t = [torch.from_numpy(np.ascontiguousarray(v)).cuda() for v in (p[..., 0], p[..., 1], g[..., 0], g[..., 1])]
+        b.build_tokens_from_state(*t)
+        ob.build_state(p[..., 0], p[..., 1], g[..., 0], g[..., 1])
+        torch.cuda.synchronize()
+        assert np.array_equal(b.tokens.cpu().numpy(), ob.tokens), (W, H, it)
+        assert b.diagnostics.cpu().tolist() == ob.diagnostics.tolist(), (W, H, it)
+
+
 @pytest.mark.parametrize("W,H,A,block", [(128, 96, 1100, True), (256, 128, 1300, False)])
 def test_token_pass_beyond_1024_agents_matches_oracle(oracle, W, H, A, block):
     """More than 1024 agents (three workgroups per env of the token pass, ids
