@@ -431,15 +431,16 @@ def run_gpu(args) -> dict:
             one_step(s)
     torch.cuda.synchronize()
     if args.graph and policy is not None:
-        raise SystemExit("--graph replays the loop with actions written into the graph's buffer: use --policy random")
+        raise SystemExit("--graph replays build, append, update and step as one graph, so the policy cannot "
+                         "run between the build and the append: use --policy random")
     if args.graph:
         from iclr_2027_jointoom_amd.graphs import MapfGPTResidentGraph
 
         graph = MapfGPTResidentGraph(sim, builder)
 
         def one_step(s):
-            graph.actions.copy_(actions[s])
-            graph.replay()
+            # the replay reads this step's pre-staged actions where they lie
+            graph.replay(actions[s])
     if timed is None:
         timed = prepare_timed_region()
     tok_events, start, end = timed
@@ -775,8 +776,7 @@ def run_gpu_magat(args) -> dict:
         if graph is None:
             one_step(args.warmup + i, node_events[i // EVENT_EVERY] if i % EVENT_EVERY == 0 else None)
         else:
-            graph.actions.copy_(actions[args.warmup + i])
-            graph.replay()
+            graph.replay(actions[args.warmup + i])
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     if graph is not None:

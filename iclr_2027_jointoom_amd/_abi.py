@@ -154,6 +154,7 @@ SIGNATURES = {
     "jl_encode_map": (c_int32, [c_void_p, c_void_p, c_int32, c_int32, c_int32, c_void_p]),
     "jl_step": (c_int32, [ctypes.POINTER(SimDesc), c_void_p]),
     "jl_update_actions": (c_int32, [ctypes.POINTER(SimDesc), c_void_p, c_void_p]),
+    "jl_graph_retarget_actions": (c_int32, [c_void_p, c_void_p, c_void_p, c_void_p, ctypes.POINTER(c_int32)]),
     "jl_goal_changed_scan": (c_int32, [ctypes.POINTER(SimDesc), c_void_p, c_void_p, c_void_p, c_void_p]),
     "jl_load_state": (
         c_int32,

@@ -164,4 +164,8 @@ __device__ __forceinline__ int cost_token(uint32_t v, uint32_t center) {
     return d + kCostLimit;
 }
 
+// Host address of the builder's history-append kernel (jl_mapfgpt.hip), by
+// which jl_graph_retarget_actions (jl_sim.hip) finds its nodes in a graph.
+const void* append_actions_kernel_address();
+
 }  // namespace jl

@@ -2113,6 +2113,9 @@ __global__ __launch_bounds__(256) void clear_scratch_kernel(int32_t* s) {
 static_assert(JL_BUILD_SCRATCH_WORDS % 4 == 0, "16-byte clearing");
 
 }  // namespace
+
+const void* append_actions_kernel_address() { return reinterpret_cast<const void*>(&append_actions_kernel); }
+
 }  // namespace jl
 
 using namespace jl;

@@ -13,6 +13,8 @@
 // atomicMax of (round << 16 | ~id), so no table reset is needed between
 // rounds: two barriers per round.  Rejections are never undone and the round
 // structure is the reference's, so positions are identical.
+#include <vector>
+
 #include "jl_common.h"
 
 namespace jl {
@@ -995,6 +997,59 @@ extern "C" int jl_update_actions(const jl_sim_t* s, const uint8_t* actions, jl_s
                            s->actions, actions, n);
     }
     return launch_status();
+}
+
+// The action-reading nodes of a captured graph: the history append (the
+// builder, actions at argument 1 of 2) and the action copy (update_actions,
+// source at argument 1 of 3).  Every node is checked before any is changed.
+extern "C" int jl_graph_retarget_actions(void* graph, void* graph_exec, const void* captured,
+                                         const void* actions, int32_t* n_nodes) {
+    if (!graph || !graph_exec || !captured || !actions) return JL_ERR_ARG;
+    size_t count = 0;
+    int rc = status(hipGraphGetNodes(static_cast<hipGraph_t>(graph), nullptr, &count));
+    if (rc) return rc;
+    std::vector<hipGraphNode_t> nodes(count);
+    if (count) {
+        rc = status(hipGraphGetNodes(static_cast<hipGraph_t>(graph), nodes.data(), &count));
+        if (rc) return rc;
+    }
+    const void* append = append_actions_kernel_address();
+    const void* copy_vec = reinterpret_cast<const void*>(&copy_actions_kernel<true>);
+    const void* copy_byte = reinterpret_cast<const void*>(&copy_actions_kernel<false>);
+    struct Hit {
+        hipGraphNode_t node;
+        hipKernelNodeParams params;
+        int nargs;
+    };
+    std::vector<Hit> hits;
+    for (hipGraphNode_t node : nodes) {
+        hipGraphNodeType type;
+        rc = status(hipGraphNodeGetType(node, &type));
+        if (rc) return rc;
+        if (type != hipGraphNodeTypeKernel) continue;
+        hipKernelNodeParams p;
+        rc = status(hipGraphKernelNodeGetParams(node, &p));
+        if (rc) return rc;
+        const int nargs = p.func == append ? 2 : ((p.func == copy_vec || p.func == copy_byte) ? 3 : 0);
+        if (!nargs) continue;
+        if (!p.kernelParams || !p.kernelParams[1]) return JL_ERR_ARG;
+        if (*static_cast<const void* const*>(p.kernelParams[1]) != captured) continue;
+        // the 16-byte copy stays the captured kernel: the new source must
+        // allow it
+        if (p.func == copy_vec && (reinterpret_cast<uintptr_t>(actions) & 15u)) return JL_ERR_ARG;
+        hits.push_back({node, p, nargs});
+    }
+    for (Hit& h : hits) {
+        void* args[3];
+        for (int k = 0; k < h.nargs; ++k) args[k] = h.params.kernelParams[k];
+        const void* moved = actions;
+        args[1] = &moved;
+        h.params.kernelParams = args;
+        rc = status(hipGraphExecKernelNodeSetParams(static_cast<hipGraphExec_t>(graph_exec), h.node, &h.params));
+        if (rc) return rc;
+    }
+    if (n_nodes) *n_nodes = (int32_t)hits.size();
+    return JL_OK;
 }
 
 extern "C" int jl_goal_changed_scan(const jl_sim_t* s, int64_t* prefix, int64_t* count,

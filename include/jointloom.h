@@ -131,6 +131,20 @@ int jl_goal_changed_scan(const jl_sim_t* sim, int64_t* prefix, int64_t* count,
  * GridWorldSimulator::update_actions, grid_world_simulator.cpp:678-688. */
 int jl_update_actions(const jl_sim_t* sim, const uint8_t* actions, jl_stream_t stream);
 
+/* Point the action-reading kernels of an instantiated HIP graph at another
+ * action buffer, without device work: every node of `graph` that is a
+ * history append (jl_mapfgpt_append_actions) or an action copy
+ * (jl_update_actions) reading `captured` reads `actions` in `graph_exec`
+ * from its next launch on; *n_nodes (may be null) receives how many.  The
+ * captured copy kernel stays: a 16-byte-word copy needs `actions` 16-byte
+ * aligned (JL_ERR_ARG otherwise, and then no node is changed).  No
+ * counterpart in the reference, which launches every step from the host:
+ * it serves graph replays of the resident loops (graphs.py), so that each
+ * replay reads that step's actions where they lie instead of copying them
+ * into the graph's buffer first. */
+int jl_graph_retarget_actions(void* graph, void* graph_exec, const void* captured,
+                              const void* actions, int32_t* n_nodes);
+
 /* Write loaded positions/goals (int16 [E, A, 2] each), arrival latches
  * (uint8 [E, A]) and step counts (int32 [E]) into the simulator: split
  * state, terminated/truncated, zero rewards and actions, occupancy, packed

@@ -41,16 +41,22 @@ def test_mapf_gpt_resident_graph_matches_eager():
     eager(sim_e, b_e, first)
     eager(sim_g, b_g, first)
     graph = MapfGPTResidentGraph(sim_g, b_g)
-    for it in range(6):
+    # pre-staged actions, one slice per replay (offsets into one allocation)
+    staged = torch.from_numpy(rng.integers(0, 5, (8, E, A), dtype=np.uint8)).cuda()
+    for it in range(8):
         if it == 3:
             # a changed goal: the captured build refreshes that field on the device
             for sim in (sim_e, sim_g):
                 sim.goal_x[1, 5] = int(starts[1, 7, 0])
                 sim.goal_y[1, 5] = int(starts[1, 7, 1])
-        acts = torch.from_numpy(rng.integers(0, 5, (E, A), dtype=np.uint8)).cuda()
+        acts = staged[it]
         eager(sim_e, b_e, acts)
-        graph.actions.copy_(acts)
-        graph.replay()
+        if it in (2, 5):
+            # the graph's own buffer again, after replays read other tensors
+            graph.actions.copy_(acts)
+            graph.replay()
+        else:
+            graph.replay(acts)
         torch.cuda.synchronize()
         for name in ("tokens", "histories", "active_mask", "state_packed", "diagnostics", "goal_cache"):
             assert torch.equal(getattr(b_e, name), getattr(b_g, name)), (it, name)
@@ -75,12 +81,15 @@ def test_magat_stateful_graph_matches_eager():
         _, _, fresh, _ = _setup(E, W, A, 8, density=0.3)
         MagatStatefulGraph(fresh)
     graph = MagatStatefulGraph(sim_g)
-    for it in range(5):
+    for it in range(6):
         acts = torch.from_numpy(rng.integers(0, 5, (E, A), dtype=np.uint8)).cuda()
         sim_e.update_actions(acts)
         sim_e.step_and_build_pyg()
-        graph.actions.copy_(acts)
-        graph.replay()
+        if it % 3 == 1:
+            graph.actions.copy_(acts)
+            graph.replay()
+        else:
+            graph.replay(acts)
         torch.cuda.synchronize()
         me, mg = sim_e.memory_tensors, sim_g.memory_tensors
         for name in ("pyg_x", "pyg_pos", "edge_counts", "pyg_edge_prefix", "pyg_num_edges",
@@ -90,3 +99,41 @@ def test_magat_stateful_graph_matches_eager():
         assert torch.equal(sim_e.pyg_edge_index, sim_g.pyg_edge_index), it
         assert torch.equal(sim_e.pyg_edge_attr, sim_g.pyg_edge_attr), it
         assert torch.equal(sim_e.energy_maps, sim_g.energy_maps), it
+
+
+def test_graph_replay_rejects_mismatched_actions_before_launching():
+    """replay(actions) checks the tensor before any node is retargeted or the
+    graph launched: the step counter and the simulator state stay put."""
+    from iclr_2027_jointoom_amd.graphs import MapfGPTResidentGraph
+
+    E, W, A = 2, 32, 16
+    ext, g, sim, _ = _setup(E, W, A, 5)
+    b = ext.MapfGPTObservationBuilder(g, A)
+    acts = torch.zeros((E, A), dtype=torch.uint8, device="cuda")
+    b.build_tokens_from_state(sim.cur_x, sim.cur_y, sim.goal_x, sim.goal_y)
+    b.append_actions(acts)
+    sim.update_actions(acts)
+    sim.step_sim_only()
+    graph = MapfGPTResidentGraph(sim, b)
+    torch.cuda.synchronize()
+    step, x = sim.current_step, sim.cur_x.clone()
+    bad = [
+        (acts.to(torch.int32), "uint8"),
+        (torch.zeros((E, A + 1), dtype=torch.uint8, device="cuda"), "shape"),
+        (torch.zeros((A, E), dtype=torch.uint8, device="cuda").t(), "contiguous"),
+        (acts.cpu(), "device"),
+    ]
+    for t, msg in bad:
+        with pytest.raises(ValueError, match=msg):
+            graph.replay(t)
+    torch.cuda.synchronize()
+    assert sim.current_step == step
+    assert torch.equal(sim.cur_x, x)
+    # a 16-byte-word copy was captured: a source off 16-byte alignment is
+    # refused by the library, and no node is changed
+    flat = torch.zeros(E * A + 1, dtype=torch.uint8, device="cuda")
+    with pytest.raises(RuntimeError, match="retarget"):
+        graph.replay(flat[1:].view(E, A))
+    graph.replay(acts)
+    torch.cuda.synchronize()
+    assert sim.current_step == step + 1
