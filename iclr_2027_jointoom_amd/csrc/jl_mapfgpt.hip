@@ -1064,14 +1064,13 @@ __global__ __launch_bounds__(kTokThreads) void tokens_kernel(jl_mapfgpt_t b) {
     // window of two strips re-reads the second for its third)
     const uint32_t lane_seg3 = (uint32_t)g_i * 16u + (uint32_t)g_j * strip_bytes;
     const uint32_t lane_seg2 = (uint32_t)g_i * 16u + (uint32_t)(g_j < 1 ? g_j : 1) * strip_bytes;
-    // Non-temporal: at C5 (256 envs x 1024 agents on 256x256 maps) a
-    // build's window lines are about 170 MB, and loading them as streaming
-    // data took the step 1.2 us shorter than plain loads (the unpack's plain
-    // loads of each agent's own cells still bring those lines in).
+    // Plain loads: they leave the agents' own-cell lines in the caches for
+    // the next build's unpack, which reads them first (non-temporal loads
+    // here took the token pass from 91.0 to 86.7 us at C5 and the unpack
+    // from 11 to 14 us, the step unchanged).
     auto seg_load = [&](uint32_t seg) -> uint4 {
         const uint32_t off = (seg & ~15u) + ((seg & 1u) ? lane_seg3 : lane_seg2);
-        const v4i q = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(env_tiles + off));
-        return make_uint4((uint32_t)q.x, (uint32_t)q.y, (uint32_t)q.z, (uint32_t)q.w);
+        return *reinterpret_cast<const uint4*>(env_tiles + off);
     };
 
     // One agent-section token from template half w of a slot's agent: a
