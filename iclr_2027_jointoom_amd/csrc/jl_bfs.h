@@ -34,6 +34,30 @@ __device__ __forceinline__ uint64_t from_lane_above(uint64_t v) {
     return ((uint64_t)hi << 32) | lo;
 }
 
+// One level of a row held in 64 bits: the new frontier (the cells of `avail`
+// that neighbour the frontier: `up` / `down` its rows of the lanes below
+// and above, `left` / `right` its own row shifted by one column) is returned
+// and removed from `avail`.  Per 32-bit half: a = up | right and
+// b = down | left (a DPP lane move folded into each OR), then gfx950's
+// three-input bit operation twice, (a | b) & avail (truth table 0xA8 with
+// a, b, avail as its first, second and third input) and avail & ~(a | b)
+// (0x02): four VALU instructions per half instead of the six of an OR3, an
+// AND and an XOR after the two ORs.
+__device__ __forceinline__ uint64_t level_step(uint64_t up, uint64_t down, uint64_t left, uint64_t right,
+                                               uint64_t& avail) {
+    const uint32_t a_lo = (uint32_t)up | (uint32_t)right, a_hi = (uint32_t)(up >> 32) | (uint32_t)(right >> 32);
+    const uint32_t b_lo = (uint32_t)down | (uint32_t)left, b_hi = (uint32_t)(down >> 32) | (uint32_t)(left >> 32);
+    const uint32_t v_lo = (uint32_t)avail, v_hi = (uint32_t)(avail >> 32);
+    // (the builtin returns a signed int: each half is taken as uint32_t
+    // before it is widened, so no sign bit reaches the high half)
+    const uint32_t n_lo = (uint32_t)__builtin_amdgcn_bitop3_b32(a_lo, b_lo, v_lo, 0xA8);
+    const uint32_t n_hi = (uint32_t)__builtin_amdgcn_bitop3_b32(a_hi, b_hi, v_hi, 0xA8);
+    const uint32_t r_lo = (uint32_t)__builtin_amdgcn_bitop3_b32(a_lo, b_lo, v_lo, 0x02);
+    const uint32_t r_hi = (uint32_t)__builtin_amdgcn_bitop3_b32(a_hi, b_hi, v_hi, 0x02);
+    avail = ((uint64_t)r_hi << 32) | r_lo;
+    return ((uint64_t)n_hi << 32) | n_lo;
+}
+
 // Value of a fixed lane, wavefront-uniform.
 __device__ __forceinline__ uint64_t lane_value(uint64_t v, int lane) {
     const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, lane);
@@ -89,13 +113,13 @@ __device__ int wave_bfs(const uint64_t (&fr)[R][RowWords<H>::HW], int gx, int gy
     constexpr int HW = RowWords<H>::HW;
     const int lane = threadIdx.x & (kWave - 1);
     uint64_t front[R][HW];
-    uint64_t vis[R][HW];
+    uint64_t avail[R][HW];  // free cells not reached yet
 #pragma unroll
     for (int r = 0; r < R; ++r) {
 #pragma unroll
         for (int k = 0; k < HW; ++k) {
             front[r][k] = 0;
-            vis[r][k] = 0;
+            avail[r][k] = fr[r][k];
         }
     }
     {
@@ -108,7 +132,7 @@ __device__ int wave_bfs(const uint64_t (&fr)[R][RowWords<H>::HW], int gx, int gy
             for (int k = 0; k < HW; ++k) {
                 if (lane == owner_lane && r == owner_r && k == (gy >> 6)) {
                     front[r][k] = bit;
-                    vis[r][k] = bit;
+                    avail[r][k] &= ~bit;
                 }
             }
         }
@@ -137,7 +161,7 @@ __device__ int wave_bfs(const uint64_t (&fr)[R][RowWords<H>::HW], int gx, int gy
                 uint64_t right = front[r][k] >> 1;
                 if (k > 0) left |= front[r][k - 1] >> 63;
                 if (k + 1 < HW) right |= front[r][k + 1] << 63;
-                const uint64_t n = (left | right | up | down) & fr[r][k] & ~vis[r][k];
+                const uint64_t n = level_step(up, down, left, right, avail[r][k]);
                 nf[r][k] = n;
                 any_new |= (n != 0);
             }
@@ -149,7 +173,6 @@ __device__ int wave_bfs(const uint64_t (&fr)[R][RowWords<H>::HW], int gx, int gy
             const int x = lane + kWave * r;
 #pragma unroll
             for (int k = 0; k < HW; ++k) {
-                vis[r][k] |= nf[r][k];
                 front[r][k] = nf[r][k];
                 uint64_t m = nf[r][k];
                 if (kCountOverflow) local += __popcll(m);
@@ -217,11 +240,10 @@ __device__ void wave_bfs_batched(const uint64_t (&fr)[RowWords<H>::HW], int gx, 
                 uint64_t right = front[k] >> 1;
                 if (k > 0) left |= front[k - 1] >> 63;
                 if (k + 1 < HW) right |= front[k + 1] << 63;
-                nf[k] = (left | right | up | down) & avail[k];
+                nf[k] = level_step(up, down, left, right, avail[k]);
             }
 #pragma unroll
             for (int k = 0; k < HW; ++k) {
-                avail[k] &= ~nf[k];
                 front[k] = nf[k];
                 bm[k] |= nf[k];
                 if (j & 1) p0[k] |= nf[k];
@@ -290,11 +312,7 @@ __device__ void wave_bfs_levels(uint64_t fr, int gx, int gy, uint64_t& vis, uint
         uint64_t s1 = 0, s3 = 0, s5 = 0, s7 = 0, s9 = 0, s11 = 0, s13 = 0, most = 0, last = 0;
 #pragma unroll
         for (int j = 0; j < 16; ++j) {
-            const uint64_t up = from_lane_below(front);
-            const uint64_t down = from_lane_above(front);
-            const uint64_t nf = ((front << 1) | (front >> 1) | up | down) & avail;
-            avail ^= nf;
-            front = nf;
+            front = level_step(from_lane_below(front), from_lane_above(front), front << 1, front >> 1, avail);
             switch (j + 1) {  // avail is now a[j + 1]
                 case 1: s1 = avail; break;
                 case 3: lowp[1] |= s1 ^ avail; s3 = avail; break;
@@ -504,11 +522,11 @@ __device__ int group_bfs_planes(const uint64_t (&fr)[RowWords<H>::HW], int gx, i
     uint64_t* s_edge = s_words;
     int* s_flag = reinterpret_cast<int*>(s_words + 2 * R * 2 * HW);
     int* s_count = s_flag + 2 * 2 * R;
-    uint64_t front[HW];
+    uint64_t front[HW], avail[HW];  // avail: free cells not reached yet
 #pragma unroll
     for (int k = 0; k < HW; ++k) {
         front[k] = 0;
-        vis[k] = 0;
+        avail[k] = fr[k];
 #pragma unroll
         for (int b = 0; b < kLevelPlanes; ++b) pl[b][k] = 0;
     }
@@ -517,10 +535,12 @@ __device__ int group_bfs_planes(const uint64_t (&fr)[RowWords<H>::HW], int gx, i
         for (int k = 0; k < HW; ++k) {
             if (k == (gy >> 6)) {
                 front[k] = 1ull << (gy & 63);
-                vis[k] = front[k];
+                avail[k] &= ~front[k];
             }
         }
     }
+#pragma unroll
+    for (int k = 0; k < HW; ++k) vis[k] = front[k];  // the start, obstacle or not
     auto publish = [&](int slot, const uint64_t (&f)[HW], int flag) {
         uint64_t* e = s_edge + (size_t)((slot * R + wave) * 2) * HW;
         if (lane == 0) {
@@ -554,7 +574,7 @@ __device__ int group_bfs_planes(const uint64_t (&fr)[RowWords<H>::HW], int gx, i
             uint64_t right = front[k] >> 1;
             if (k > 0) left |= front[k - 1] >> 63;
             if (k + 1 < HW) right |= front[k + 1] << 63;
-            const uint64_t n = (left | right | up | down) & fr[k] & ~vis[k];
+            const uint64_t n = level_step(up, down, left, right, avail[k]);
             nf[k] = n;
             any_new |= (n != 0);
             if (kCountOverflow) local += __popcll(n);
@@ -563,10 +583,7 @@ __device__ int group_bfs_planes(const uint64_t (&fr)[RowWords<H>::HW], int gx, i
         const bool big = kCountOverflow && __any(local > kBigRow);
         publish(wr, nf, (wave_new ? 1 : 0) | (big ? 2 : 0));
 #pragma unroll
-        for (int k = 0; k < HW; ++k) {
-            vis[k] |= nf[k];
-            front[k] = nf[k];
-        }
+        for (int k = 0; k < HW; ++k) front[k] = nf[k];
 #pragma unroll
         for (int b = 0; b < kLevelPlanes; ++b) {
             if ((level >> b) & 1) {
@@ -594,6 +611,8 @@ __device__ int group_bfs_planes(const uint64_t (&fr)[RowWords<H>::HW], int gx, i
         if (!(flags & 1)) break;
         top = level;
     }
+#pragma unroll
+    for (int k = 0; k < HW; ++k) vis[k] |= fr[k] & ~avail[k];
     return overflow;
 }
 
