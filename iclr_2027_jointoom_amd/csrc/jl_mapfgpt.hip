@@ -1986,10 +1986,14 @@ int launch_pass1(const jl_mapfgpt_t* b, const int16_t* rows, const int16_t* cx, 
 }
 
 // The whole build runs as one launch (build_kernel) on maps of at most
-// kMarkedCells cells when an env fits one workgroup and the builder has its
-// build scratch.
+// kMarkedCells cells whose rows have at most 64 columns (one 64-bit word per
+// row in the field refresh) when an env fits one workgroup and the builder
+// has its build scratch.  Narrower maps of longer rows (at most 42 rows of
+// 96-256 columns) take the two-launch build: the single launch's refresh of
+// rows of several words did not fit its registers.
 bool single_launch(const jl_mapfgpt_t* b) {
-    if (!b->build_scratch || !marked_fields(b->map_w, b->map_h) || b->n_agents > 1024) return false;
+    if (!b->build_scratch || !marked_fields(b->map_w, b->map_h) || b->map_h > 64 || b->n_agents > 1024)
+        return false;
     const int threads = build_threads(b->n_agents);
     return build_layout(b->n_agents, b->map_w, b->map_h, threads / kWave).total <= 160 * 1024;
 }
@@ -2003,7 +2007,9 @@ int launch_single(const jl_mapfgpt_t* b, const int16_t* rows, const int16_t* cx,
 #define JL_LAUNCH_BUILD(R, T)                                                                      \
     hipLaunchKernelGGL((build_kernel<H, kRows, R, T>), grid, dim3(T), lds, stream, *b, rows, cx, cy, \
                        gx, gy)
-    if (b->map_w <= 64) {
+    if constexpr (H > 64) {
+        return JL_ERR_PROFILE;  // single_launch() is false for these maps
+    } else if (b->map_w <= 64) {
         if (threads == 512) JL_LAUNCH_BUILD(1, 512); else JL_LAUNCH_BUILD(1, 1024);
     } else {
         // W > 64 with W * H <= kMarkedCells: H == 32 only

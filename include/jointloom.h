@@ -258,7 +258,8 @@ int jl_mapfgpt_build_state(const jl_mapfgpt_t* b, const int16_t* cur_x,
                            const int16_t* goal_y, jl_stream_t stream);
 
 /* 1 when a build of this builder runs as one launch (maps of at most
- * 4096 cells, an env of at most 1024 agents, build_scratch set): unpack,
+ * 4096 cells with rows of at most 64 columns (map_h <= 64), an env of at
+ * most 1024 agents, build_scratch set): unpack,
  * field refreshes and tokens of an env in one workgroup, also when captured
  * into a graph; 0 when it runs as two or three launches.  No
  * counterpart in the reference (a profiling query: the token_events pair
