@@ -26,7 +26,10 @@ def _bank(seed, episodes, E, W, A, density):
     return grids, np.stack(pos).astype(np.int16), np.stack(goal).astype(np.int16)
 
 
-@pytest.mark.parametrize("W,E,A,horizon,steps", [(32, 3, 24, 6, 15), (64, 2, 100, 5, 11)])
+# 32x32 and 64x64 fields carry greedy marks in their tiles (at most 4,096
+# cells); 128x128 ones hold plain distances and refresh through the
+# workgroup BFS of maps of more than 64 rows
+@pytest.mark.parametrize("W,E,A,horizon,steps", [(32, 3, 24, 6, 15), (64, 2, 100, 5, 11), (128, 2, 64, 5, 8)])
 def test_costtracer_loop_matches_oracle(oracle, W, E, A, horizon, steps):
     from iclr_2027_jointoom_amd import profile
     from oracle.costtracer import OracleCostTracer
