@@ -2,11 +2,12 @@
 //
 // nodes: one workgroup per (env, 64-agent slice).  The env's static and
 // occupancy bitmaps and its agents' positions and goals are staged in LDS,
-// the slice's 11 x 11 energy windows are requested (non-temporal 16-byte
-// loads) and, while they are in flight, the slice's neighbour counts are
-// taken and its edge total written; then one wavefront per agent assembles
-// the 676-float row in LDS (lane l owning patch cells l, l + 64, l + 128)
-// and stores it as 16-byte words in address order (the reference zero-fills
+// the slice's 11 x 11 energy windows are requested (16-byte loads) and,
+// while they are in flight, the slice's neighbour counts are taken and its
+// edge total written; then one wavefront per agent assembles the 676-float
+// row in LDS (lane l owning patch cells l, l + 64, l + 128) and stores it as
+// 16-byte words in address order, its whole 128-byte lines non-temporally
+// (the reference zero-fills
 // the row and rewrites it one float per thread, 128_agents_map_stateless_
 // step.cu:414-421, 438-478).  The clamped ctg value is one of 21 float
 // constants k/10 (the IEEE quotients), so no division is evaluated on the
@@ -28,6 +29,7 @@ constexpr int kNodeThreads = 256;
 
 typedef short jl_v2s __attribute__((ext_vector_type(2)));  // (x, y) as packed int16
 typedef unsigned int jl_v4u __attribute__((ext_vector_type(4)));
+typedef float jl_v4f __attribute__((ext_vector_type(4)));
 
 // (float)k / 10.0f rounded to nearest even, k = -10..10.
 __device__ __constant__ float kTenths[21] = {-1.0f, -0.9f, -0.8f, -0.7f, -0.6f, -0.5f, -0.4f,
@@ -202,10 +204,11 @@ __global__ __launch_bounds__(kNodeThreads) void nodes_kernel(jl_magat_t m) {
         ok_hi[it] = rok && c0 + 1 >= 0 && c0 + 1 < H / 16;
         const uint4* row4 =
             reinterpret_cast<const uint4*>(env_energy + (size_t)a * cells + (size_t)(rok ? x : 0) * H);
-        // read once per step: streamed past the caches the row stores fill
+        // plain loads: the rows' whole lines are stored non-temporally (below),
+        // so these lines stay cached for the next step's windows
         const jl_v4u* r4 = reinterpret_cast<const jl_v4u*>(row4);
-        const jl_v4u l4 = __builtin_nontemporal_load(r4 + (ok_lo[it] ? c0 : 0));
-        const jl_v4u h4 = __builtin_nontemporal_load(r4 + (ok_hi[it] ? c0 + 1 : 0));
+        const jl_v4u l4 = r4[ok_lo[it] ? c0 : 0];
+        const jl_v4u h4 = r4[ok_hi[it] ? c0 + 1 : 0];
         lo[it] = make_uint4(l4.x, l4.y, l4.z, l4.w);
         hi[it] = make_uint4(h4.x, h4.y, h4.z, h4.w);
         shift[it] = y0 - c0 * 16;  // 0..15: byte of column y0 in lo
@@ -328,12 +331,30 @@ __global__ __launch_bounds__(kNodeThreads) void nodes_kernel(jl_magat_t m) {
             my_row[3 * kPygArea + p] = pwin[k] ? (free_cell ? cv : 1.0f) : 0.0f;
         }
         wave_sync();
+        // The row's whole 128-byte lines leave non-temporally (nothing reads
+        // them again in this step, and out of the caches they leave the
+        // energy windows and the edge pass's data there: C4 step 134.9 ->
+        // 133.1 us); the partial lines at either end, which the neighbouring
+        // rows complete, go through the L2 to be merged there.
+        // (The two stores are written through different types: stores of one
+        // type in both branches were merged by the compiler into one plain
+        // store, dropping the non-temporal hint.)
         const float4* src = reinterpret_cast<const float4*>(my_row);
         float4* dst = reinterpret_cast<float4*>(row);
+        const uintptr_t row_begin = reinterpret_cast<uintptr_t>(row);
+        const uintptr_t row_end = row_begin + kPygFeatures * 4;
 #pragma unroll
         for (int k = 0; k < 3; ++k) {
             const int q = lane + kWave * k;
-            if (q < kPygFeatures / 4) dst[q] = src[q];
+            if (q < kPygFeatures / 4) {
+                const uintptr_t line = reinterpret_cast<uintptr_t>(dst + q) & ~(uintptr_t)127;
+                if (line >= row_begin && line + 128 <= row_end) {
+                    __builtin_nontemporal_store(*reinterpret_cast<const jl_v4f*>(src + q),
+                                                reinterpret_cast<jl_v4f*>(dst + q));
+                } else {
+                    dst[q] = src[q];
+                }
+            }
         }
         wave_sync();  // the row buffer is rewritten by the next agent
     }
