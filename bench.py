@@ -113,11 +113,23 @@ def cpu_baseline(args) -> dict:
 # invalidates the caches where it is recorded, which slowed the resident
 # loop by about 7 us per step with two events around every build.
 HIP_EVENT_DISABLE_SYSTEM_FENCE = 0x20000000
-# the timed loops bracket the hot kernel with events on every EVENT_EVERY-th
-# step only: each event is a packet of its own that the command processor
-# takes about 1.7 us to pass between the kernels, so a pair on every fourth
-# step cost the resident loop about 0.9 us per step
+# the timed loops bracket the hot kernel with events on one step in
+# EVENT_EVERY only: each event is a packet of its own that the command
+# processor takes about 1.7 us to pass between the kernels, so a pair on
+# every fourth step cost the resident loop about 0.9 us per step
 EVENT_EVERY = 10
+
+
+def event_slots(steps: int) -> dict:
+    """Timed steps that carry the event pair, each mapped to its slot: the
+    middle step of every block of EVENT_EVERY timed steps (the middle step of
+    the last, shorter block).  Not each block's first step: the region's
+    first step follows its opening synchronize and event (torch records a
+    default event, which writes back and invalidates the caches), and the
+    first builds after the warmup still run slower while the caches fill, so
+    samples at the blocks' starts lean toward those."""
+    n = (steps + EVENT_EVERY - 1) // EVENT_EVERY
+    return {b * EVENT_EVERY + min(EVENT_EVERY, steps - b * EVENT_EVERY) // 2: b for b in range(n)}
 
 
 class HipEvents:
@@ -403,10 +415,10 @@ def run_gpu(args) -> dict:
         diag = builder.diagnostics.cpu().tolist()
         if any(diag):
             raise RuntimeError(f"builder diagnostics non-zero after warmup: {diag}")
-        # every EVENT_EVERY-th timed step carries the event pair around its
-        # build: each event is a packet of its own that the command processor
-        # takes about 1.7 us to pass between the kernels
-        evs = [(hip.create(), hip.create()) for _ in range(0, args.steps, EVENT_EVERY)]
+        # one timed step in EVENT_EVERY carries the event pair around its
+        # build (event_slots): each event is a packet of its own that the
+        # command processor takes about 1.7 us to pass between the kernels
+        evs = [(hip.create(), hip.create()) for _ in event_slots(args.steps)]
         start = torch.cuda.Event(enable_timing=True)
         end = torch.cuda.Event(enable_timing=True)
         start.record()  # torch creates an event at its first record
@@ -444,13 +456,14 @@ def run_gpu(args) -> dict:
     if timed is None:
         timed = prepare_timed_region()
     tok_events, start, end = timed
+    slots = event_slots(args.steps)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     start.record()
     for i in range(args.steps):
         if graph is None:
-            if i % EVENT_EVERY == 0:
-                builder._desc.token_events[0], builder._desc.token_events[1] = tok_events[i // EVENT_EVERY]
+            if i in slots:
+                builder._desc.token_events[0], builder._desc.token_events[1] = tok_events[slots[i]]
             else:
                 builder._desc.token_events[0] = builder._desc.token_events[1] = None
         one_step(args.warmup + i)
@@ -499,7 +512,7 @@ def run_gpu(args) -> dict:
                         else None),
             "bytes_per_launch": tok_bytes,
             "avg_launch_us": tok_avg_s * 1e6,
-            "timed_launches": len(tok_ms),  # HIP events on every EVENT_EVERY-th timed step
+            "timed_launches": len(tok_ms),  # HIP events on one timed step in EVENT_EVERY (event_slots)
         },
         "first_build_ms": first_build_ms,
         "goals_reassigned": int(sim.goal_cursors.sum().item()) if args.task_mode == "lifelong" else None,
@@ -769,12 +782,13 @@ def run_gpu_magat(args) -> dict:
         graph = MagatStatefulGraph(sim)
     # all kernels run on torch's current stream, so events recorded there bracket the node pass
     hip = HipEvents()
-    node_events = [tuple(hip.event() for _ in range(3)) for _ in range(0, args.steps, EVENT_EVERY)]
+    slots = event_slots(args.steps)
+    node_events = [tuple(hip.event() for _ in range(3)) for _ in slots]
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(args.steps):
         if graph is None:
-            one_step(args.warmup + i, node_events[i // EVENT_EVERY] if i % EVENT_EVERY == 0 else None)
+            one_step(args.warmup + i, node_events[slots[i]] if i in slots else None)
         else:
             graph.replay(actions[args.warmup + i])
     torch.cuda.synchronize()
@@ -807,7 +821,7 @@ def run_gpu_magat(args) -> dict:
             "traffic": measured_traffic(MAGAT_TRAFFIC_FILE) if (E, A, W) == (512, 256, 64) else None,
             "bytes_per_launch": node_bytes,
             "avg_launch_us": node_s * 1e6,
-            "timed_launches": len(node_ms),  # HIP events on every EVENT_EVERY-th timed step
+            "timed_launches": len(node_ms),  # HIP events on one timed step in EVENT_EVERY (event_slots)
         },
         "edges_per_step": int(sim.pyg_num_edges.item()),
         "graph_us": float(np.mean(graph_ms)) * 1e3,
@@ -916,15 +930,16 @@ def run_gpu_ring(args) -> dict:
         out = {}
         for fmt, path in archives.items():
             builder = ext.MapfGPTObservationBuilder(g, A)
-            tok_events = [(hip.create(), hip.create()) for _ in range(0, args.steps, EVENT_EVERY)]
+            slots = event_slots(args.steps)
+            tok_events = [(hip.create(), hip.create()) for _ in slots]
 
             class _Build:
                 n = 0
 
                 def train_step(self, b, raw):
                     i = self.n - args.warmup
-                    if 0 <= i < args.steps and i % EVENT_EVERY == 0:
-                        b._desc.token_events[0], b._desc.token_events[1] = tok_events[i // EVENT_EVERY]
+                    if i in slots:
+                        b._desc.token_events[0], b._desc.token_events[1] = tok_events[slots[i]]
                     else:
                         b._desc.token_events[0] = b._desc.token_events[1] = None
                     b.build_tokens(raw)
@@ -1205,12 +1220,13 @@ def run_gpu_costtracer(args) -> dict:
     if any(builder.diagnostics.cpu().tolist()):
         raise RuntimeError(f"builder diagnostics non-zero: {builder.diagnostics.cpu().tolist()}")
     hip = HipEvents()
-    obs_events = [(hip.event(), hip.event()) for _ in range(0, args.steps, EVENT_EVERY)]
+    slots = event_slots(args.steps)
+    obs_events = [(hip.event(), hip.event()) for _ in slots]
     hits0 = int(cursor.sum().item())
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(args.steps):
-        one_step(args.warmup + i, obs_events[i // EVENT_EVERY] if i % EVENT_EVERY == 0 else None)
+        one_step(args.warmup + i, obs_events[slots[i]] if i in slots else None)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     obs_s = float(np.mean([a.elapsed_time(b) for a, b in obs_events])) / 1000.0
@@ -1229,7 +1245,7 @@ def run_gpu_costtracer(args) -> dict:
             "traffic": None,
             "bytes_per_launch": nbytes,
             "avg_launch_us": obs_s * 1e6,
-            "timed_launches": len(obs_events),  # HIP events on every EVENT_EVERY-th timed step
+            "timed_launches": len(obs_events),  # HIP events on one timed step in EVENT_EVERY (event_slots)
         },
         "goal_hits_in_timed_steps": int(cursor.sum().item()) - hits0,
         "resets": int(episodes.sum().item()),
