@@ -1,0 +1,84 @@
+"""Seeded random configurations across the accepted map profiles: a height
+that is any multiple of 32 up to 256, a width from 8 to 256, 1 to 1,100
+agents per env (at most a quarter of the cells), 1 to 3 envs, i.i.d. maps of
+density 0-0.35 or mazes.  Three steps of the resident loop (token build,
+history append, action copy, step) and then the stateless MAGAT build, each
+against the C oracle: tokens, histories, diagnostics, positions, packed
+rows, occupancy, cost_to_go, energy fields, node features and edges.  The
+configurations cover every build path (single launch, two launches with
+one to four row words per lane, the workgroup BFS) without naming them."""
+import numpy as np
+import pytest
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+
+def _config(seed):
+    rng = np.random.default_rng(1000 + seed)
+    H = 32 * int(rng.integers(1, 9))
+    W = int(rng.integers(8, 257))
+    kind = "maze" if rng.random() < 0.25 else "iid"
+    density = float(rng.uniform(0.0, 0.35))
+    A = int(rng.integers(1, max(2, min(1100, int(W * H * 0.25)))))
+    E = int(rng.integers(1, 4))
+    return W, H, kind, density, A, E
+
+
+@pytest.mark.parametrize("seed", range(24))
+def test_random_configuration_matches_oracle(oracle, seed):
+    from iclr_2027_jointoom_amd import profile
+    from iclr_2027_jointoom_amd.synthetic import make_batch, random_actions
+
+    W, H, kind, density, A, E = _config(seed)
+    tag = f"seed {seed}: {kind} {W}x{H} A{A} E{E} density {density:.2f}"
+    print(tag, flush=True)
+    grids, starts, goals = make_batch(seed, E, W, H, A, kind=kind, density=density)
+    ext = profile(W, H)
+    g = torch.from_numpy(grids.astype(np.int32)).cuda()
+    sim = ext.GridWorldSimulator(g, A, 0, E * W * H, 3, "standard_mapf", 64)
+    sim.load_state(torch.from_numpy(starts).cuda(), torch.from_numpy(goals).cuda(),
+                   torch.zeros((E, A), dtype=torch.uint8, device="cuda"), torch.zeros(E, dtype=torch.int32, device="cuda"))
+    builder = ext.MapfGPTObservationBuilder(g, A)
+    osim = oracle.OracleSim(grids, A, task_mode=1, max_episode_steps=64)
+    osim.load_state(starts, goals)
+    ob = oracle.OracleMapfGPT(grids, A)
+    acts = random_actions(np.random.default_rng(seed), 3, E, A)
+    for s in range(3):
+        builder.build_tokens_from_state(sim.cur_x, sim.cur_y, sim.goal_x, sim.goal_y)
+        ob.build_state(osim.cur_x.view(np.int16), osim.cur_y.view(np.int16), osim.goal_x.view(np.int16),
+                       osim.goal_y.view(np.int16))
+        a = torch.from_numpy(acts[s]).cuda()
+        builder.append_actions(a)
+        ob.append(acts[s])
+        sim.update_actions(a)
+        sim.step_sim_only()
+        osim.step(acts[s])
+        torch.cuda.synchronize()
+        t = f"{tag} step {s}"
+        assert np.array_equal(builder.tokens.cpu().numpy(), ob.tokens), t
+        assert np.array_equal(builder.histories.cpu().numpy().view(np.uint16), ob.histories), t
+        assert builder.diagnostics.cpu().tolist() == ob.diagnostics.tolist(), t
+        assert np.array_equal(torch.stack((sim.cur_x, sim.cur_y), -1).cpu().numpy(), osim.positions()), t
+        assert np.array_equal(sim.state_packed.cpu().numpy().view(np.uint16), osim.state_packed), t
+        assert np.array_equal(sim.grid_ocp.cpu().numpy().view(np.uint32), osim.grid_ocp), t
+    assert np.array_equal(builder.cost_to_go.cpu().numpy().view(np.uint16), ob.cost_to_go), tag
+
+    stateless = ext.StatelessGridWorldSimulator(g, A, 3)
+    rows = osim.state_packed.view(np.int16).copy()
+    rows_reset = rows.copy()
+    rows_reset[:, 7] = 1
+    stateless.update_energy_maps(torch.from_numpy(rows_reset).cuda(), len(rows_reset))
+    stateless.refresh_compact_state_from_raw_batch(torch.from_numpy(rows).cuda())
+    stateless.materialize_pyg_inputs()
+    m = oracle.OracleMagat(grids, A)
+    m.update_energy(rows_reset.view(np.uint16), len(rows_reset))
+    m.refresh(rows.view(np.uint16))
+    m.nodes()
+    m.edges()
+    torch.cuda.synchronize()
+    assert np.array_equal(stateless.energy_maps.cpu().numpy(), m.energy), tag
+    assert np.array_equal(stateless.pyg_x.cpu().numpy(), m.pyg_x), tag
+    ei, ea = m.valid_edges()
+    assert np.array_equal(stateless.pyg_edge_index.cpu().numpy(), ei), tag
+    assert np.array_equal(stateless.pyg_edge_attr.cpu().numpy(), ea), tag
