@@ -6,7 +6,9 @@ history append, action copy, step) and then the stateless MAGAT build, each
 against the C oracle: tokens, histories, diagnostics, positions, packed
 rows, occupancy, cost_to_go, energy fields, node features and edges.  The
 configurations cover every build path (single launch, two launches with
-one to four row words per lane, the workgroup BFS) without naming them."""
+one to four row words per lane, the workgroup BFS) without naming them.
+A second set runs candidate-list lifelong goals, so that builds refresh the
+fields of goals changed mid-rollout on those shapes."""
 import numpy as np
 import pytest
 
@@ -82,3 +84,72 @@ def test_random_configuration_matches_oracle(oracle, seed):
     ei, ea = m.valid_edges()
     assert np.array_equal(stateless.pyg_edge_index.cpu().numpy(), ei), tag
     assert np.array_equal(stateless.pyg_edge_attr.cpu().numpy(), ea), tag
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_random_lifelong_configuration_matches_oracle(oracle, seed):
+    """Candidate-list lifelong goals (a third of the agents start on their
+    goals) on seeded random shapes: each of six steps builds the tokens,
+    refreshing the fields of the goals changed by the step before, then
+    steps; tokens, diagnostics, positions, goals and cursors against the
+    oracle, cost_to_go at the end."""
+    from iclr_2027_jointoom_amd import profile
+    from iclr_2027_jointoom_amd.synthetic import make_batch
+
+    rng = np.random.default_rng(5000 + seed)
+    H = 32 * int(rng.integers(1, 9))
+    W = int(rng.integers(8, 257))
+    kind = "maze" if rng.random() < 0.25 else "iid"
+    density = float(rng.uniform(0.0, 0.35))
+    A = int(rng.integers(1, max(2, min(1100, int(W * H * 0.2)))))
+    E = int(rng.integers(1, 4))
+    tag = f"seed {seed}: lifelong {kind} {W}x{H} A{A} E{E} density {density:.2f}"
+    print(tag, flush=True)
+    grids, starts, goals = make_batch(seed, E, W, H, A, kind=kind, density=density)
+    r2 = np.random.default_rng(seed + 100)
+    cells_l = [np.argwhere(gr == 0).astype(np.int16) for gr in grids]
+    cells = np.full((E, max(len(c) for c in cells_l) + 3, 2), -1, np.int16)
+    for e, c in enumerate(cells_l):
+        cells[e, :len(c)] = r2.permutation(c)
+    counts = np.array([len(c) for c in cells_l], np.int32)
+    cand = r2.integers(0, 1 << 30, size=(E, A, 6)).astype(np.int32)
+    goals = goals.copy()
+    goals[:, ::3] = starts[:, ::3]
+    ext = profile(W, H)
+    g = torch.from_numpy(grids.astype(np.int32)).cuda()
+    sim = ext.GridWorldSimulator(g, A, 2, E * W * H, 5, "lifelong", 4096)
+    sim.load_state(torch.from_numpy(starts).cuda(), torch.from_numpy(goals).cuda(),
+                   torch.zeros((E, A), dtype=torch.uint8, device="cuda"), torch.zeros(E, dtype=torch.int32, device="cuda"))
+    sim.set_goal_candidates(torch.from_numpy(cand).cuda(), torch.from_numpy(cells).cuda(),
+                            torch.from_numpy(counts).cuda())
+    osim = oracle.OracleSim(grids, A, task_mode=0, max_episode_steps=4096)
+    osim.load_state(starts, goals)
+    osim.set_goal_candidates(cand, cells, counts)
+    builder = ext.MapfGPTObservationBuilder(g, A)
+    ob = oracle.OracleMapfGPT(grids, A)
+    acts_rng = np.random.default_rng(A + seed)
+    changed = 0
+    for t in range(6):
+        builder.build_tokens_from_state(sim.cur_x, sim.cur_y, sim.goal_x, sim.goal_y)
+        ob.build_state(osim.cur_x.view(np.int16), osim.cur_y.view(np.int16), osim.goal_x.view(np.int16),
+                       osim.goal_y.view(np.int16))
+        acts = acts_rng.integers(0, 5, size=(E, A)).astype(np.uint8)
+        if t == 0:
+            acts[:] = 0
+        a = torch.from_numpy(acts).cuda()
+        builder.append_actions(a)
+        ob.append(acts)
+        sim.update_actions(a)
+        sim.step_sim_only()
+        osim.step(acts)
+        torch.cuda.synchronize()
+        tt = f"{tag} step {t}"
+        assert np.array_equal(builder.tokens.cpu().numpy(), ob.tokens), tt
+        assert builder.diagnostics.cpu().tolist() == ob.diagnostics.tolist(), tt
+        assert np.array_equal(torch.stack((sim.cur_x, sim.cur_y), -1).cpu().numpy(), osim.positions()), tt
+        assert np.array_equal(sim.goal_x.cpu().numpy(), osim.goal_x.astype(np.int16)), tt
+        assert np.array_equal(sim.goal_y.cpu().numpy(), osim.goal_y.astype(np.int16)), tt
+        assert np.array_equal(sim.goal_cursors.cpu().numpy(), osim.goal_cursors), tt
+        changed += int(osim.goal_changed.sum())
+    assert np.array_equal(builder.cost_to_go.cpu().numpy().view(np.uint16), ob.cost_to_go), tag
+    assert changed >= E * len(range(0, A, 3))
