@@ -8,7 +8,8 @@ rows, occupancy, cost_to_go, energy fields, node features and edges.  The
 configurations cover every build path (single launch, two launches with
 one to four row words per lane, the workgroup BFS) without naming them.
 A second set runs candidate-list lifelong goals, so that builds refresh the
-fields of goals changed mid-rollout on those shapes."""
+fields of goals changed mid-rollout on those shapes, and a third the
+CostTracer loop."""
 import numpy as np
 import pytest
 
@@ -153,3 +154,91 @@ def test_random_lifelong_configuration_matches_oracle(oracle, seed):
         changed += int(osim.goal_changed.sum())
     assert np.array_equal(builder.cost_to_go.cpu().numpy().view(np.uint16), ob.cost_to_go), tag
     assert changed >= E * len(range(0, A, 3))
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_random_costtracer_configuration_matches_oracle(seed):
+    """The CostTracer loop (update_actions, CostTracer step, reward and goal
+    stream, distance refresh, observation, horizon reset from a bank of three
+    episodes) on seeded random shapes, against oracle/costtracer.py:
+    observations (float32, bit for bit), rewards, hits, best distances,
+    cursors, positions and step counts."""
+    from iclr_2027_jointoom_amd import profile
+    from iclr_2027_jointoom_amd.synthetic import make_batch
+    from oracle.costtracer import OracleCostTracer
+
+    r0 = np.random.default_rng(9000 + seed)
+    H = 32 * int(r0.integers(1, 9))
+    W = int(r0.integers(8, 257))
+    density = float(r0.uniform(0.0, 0.3))
+    A = int(r0.integers(1, max(2, min(600, int(W * H * 0.15)))))
+    E = int(r0.integers(1, 4))
+    horizon = int(r0.integers(3, 7))
+    tag = f"seed {seed}: costtracer {W}x{H} A{A} E{E} density {density:.2f} horizon {horizon}"
+    print(tag, flush=True)
+    grids, s0, g0 = make_batch(seed, E, W, H, A, density=density)
+    rng = np.random.default_rng(seed)
+    pos, goal = [s0], [g0]
+    for _ in range(2):  # other episodes: the same cells, agents permuted
+        pos.append(np.stack([s0[e][rng.permutation(A)] for e in range(E)]))
+        goal.append(np.stack([g0[e][rng.permutation(A)] for e in range(E)]))
+    bank_pos, bank_goal = np.stack(pos).astype(np.int16), np.stack(goal).astype(np.int16)
+    streams = np.stack([np.stack([np.roll(bank_goal[ep], k + 1, axis=1) for k in range(horizon + 3)], axis=2)
+                        for ep in range(3)]).astype(np.int16)  # [bank, E, A, K, 2]
+    ext = profile(W, H)
+    dev = "cuda"
+    g = torch.from_numpy(grids.astype(np.int32)).to(dev)
+    sim = ext.GridWorldSimulator(g, A, 0, E * W * H, 3, "costtracer", horizon)
+    builder = ext.MapfGPTObservationBuilder(g, A)
+    bp, bg = torch.from_numpy(bank_pos).to(dev), torch.from_numpy(bank_goal).to(dev)
+    sbank = torch.from_numpy(streams).to(dev)
+    episodes = torch.zeros(E, dtype=torch.int32, device=dev)
+    env_ids = torch.arange(E, device=dev)
+    stream = sbank[0].contiguous()
+    cursor = torch.zeros((E, A), dtype=torch.int32, device=dev)
+    best = torch.full_like(cursor, -1)
+    reward = torch.empty((E, A), device=dev)
+    reached = torch.empty_like(reward)
+    obs = torch.empty((E, A, 2, 11, 11), device=dev)
+    sim.load_state(bp[0], bg[0], torch.zeros((E, A), dtype=torch.uint8, device=dev),
+                   torch.zeros(E, dtype=torch.int32, device=dev))
+    ct = OracleCostTracer(grids, A, horizon)
+    ct.sim.load_state(bank_pos[0], bank_goal[0])
+    o_episodes = np.zeros(E, np.int64)
+    o_stream = streams[0]
+
+    def observe():
+        builder.refresh_distances(sim.cur_x, sim.cur_y, sim.goal_x, sim.goal_y)
+        ext.costtracer_observe(sim, builder, best, obs)
+        ct.refresh_distances()
+        return ct.observe()
+
+    def compare(t, want):
+        torch.cuda.synchronize()
+        got = obs.cpu().numpy()
+        assert np.array_equal(got, want), f"{tag} {t} obs differs at {np.argwhere(got != want)[:4].tolist()}"
+        assert np.array_equal(best.cpu().numpy(), ct.best), f"{tag} {t}"
+        assert np.array_equal(cursor.cpu().numpy(), ct.cursor), f"{tag} {t}"
+        assert np.array_equal(torch.stack((sim.cur_x, sim.cur_y), -1).cpu().numpy(), ct.sim.positions()), f"{tag} {t}"
+        assert np.array_equal(sim.step_counts.cpu().numpy(), ct.sim.step_counts), f"{tag} {t}"
+        assert not any(builder.diagnostics.cpu().tolist()), f"{tag} {t}"
+
+    compare("init", observe())
+    for t in range(2 * horizon + 1):
+        acts = rng.integers(0, 5, size=(E, A)).astype(np.uint8)
+        sim.update_actions(torch.from_numpy(acts).to(dev))
+        sim.step_sim_only()
+        ext.costtracer_reward_goals(sim, builder, best, stream, cursor, reward, reached)
+        ct.step(acts, o_stream)
+        torch.cuda.synchronize()
+        assert np.array_equal(reward.cpu().numpy(), ct.rewards), f"{tag} {t}"
+        assert np.array_equal(reached.cpu().numpy(), ct.reached), f"{tag} {t}"
+        compare(t, observe())
+        if int(sim.step_counts.max()) >= horizon:
+            ext.costtracer_reset(sim, bp, bg, episodes, cursor, best, episodes, horizon)
+            stream = sbank[episodes.long() % 3, env_ids].contiguous()
+            ct.reset_due(bank_pos, bank_goal, o_episodes, horizon)
+            o_stream = streams[o_episodes % 3, np.arange(E)]
+            assert episodes.cpu().tolist() == o_episodes.tolist()
+            compare(f"reset {t}", observe())
+    assert int(o_episodes.sum()) >= E  # every env passed through a reset
