@@ -8,8 +8,8 @@ rows, occupancy, cost_to_go, energy fields, node features and edges.  The
 configurations cover every build path (single launch, two launches with
 one to four row words per lane, the workgroup BFS) without naming them.
 A second set runs candidate-list lifelong goals, so that builds refresh the
-fields of goals changed mid-rollout on those shapes, and a third the
-CostTracer loop."""
+fields of goals changed mid-rollout on those shapes, a third the CostTracer
+loop and a fourth the MAGAT stateful step with lifelong goals."""
 import numpy as np
 import pytest
 
@@ -242,3 +242,68 @@ def test_random_costtracer_configuration_matches_oracle(seed):
             assert episodes.cpu().tolist() == o_episodes.tolist()
             compare(f"reset {t}", observe())
     assert int(o_episodes.sum()) >= E  # every env passed through a reset
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_random_stateful_magat_lifelong_matches_oracle(oracle, seed):
+    """The MAGAT stateful step on seeded random shapes with candidate-list
+    lifelong goals: every step (step_and_build_pyg, or step_sim_only ->
+    update_derived_state -> build_magat_plus_nodes ->
+    finalize_magat_plus_graph) refreshes the energy fields of the goals the
+    step changed, incrementally; energy fields, occupancy, node features,
+    positions and edge counts, prefix and total equal a full recompute by the
+    oracle after every step."""
+    from iclr_2027_jointoom_amd import profile
+    from iclr_2027_jointoom_amd.synthetic import make_batch
+    from test_gpu_magat import _compare, _oracle_stateless
+
+    r0 = np.random.default_rng(11000 + seed)
+    H = 32 * int(r0.integers(1, 9))
+    W = int(r0.integers(8, 257))
+    density = float(r0.uniform(0.0, 0.3))
+    A = int(r0.integers(1, max(2, min(1100, int(W * H * 0.15)))))
+    E = int(r0.integers(1, 4))
+    tag = f"seed {seed}: stateful MAGAT lifelong {W}x{H} A{A} E{E} density {density:.2f}"
+    print(tag, flush=True)
+    grids, starts, goals = make_batch(seed, E, W, H, A, density=density)
+    r2 = np.random.default_rng(seed + 100)
+    cells_l = [np.argwhere(gr == 0).astype(np.int16) for gr in grids]
+    cells = np.full((E, max(len(c) for c in cells_l) + 3, 2), -1, np.int16)
+    for e, c in enumerate(cells_l):
+        cells[e, :len(c)] = r2.permutation(c)
+    counts = np.array([len(c) for c in cells_l], np.int32)
+    cand = r2.integers(0, 1 << 30, size=(E, A, 6)).astype(np.int32)
+    goals = goals.copy()
+    goals[:, ::3] = starts[:, ::3]
+    ext = profile(W, H)
+    g = torch.from_numpy(grids.astype(np.int32)).cuda()
+    sim = ext.GridWorldSimulator(g, A, 2, E * W * H, 5, "lifelong", 4096)
+    sim.load_state(torch.from_numpy(starts).cuda(), torch.from_numpy(goals).cuda(),
+                   torch.zeros((E, A), dtype=torch.uint8, device="cuda"), torch.zeros(E, dtype=torch.int32, device="cuda"))
+    sim.set_goal_candidates(torch.from_numpy(cand).cuda(), torch.from_numpy(cells).cuda(),
+                            torch.from_numpy(counts).cuda())
+    osim = oracle.OracleSim(grids, A, task_mode=0, max_episode_steps=4096)
+    osim.load_state(starts, goals)
+    osim.set_goal_candidates(cand, cells, counts)
+    rng = np.random.default_rng(seed)
+    changed = 0
+    for t in range(5):
+        acts = rng.integers(0, 5, size=(E, A)).astype(np.uint8)
+        if t == 0:
+            acts[:] = 0
+        sim.update_actions(torch.from_numpy(acts).cuda())
+        if t % 2:
+            sim.step()
+        else:
+            sim.step_sim_only()
+            sim.update_derived_state()
+            sim.build_magat_plus_nodes()
+            sim.finalize_magat_plus_graph()
+        osim.step(acts)
+        rows = osim.state_packed.copy()
+        rows_reset = rows.copy()
+        rows_reset[:, 7] = 1
+        _compare(sim, _oracle_stateless(oracle, grids, rows_reset.view(np.int16), rows.view(np.int16)),
+                 f"{tag} step {t}")
+        changed += int(osim.goal_changed.sum())
+    assert changed >= E * len(range(0, A, 3))
