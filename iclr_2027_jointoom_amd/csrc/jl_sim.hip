@@ -804,20 +804,25 @@ __global__ void init_agents_kernel(jl_sim_t s, const uint32_t* free_cells, const
     }
 }
 
-// Copy of the caller's actions into the simulator's buffer: 16-byte words
-// when both ends are aligned, bytes otherwise.
-template <bool kVec>
+// Copy of the caller's actions into the simulator's buffer, one thread per
+// 16 bytes: a 16-byte word when both ends are 16-byte aligned, else the same
+// 16 bytes one by one (decided on the device from the pointers, so a copy
+// captured into a graph stays right when its source is pointed at a buffer
+// of another alignment); the last n % 16 bytes go to the first threads (a
+// grid has at least 256).
 __global__ __launch_bounds__(256) void copy_actions_kernel(uint8_t* __restrict__ dst,
-                                                           const uint8_t* __restrict__ src,
-                                                           size_t n) {
+                                                           const uint8_t* __restrict__ src, size_t n) {
     const size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
-    if (kVec) {
-        const size_t words = n / 16;
-        if (i < words) reinterpret_cast<uint4*>(dst)[i] = reinterpret_cast<const uint4*>(src)[i];
-        if (i < n - words * 16) dst[words * 16 + i] = src[words * 16 + i];
-    } else if (i < n) {
-        dst[i] = src[i];
+    const size_t words = n / 16;
+    if (i < words) {
+        if (((reinterpret_cast<uintptr_t>(dst) | reinterpret_cast<uintptr_t>(src)) & 15u) == 0) {
+            reinterpret_cast<uint4*>(dst)[i] = reinterpret_cast<const uint4*>(src)[i];
+        } else {
+#pragma unroll
+            for (int k = 0; k < 16; ++k) dst[i * 16 + k] = src[i * 16 + k];
+        }
     }
+    if (i < n - words * 16) dst[words * 16 + i] = src[words * 16 + i];
 }
 
 // Inclusive int64 prefix sum of the goal_changed values and its last value
@@ -986,16 +991,8 @@ extern "C" int jl_update_actions(const jl_sim_t* s, const uint8_t* actions, jl_s
     if (rc) return rc;
     if (!actions) return JL_ERR_ARG;
     const size_t n = (size_t)s->n_envs * s->n_agents;
-    const bool vec = ((reinterpret_cast<uintptr_t>(actions) | reinterpret_cast<uintptr_t>(s->actions)) & 15u) == 0;
-    const size_t threads = vec ? (n + 15) / 16 : n;
-    const dim3 grid((unsigned)((threads + 255) / 256));
-    if (vec) {
-        hipLaunchKernelGGL(copy_actions_kernel<true>, grid, dim3(256), 0, (hipStream_t)stream,
-                           s->actions, actions, n);
-    } else {
-        hipLaunchKernelGGL(copy_actions_kernel<false>, grid, dim3(256), 0, (hipStream_t)stream,
-                           s->actions, actions, n);
-    }
+    const dim3 grid((unsigned)(((n + 15) / 16 + 255) / 256));
+    hipLaunchKernelGGL(copy_actions_kernel, grid, dim3(256), 0, (hipStream_t)stream, s->actions, actions, n);
     return launch_status();
 }
 
@@ -1014,8 +1011,7 @@ extern "C" int jl_graph_retarget_actions(void* graph, void* graph_exec, const vo
         if (rc) return rc;
     }
     const void* append = append_actions_kernel_address();
-    const void* copy_vec = reinterpret_cast<const void*>(&copy_actions_kernel<true>);
-    const void* copy_byte = reinterpret_cast<const void*>(&copy_actions_kernel<false>);
+    const void* copy = reinterpret_cast<const void*>(&copy_actions_kernel);
     struct Hit {
         hipGraphNode_t node;
         hipKernelNodeParams params;
@@ -1030,13 +1026,10 @@ extern "C" int jl_graph_retarget_actions(void* graph, void* graph_exec, const vo
         hipKernelNodeParams p;
         rc = status(hipGraphKernelNodeGetParams(node, &p));
         if (rc) return rc;
-        const int nargs = p.func == append ? 2 : ((p.func == copy_vec || p.func == copy_byte) ? 3 : 0);
+        const int nargs = p.func == append ? 2 : (p.func == copy ? 3 : 0);
         if (!nargs) continue;
         if (!p.kernelParams || !p.kernelParams[1]) return JL_ERR_ARG;
         if (*static_cast<const void* const*>(p.kernelParams[1]) != captured) continue;
-        // the 16-byte copy stays the captured kernel: the new source must
-        // allow it
-        if (p.func == copy_vec && (reinterpret_cast<uintptr_t>(actions) & 15u)) return JL_ERR_ARG;
         hits.push_back({node, p, nargs});
     }
     for (Hit& h : hits) {

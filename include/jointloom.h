@@ -135,9 +135,9 @@ int jl_update_actions(const jl_sim_t* sim, const uint8_t* actions, jl_stream_t s
  * action buffer, without device work: every node of `graph` that is a
  * history append (jl_mapfgpt_append_actions) or an action copy
  * (jl_update_actions) reading `captured` reads `actions` in `graph_exec`
- * from its next launch on; *n_nodes (may be null) receives how many.  The
- * captured copy kernel stays: a 16-byte-word copy needs `actions` 16-byte
- * aligned (JL_ERR_ARG otherwise, and then no node is changed).  No
+ * from its next launch on; *n_nodes (may be null) receives how many.
+ * `actions` may have any alignment (the copy picks 16-byte words or bytes on
+ * the device).  Every node is checked before any is changed.  No
  * counterpart in the reference, which launches every step from the host:
  * it serves graph replays of the resident loops (graphs.py), so that each
  * replay reads that step's actions where they lie instead of copying them

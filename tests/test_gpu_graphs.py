@@ -41,8 +41,10 @@ def test_mapf_gpt_resident_graph_matches_eager():
     eager(sim_e, b_e, first)
     eager(sim_g, b_g, first)
     graph = MapfGPTResidentGraph(sim_g, b_g)
-    # pre-staged actions, one slice per replay (offsets into one allocation)
+    # pre-staged actions, one slice per replay (offsets into one allocation),
+    # and an unaligned copy of one of them
     staged = torch.from_numpy(rng.integers(0, 5, (8, E, A), dtype=np.uint8)).cuda()
+    odd = torch.empty(E * A + 3, dtype=torch.uint8, device="cuda")[3:].view(E, A)
     for it in range(8):
         if it == 3:
             # a changed goal: the captured build refreshes that field on the device
@@ -55,6 +57,9 @@ def test_mapf_gpt_resident_graph_matches_eager():
             # the graph's own buffer again, after replays read other tensors
             graph.actions.copy_(acts)
             graph.replay()
+        elif it == 6:
+            odd.copy_(acts)
+            graph.replay(odd)
         else:
             graph.replay(acts)
         torch.cuda.synchronize()
@@ -103,7 +108,8 @@ def test_magat_stateful_graph_matches_eager():
 
 def test_graph_replay_rejects_mismatched_actions_before_launching():
     """replay(actions) checks the tensor before any node is retargeted or the
-    graph launched: the step counter and the simulator state stay put."""
+    graph launched: the step counter and the simulator state stay put.  A
+    valid tensor of any alignment then replays."""
     from iclr_2027_jointoom_amd.graphs import MapfGPTResidentGraph
 
     E, W, A = 2, 32, 16
@@ -129,11 +135,14 @@ def test_graph_replay_rejects_mismatched_actions_before_launching():
     torch.cuda.synchronize()
     assert sim.current_step == step
     assert torch.equal(sim.cur_x, x)
-    # a 16-byte-word copy was captured: a source off 16-byte alignment is
-    # refused by the library, and no node is changed
-    flat = torch.zeros(E * A + 1, dtype=torch.uint8, device="cuda")
-    with pytest.raises(RuntimeError, match="retarget"):
-        graph.replay(flat[1:].view(E, A))
-    graph.replay(acts)
+    # a source off 16-byte alignment (the capture read an aligned one): the
+    # captured copy moves it byte by byte
+    flat = torch.randint(0, 5, (E * A + 1,), dtype=torch.uint8, device="cuda")
+    graph.replay(flat[1:].view(E, A))
     torch.cuda.synchronize()
     assert sim.current_step == step + 1
+    assert torch.equal(sim.actions, flat[1:].view(E, A))
+    graph.replay(acts)
+    torch.cuda.synchronize()
+    assert sim.current_step == step + 2
+    assert torch.equal(sim.actions, acts)
