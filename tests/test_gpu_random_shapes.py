@@ -9,7 +9,8 @@ configurations cover every build path (single launch, two launches with
 one to four row words per lane, the workgroup BFS) without naming them.
 A second set runs candidate-list lifelong goals, so that builds refresh the
 fields of goals changed mid-rollout on those shapes, a third the CostTracer
-loop and a fourth the MAGAT stateful step with lifelong goals."""
+loop, a fourth the MAGAT stateful step with lifelong goals, and a fifth both
+captured loops (HIP graphs) against eager twins."""
 import numpy as np
 import pytest
 
@@ -307,3 +308,98 @@ def test_random_stateful_magat_lifelong_matches_oracle(oracle, seed):
                  f"{tag} step {t}")
         changed += int(osim.goal_changed.sum())
     assert changed >= E * len(range(0, A, 3))
+
+
+def _lifelong_pair(ext, g, grids, starts, goals, seed, E, A):
+    """Two identical lifelong simulators (candidate-list goals, a third of
+    the agents on their goals), for an eager run beside a graph's."""
+    r2 = np.random.default_rng(seed + 100)
+    cells_l = [np.argwhere(gr == 0).astype(np.int16) for gr in grids]
+    cells = np.full((E, max(len(c) for c in cells_l) + 3, 2), -1, np.int16)
+    for e, c in enumerate(cells_l):
+        cells[e, :len(c)] = r2.permutation(c)
+    counts = np.array([len(c) for c in cells_l], np.int32)
+    cand = r2.integers(0, 1 << 30, size=(E, A, 6)).astype(np.int32)
+    goals = goals.copy()
+    goals[:, ::3] = starts[:, ::3]
+    W, H = grids.shape[1:]
+    sims = []
+    for _ in range(2):
+        sim = ext.GridWorldSimulator(g, A, 2, E * W * H, 5, "lifelong", 1 << 20)
+        sim.load_state(torch.from_numpy(starts).cuda(), torch.from_numpy(goals).cuda(),
+                       torch.zeros((E, A), dtype=torch.uint8, device="cuda"),
+                       torch.zeros(E, dtype=torch.int32, device="cuda"))
+        sim.set_goal_candidates(torch.from_numpy(cand).cuda(), torch.from_numpy(cells).cuda(),
+                                torch.from_numpy(counts).cuda())
+        sims.append(sim)
+    return sims
+
+
+@pytest.mark.parametrize("seed", range(4))
+def test_random_graph_replays_match_eager(seed):
+    """Both captured loops on seeded random shapes with lifelong goals (so
+    captured builds and derived-state launches refresh changed goals'
+    fields on the device): MapfGPTResidentGraph replays reading pre-staged
+    action slices (most of them off 16-byte alignment) and
+    MagatStatefulGraph replays, each against an eager twin."""
+    from iclr_2027_jointoom_amd import profile
+    from iclr_2027_jointoom_amd.graphs import MagatStatefulGraph, MapfGPTResidentGraph
+    from iclr_2027_jointoom_amd.synthetic import make_batch
+
+    r0 = np.random.default_rng(13000 + seed)
+    H = 32 * int(r0.integers(1, 9))
+    W = int(r0.integers(8, 257))
+    density = float(r0.uniform(0.0, 0.3))
+    A = int(r0.integers(1, max(2, min(1100, int(W * H * 0.15)))))
+    E = int(r0.integers(1, 4))
+    tag = f"seed {seed}: graphs {W}x{H} A{A} E{E} density {density:.2f}"
+    print(tag, flush=True)
+    grids, starts, goals = make_batch(seed, E, W, H, A, density=density)
+    ext = profile(W, H)
+    g = torch.from_numpy(grids.astype(np.int32)).cuda()
+    rng = np.random.default_rng(seed)
+
+    se, sg = _lifelong_pair(ext, g, grids, starts, goals, seed, E, A)
+    be, bg = ext.MapfGPTObservationBuilder(g, A), ext.MapfGPTObservationBuilder(g, A)
+
+    def eager(sim, b, acts):
+        b.build_tokens_from_state(sim.cur_x, sim.cur_y, sim.goal_x, sim.goal_y)
+        b.append_actions(acts)
+        sim.update_actions(acts)
+        sim.step_sim_only()
+
+    first = torch.zeros((E, A), dtype=torch.uint8, device="cuda")
+    eager(se, be, first)
+    eager(sg, bg, first)
+    graph = MapfGPTResidentGraph(sg, bg)
+    staged = torch.from_numpy(rng.integers(0, 5, (6, E, A), dtype=np.uint8)).cuda()
+    for it in range(6):
+        eager(se, be, staged[it])
+        graph.replay(staged[it])
+        torch.cuda.synchronize()
+        for name in ("tokens", "histories", "active_mask", "state_packed", "diagnostics", "goal_cache"):
+            assert torch.equal(getattr(be, name), getattr(bg, name)), (tag, it, name)
+        for name in ("cur_x", "cur_y", "goal_x", "goal_y", "step_counts", "state_packed"):
+            assert torch.equal(getattr(se, name), getattr(sg, name)), (tag, it, name)
+    assert torch.equal(be.cost_to_go, bg.cost_to_go), tag
+    del graph
+
+    se, sg = _lifelong_pair(ext, g, grids, starts, goals, seed, E, A)
+    for sim in (se, sg):
+        sim.update_actions(first)
+        sim.step_and_build_pyg()
+    graph = MagatStatefulGraph(sg)
+    for it in range(5):
+        acts = torch.from_numpy(rng.integers(0, 5, (E, A), dtype=np.uint8)).cuda()
+        se.update_actions(acts)
+        se.step_and_build_pyg()
+        graph.replay(acts)
+        torch.cuda.synchronize()
+        me, mg = se.memory_tensors, sg.memory_tensors
+        for name in ("pyg_x", "pyg_pos", "edge_counts", "pyg_edge_prefix", "pyg_num_edges",
+                     "goal_changed_prefix", "goal_changed_count", "changed_state_packed",
+                     "cur_x", "cur_y", "state_packed"):
+            assert torch.equal(me[name], mg[name]), (tag, it, name)
+        assert torch.equal(se.pyg_edge_index, sg.pyg_edge_index), (tag, it)
+        assert torch.equal(se.pyg_edge_attr, sg.pyg_edge_attr), (tag, it)
+        assert torch.equal(se.energy_maps, sg.energy_maps), (tag, it)
