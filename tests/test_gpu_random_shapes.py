@@ -9,8 +9,9 @@ configurations cover every build path (single launch, two launches with
 one to four row words per lane, the workgroup BFS) without naming them.
 A second set runs candidate-list lifelong goals, so that builds refresh the
 fields of goals changed mid-rollout on those shapes, a third the CostTracer
-loop, a fourth the MAGAT stateful step with lifelong goals, and a fifth both
-captured loops (HIP graphs) against eager twins."""
+loop, a fourth the MAGAT stateful step with lifelong goals, a fifth both
+captured loops (HIP graphs) against eager twins, and a sixth row stages
+through the expert ring into both builders."""
 import numpy as np
 import pytest
 
@@ -403,3 +404,97 @@ def test_random_graph_replays_match_eager(seed):
         assert torch.equal(se.pyg_edge_index, sg.pyg_edge_index), (tag, it)
         assert torch.equal(se.pyg_edge_attr, sg.pyg_edge_attr), (tag, it)
         assert torch.equal(se.energy_maps, sg.energy_maps), (tag, it)
+
+
+@pytest.mark.parametrize("seed", range(3))
+def test_random_ring_stages_match_oracle(oracle, seed):
+    """Row stages on seeded random shapes through the expert ring (producer
+    threads -> shared ring -> pinned staging -> HBM ring of 2-4 stage
+    slots): 13-column stages into MapfGPTOnlinePipeline's builder (tokens)
+    and 8-column stages into ExtremeMAPFPipeline's MAGAT simulator (node
+    features and edges), against the oracle fed the same rows."""
+    import time
+
+    from iclr_2027_jointoom_amd import profile
+    from iclr_2027_jointoom_amd.ring import ExtremeMAPFPipeline, MapfGPTOnlinePipeline
+    from iclr_2027_jointoom_amd.synthetic import make_batch
+    from test_gpu_ring import _TokenRuntime, _produce
+
+    r0 = np.random.default_rng(15000 + seed)
+    H = 32 * int(r0.integers(1, 9))
+    W = int(r0.integers(8, 257))
+    A = int(r0.integers(1, max(2, min(700, int(W * H * 0.15)))))
+    E = int(r0.integers(1, 5))
+    S = int(r0.integers(2, 6))
+    slots = int(r0.integers(2, 5))
+    tag = f"seed {seed}: ring {W}x{H} A{A} E{E} stages {S} slots {slots}"
+    print(tag, flush=True)
+
+    def stages_for(features, s_seed):
+        grids, starts, goals = make_batch(s_seed, E, W, H, A)
+        rng = np.random.default_rng(s_seed)
+        stages = np.zeros((S, E * A, features), np.uint16)
+        pos = starts.astype(np.int64)
+        for s in range(S):
+            blk = stages[s].reshape(E, A, features)
+            blk[:, :, 0] = np.arange(E)[:, None]
+            blk[:, :, 1] = np.arange(A)[None]
+            blk[:, :, 2:4] = pos
+            blk[:, :, 4:6] = goals
+            blk[:, :, 6] = rng.integers(0, 5, size=(E, A))
+            blk[:, :, 7] = 1 if s == 0 else (rng.random((E, A)) < 0.05)
+            if features == 13:
+                blk[:, :, 8:13] = rng.integers(0, 6, size=(E, A, 5))
+            pos = np.roll(pos, 1, axis=1)  # distinct cells, still on the free component
+        return grids, stages
+
+    grids, stages = stages_for(13, seed)
+    builder = profile(W, H).MapfGPTObservationBuilder(torch.from_numpy(grids.astype(np.int32)).cuda(), A)
+    runtime = _TokenRuntime()
+    pipe = MapfGPTOnlinePipeline(builder, runtime, capacity=slots * E * A, batch_threshold=E * A).initialize()
+    pipe.dma_worker_loop()
+    threads = _produce(pipe.ring_buffer, stages, E, A)
+    deadline = time.monotonic() + 60
+    try:
+        while len(runtime.tokens) < S:
+            if pipe.consume_once() is None:
+                assert time.monotonic() < deadline, (tag, pipe.get_stats())
+                time.sleep(0.0005)
+    finally:
+        pipe.shutdown()
+    for t in threads:
+        t.join(timeout=5)
+    ob = oracle.OracleMapfGPT(grids, A)
+    for s in range(S):
+        ob.build_rows(stages[s])
+        assert np.array_equal(runtime.tokens[s].cpu().numpy(), ob.tokens), (tag, s)
+
+    grids, stages = stages_for(8, seed + 1)
+    sim = profile(W, H).StatelessGridWorldSimulator(torch.from_numpy(grids.astype(np.int32)).cuda(), A, 3)
+    pipe = ExtremeMAPFPipeline(sim, capacity=slots * E * A, batch_threshold=E * A).initialize()
+    pipe.dma_worker_loop()
+    threads = _produce(pipe.ring_buffer, stages, E, A)
+    m = oracle.OracleMagat(grids, A)
+    deadline = time.monotonic() + 60
+    try:
+        for s in range(S):
+            x = None
+            while x is None:
+                x = pipe.train_step()
+                if x is None:
+                    assert time.monotonic() < deadline, (tag, pipe.get_stats())
+                    time.sleep(0.0005)
+            sim.materialize_pyg_inputs()
+            rows = stages[s]
+            reset = rows[rows[:, 7] != 0]
+            m.update_energy(reset, len(reset))
+            m.refresh(rows)
+            m.nodes()
+            m.edges()
+            torch.cuda.synchronize()
+            assert np.array_equal(sim.pyg_x.cpu().numpy(), m.pyg_x), (tag, s)
+            assert np.array_equal(sim.pyg_edge_index.cpu().numpy(), m.valid_edges()[0]), (tag, s)
+    finally:
+        pipe.shutdown()
+    for t in threads:
+        t.join(timeout=5)
