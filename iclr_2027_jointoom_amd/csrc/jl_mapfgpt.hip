@@ -2030,7 +2030,7 @@ int build(const jl_mapfgpt_t* b, const int16_t* rows, const int16_t* cx, const i
     if (rc) return rc;
     const int W = b->map_w;
     const TokLayout L = tok_layout(b->n_agents, W, b->map_h);
-    if (L.total > 160 * 1024) return JL_ERR_PROFILE;
+    if (L.total > 160 * 1024) return JL_ERR_AGENTS;
     if (single_launch(b)) {
         JL_DISPATCH_H(b->map_h, {
             if (b->token_events[0]) {

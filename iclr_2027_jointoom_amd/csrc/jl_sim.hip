@@ -60,11 +60,13 @@ constexpr int kDenseStepCells = 4096;
 
 __host__ __device__ inline bool step_dense(int W, int H) { return W * H <= kDenseStepCells; }
 
-__host__ __device__ inline StepLayout step_layout(int A, int W, int H, bool life) {
+constexpr size_t kStepLdsBytes = 160 * 1024;
+
+// The tables of one step workgroup with s hash slots (maps of more than
+// kDenseStepCells cells).
+__host__ __device__ inline StepLayout step_layout_slots(int A, int W, int H, bool life, int s) {
     StepLayout L;
     const bool dense = step_dense(W, H);
-    int s = 64;
-    while (s < 4 * A) s <<= 1;  // load factor <= 1/2 for the <= 2A distinct cells
     L.slots = dense ? W * H : s;
     size_t o = 0;
     L.keys_off = o;
@@ -98,6 +100,23 @@ __host__ __device__ inline StepLayout step_layout(int A, int W, int H, bool life
     L.life_off = o;
     o = a16(o + (life ? (size_t)life_words(A) * 4 : 0));
     L.total = o;
+    return L;
+}
+
+// Hash slots: the smallest power of two of at least 4A (a load factor of at
+// most 1/2 for the at most 2A distinct cells of a step), or, where those
+// tables would not fit in LDS, the smallest one above 2A (a probe still
+// always finds a free slot); 2,048 agents per env fit the first way on a
+// 256 x 256 map in the standard mode, about 2,330 the second.
+__host__ __device__ inline StepLayout step_layout(int A, int W, int H, bool life) {
+    int s = 64;
+    while (s < 4 * A) s <<= 1;
+    StepLayout L = step_layout_slots(A, W, H, life, s);
+    if (!step_dense(W, H) && L.total > kStepLdsBytes) {
+        s = 64;
+        while (s <= 2 * A) s <<= 1;
+        L = step_layout_slots(A, W, H, life, s);
+    }
     return L;
 }
 
@@ -959,7 +978,7 @@ extern "C" int jl_step(const jl_sim_t* s, jl_stream_t stream) {
     if (rc) return rc;
     const StepLayout L =
         step_layout(s->n_agents, s->map_w, s->map_h, s->task_mode == JL_TASK_LIFELONG);
-    if (L.total > 160 * 1024) return JL_ERR_ARG;
+    if (L.total > kStepLdsBytes) return JL_ERR_AGENTS;
     const int nt = step_threads(s->n_agents);
     const bool dense = step_dense(s->map_w, s->map_h);
     const bool one = step_per(s->n_agents) == 1;
@@ -1123,6 +1142,8 @@ extern "C" const char* jl_error_string(int code) {
         case JL_ERR_ARG: return "invalid argument (null pointer or size out of range)";
         case JL_ERR_PROFILE: return "unsupported map profile (map_h a multiple of 32 up to 256, 1 <= map_w <= 256)";
         case JL_ERR_CAPACITY: return "edge buffer smaller than the worst case";
+        case JL_ERR_AGENTS:
+            return "too many agents per env for this map: the kernel's per-env LDS tables exceed 160 KB";
         default: return code > 0 ? hipGetErrorString((hipError_t)code) : "unknown error";
     }
 }

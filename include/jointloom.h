@@ -44,7 +44,11 @@ enum {
     JL_OK = 0,
     JL_ERR_ARG = -1,         /* null pointer, non-positive size, size overflow */
     JL_ERR_PROFILE = -2,     /* map_h not a multiple of 32 in [32, 256], or map_w outside [1, 256] */
-    JL_ERR_CAPACITY = -3     /* an edge buffer too small for the worst case */
+    JL_ERR_CAPACITY = -3,    /* an edge buffer too small for the worst case */
+    JL_ERR_AGENTS = -4       /* too many agents per env for a kernel's per-env LDS tables on
+                                this map (the step: 2,048 agents per env on a 256x256 map
+                                and about 2,330 with a fuller hash, more on smaller maps;
+                                the token pass and the MAGAT passes allow more) */
 };
 
 /* Task modes (grid_world_cuda.h:44-46 of rebuttal/online-rl/native/src/cuda_backend):

@@ -52,6 +52,7 @@ def test_version_and_error_strings(lib):
     assert b"invalid argument" in lib.jl_error_string(-1)
     assert b"map profile" in lib.jl_error_string(-2)
     assert b"edge buffer" in lib.jl_error_string(-3)
+    assert b"too many agents per env" in lib.jl_error_string(-4)
     assert lib.jl_error_string(0) == b"success"
 
 

@@ -523,3 +523,49 @@ def test_decode_to_uint8_unpacks_rows():
     rows = packed[:, :2].numpy().astype(np.uint32)
     want = (rows[..., None] >> np.arange(d, dtype=np.uint32)) & 1
     assert np.array_equal(out.cpu().numpy(), want.astype(np.uint8))
+
+
+def test_step_beyond_the_full_hash_and_past_the_lds_limit(oracle):
+    """On a 256x256 map the step's LDS tables at a load factor of 1/2 hold
+    2,048 agents per env; 2,300 take the fuller hash (the smallest power of
+    two above 2A slots) and still equal the oracle step for step, and 2,400
+    are refused with the library's agent-count error, as is a token build of
+    4,096 (its per-env tables would pass 160 KB of LDS too)."""
+    from iclr_2027_jointoom_amd import profile
+    from iclr_2027_jointoom_amd.synthetic import make_batch, random_actions
+
+    W = H = 256
+    ext = profile(W, H)
+    A = 2300
+    print(f"[step] {W}x{H} A={A}", flush=True)
+    grids, starts, goals = make_batch(2300, 1, W, H, A, density=0.1)
+    g = torch.from_numpy(grids.astype(np.int32)).cuda()
+    sim = ext.GridWorldSimulator(g, A, 0, W * H, 3, "standard_mapf", 64)
+    sim.load_state(torch.from_numpy(starts).cuda(), torch.from_numpy(goals).cuda(),
+                   torch.zeros((1, A), dtype=torch.uint8, device="cuda"), torch.zeros(1, dtype=torch.int32, device="cuda"))
+    osim = oracle.OracleSim(grids, A, task_mode=1, max_episode_steps=64)
+    osim.load_state(starts, goals)
+    acts = random_actions(np.random.default_rng(3), 3, 1, A)
+    for s in range(3):
+        sim.update_actions(torch.from_numpy(acts[s]).cuda())
+        sim.step_sim_only()
+        osim.step(acts[s])
+        compare_with_oracle(sim, osim, f"A={A} step {s}")
+
+    A = 2400
+    grids, starts, goals = make_batch(2400, 1, W, H, A, density=0.1)
+    g = torch.from_numpy(grids.astype(np.int32)).cuda()
+    sim = ext.GridWorldSimulator(g, A, 0, W * H, 3, "standard_mapf", 64)
+    sim.load_state(torch.from_numpy(starts).cuda(), torch.from_numpy(goals).cuda(),
+                   torch.zeros((1, A), dtype=torch.uint8, device="cuda"), torch.zeros(1, dtype=torch.int32, device="cuda"))
+    sim.update_actions(torch.zeros((1, A), dtype=torch.uint8, device="cuda"))
+    with pytest.raises(RuntimeError, match="too many agents per env"):
+        sim.step_sim_only()
+    A = 4096
+    grids, starts, goals = make_batch(4096, 1, W, H, A, density=0.05)
+    b = ext.MapfGPTObservationBuilder(torch.from_numpy(grids.astype(np.int32)).cuda(), A)
+    st = [torch.from_numpy(np.ascontiguousarray(v)).cuda()
+          for v in (starts[..., 0], starts[..., 1], goals[..., 0], goals[..., 1])]
+    with pytest.raises(RuntimeError, match="too many agents per env"):
+        b.build_tokens_from_state(*st)
+    torch.cuda.synchronize()
