@@ -106,6 +106,30 @@ inline int device_cus() {
 }
 
 // Map-profile dispatch on the column count H (a compile-time divisor).
+// LDS of a gfx950 CU, the most one workgroup can hold: a launch's dynamic
+// LDS plus the kernel's static LDS must fit in it.
+constexpr size_t kLdsBytes = 160 * 1024;
+
+// A kernel's static LDS (its __shared__ variables and what the compiler adds,
+// such as the reduction buffer behind __syncthreads_and), looked up once per
+// kernel; taken as 1 KB if the lookup fails.
+template <auto Kernel>
+inline size_t static_lds() {
+    static const size_t bytes = [] {
+        hipFuncAttributes a;
+        return hipFuncGetAttributes(&a, reinterpret_cast<const void*>(Kernel)) == hipSuccess
+                   ? (size_t)a.sharedSizeBytes
+                   : (size_t)1024;
+    }();
+    return bytes;
+}
+
+// Whether `dynamic` bytes of LDS fit beside the kernel's own.
+template <auto Kernel>
+inline bool lds_fits(size_t dynamic) {
+    return dynamic + static_lds<Kernel>() <= kLdsBytes;
+}
+
 #define JL_DISPATCH_H(h, ...)                                   \
     switch (h) {                                               \
         case 32: { constexpr int H = 32; __VA_ARGS__; break; } \

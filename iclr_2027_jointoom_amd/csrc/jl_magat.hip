@@ -831,9 +831,9 @@ extern "C" int jl_magat_nodes(const jl_magat_t* m, jl_stream_t stream) {
     if (!m->energy || !m->pyg_x || !m->pyg_pos || !m->edge_counts || !m->env_edge_base)
         return JL_ERR_ARG;
     const NodeLayout L = node_layout(m->n_agents, m->map_w, m->map_h);
-    if (L.total > 160 * 1024) return JL_ERR_AGENTS;
     const unsigned parts = (unsigned)((m->n_agents + kNodeEgos - 1) / kNodeEgos);
     JL_DISPATCH_H(m->map_h, {
+        if (!lds_fits<&nodes_kernel<H>>(L.total)) return JL_ERR_AGENTS;
         hipLaunchKernelGGL((nodes_kernel<H>), dim3((unsigned)m->n_envs * parts), dim3(kNodeThreads),
                            L.total, (hipStream_t)stream, *m);
     });
@@ -852,7 +852,13 @@ extern "C" int jl_magat_edges(const jl_magat_t* m, jl_stream_t stream) {
     const size_t slices = (size_t)m->n_envs * eparts;
     const bool summed = slices <= (size_t)kSummedSlices;
     const size_t elds = edge_lds(m->n_agents);
-    if (m->n_agents > kMaskMaxAgents && elds > 160 * 1024) return JL_ERR_AGENTS;
+    if (m->n_agents > kMaskMaxAgents && !(summed ? lds_fits<&edges_kernel<true>>(elds)
+                                                 : lds_fits<&edges_kernel<false>>(elds)))
+        return JL_ERR_AGENTS;
+    if (m->n_agents <= kMaskMaxAgents &&
+        !(summed ? lds_fits<&edges_mask_kernel<true>>(edge_mask_lds(m->n_agents))
+                 : lds_fits<&edges_mask_kernel<false>>(edge_mask_lds(m->n_agents))))
+        return JL_ERR_AGENTS;
     if (!summed) {
         hipLaunchKernelGGL(env_scan_kernel, dim3(1), dim3(1024), 0, (hipStream_t)stream, *m);
         rc = launch_status();

@@ -60,7 +60,10 @@ constexpr int kDenseStepCells = 4096;
 
 __host__ __device__ inline bool step_dense(int W, int H) { return W * H <= kDenseStepCells; }
 
-constexpr size_t kStepLdsBytes = 160 * 1024;
+// Dynamic LDS budget of a step workgroup: the CU's LDS less 1 KB for the
+// kernel's own (256 bytes: the workgroup reduction of __syncthreads_and),
+// which jl_step checks at launch.
+constexpr size_t kStepLdsBytes = 159 * 1024;
 
 // The tables of one step workgroup with s hash slots (maps of more than
 // kDenseStepCells cells).
@@ -107,7 +110,7 @@ __host__ __device__ inline StepLayout step_layout_slots(int A, int W, int H, boo
 // most 1/2 for the at most 2A distinct cells of a step), or, where those
 // tables would not fit in LDS, the smallest one above 2A (a probe still
 // always finds a free slot); 2,048 agents per env fit the first way on a
-// 256 x 256 map in the standard mode, about 2,330 the second.
+// 256 x 256 map in the standard mode, about 2,280 the second.
 __host__ __device__ inline StepLayout step_layout(int A, int W, int H, bool life) {
     int s = 64;
     while (s < 4 * A) s <<= 1;
@@ -982,9 +985,12 @@ extern "C" int jl_step(const jl_sim_t* s, jl_stream_t stream) {
     const int nt = step_threads(s->n_agents);
     const bool dense = step_dense(s->map_w, s->map_h);
     const bool one = step_per(s->n_agents) == 1;
-#define JL_STEP_LAUNCH(MODE, DENSE, PER)                                                        \
-    hipLaunchKernelGGL((step_kernel<H, MODE, DENSE, PER>), dim3(s->n_envs), dim3(nt), L.total, \
-                       (hipStream_t)stream, *s)
+#define JL_STEP_LAUNCH(MODE, DENSE, PER)                                                           \
+    do {                                                                                           \
+        if (!lds_fits<&step_kernel<H, MODE, DENSE, PER>>(L.total)) return JL_ERR_AGENTS;          \
+        hipLaunchKernelGGL((step_kernel<H, MODE, DENSE, PER>), dim3(s->n_envs), dim3(nt), L.total, \
+                           (hipStream_t)stream, *s);                                              \
+    } while (0)
 #define JL_STEP_SHAPES(MODE)                                                            \
     if (dense) {                                                                        \
         if (one) JL_STEP_LAUNCH(MODE, true, 1); else JL_STEP_LAUNCH(MODE, true, 4);     \

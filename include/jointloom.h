@@ -47,7 +47,7 @@ enum {
     JL_ERR_CAPACITY = -3,    /* an edge buffer too small for the worst case */
     JL_ERR_AGENTS = -4       /* too many agents per env for a kernel's per-env LDS tables on
                                 this map (the step: 2,048 agents per env on a 256x256 map
-                                and about 2,330 with a fuller hash, more on smaller maps;
+                                and about 2,280 with a fuller hash, more on smaller maps;
                                 the token pass and the MAGAT passes allow more) */
 };
 

@@ -122,8 +122,13 @@ def test_costtracer_mode_matches_oracle(oracle, W, E, A):
     assert sim.step_counts.cpu().tolist() == [8] * E
 
 
+# (252, 256, 3, 1199): four agents per thread, and step tables with the
+# half-full hash that come within 256 bytes of the 160 KB of LDS (the
+# kernel's own reduction buffer): they now take the fuller hash, where that
+# launch had run past the LDS
 @pytest.mark.parametrize("W,H,E,A,T,extent", [(32, 32, 3, 40, 40, None), (64, 64, 4, 128, 30, (50, 60)),
-                                              (96, 96, 2, 300, 20, (65, 65)), (128, 128, 2, 500, 12, None)])
+                                              (96, 96, 2, 300, 20, (65, 65)), (128, 128, 2, 500, 12, None),
+                                              (252, 256, 3, 1199, 6, None)])
 def test_random_lifelong_rollouts_match_oracle(oracle, W, H, E, A, T, extent):
     """The generator-drawn lifelong path (the default task mode without
     candidate lists; 128_agents_map_step.cu:265-343 and

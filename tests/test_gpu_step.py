@@ -527,7 +527,7 @@ def test_decode_to_uint8_unpacks_rows():
 
 def test_step_beyond_the_full_hash_and_past_the_lds_limit(oracle):
     """On a 256x256 map the step's LDS tables at a load factor of 1/2 hold
-    2,048 agents per env; 2,300 take the fuller hash (the smallest power of
+    2,048 agents per env; 2,250 take the fuller hash (the smallest power of
     two above 2A slots) and still equal the oracle step for step, and 2,400
     are refused with the library's agent-count error, as is a token build of
     4,096 (its per-env tables would pass 160 KB of LDS too)."""
@@ -536,9 +536,9 @@ def test_step_beyond_the_full_hash_and_past_the_lds_limit(oracle):
 
     W = H = 256
     ext = profile(W, H)
-    A = 2300
+    A = 2250
     print(f"[step] {W}x{H} A={A}", flush=True)
-    grids, starts, goals = make_batch(2300, 1, W, H, A, density=0.1)
+    grids, starts, goals = make_batch(2250, 1, W, H, A, density=0.1)
     g = torch.from_numpy(grids.astype(np.int32)).cuda()
     sim = ext.GridWorldSimulator(g, A, 0, W * H, 3, "standard_mapf", 64)
     sim.load_state(torch.from_numpy(starts).cuda(), torch.from_numpy(goals).cuda(),
